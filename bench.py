@@ -1,0 +1,183 @@
+#!/usr/bin/env python3
+"""Benchmark of hako's quantized-matmul hot path on one MI355X.
+
+Headline: the Q4_K x q8 matmul (q8_32 activation quantization fused with the
+GEMV, one launch) at the Qwen2.5-3B ffn_up shape, 11008 x 2048, batch 1.
+A step is one such matmul on a weight matrix already resident in HBM; the
+timed region replays K steps captured in a HIP graph, cycling through enough
+weight copies (>= 512 MB) that every step streams its weights from HBM rather
+than the 256 MB last-level cache.
+
+`value` is whole-job throughput in algorithmic GB/s: each weight byte, the
+fp32 activation and the fp32 output once per step (12,733,440 B), times K,
+over the timed region. Extra shapes (7B Q4_K, the Q6_K GEMVs) are reported
+alongside. The reference's own CPU matmul (oracle/_ref, its AVX2 pthread
+path) is timed on the host cores on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+from hako_amd import synth  # noqa: E402
+
+METRIC = "Q4_K×q8 GEMV GB/s (% HBM peak) + decode tok/s, 3B/7B shapes, batch 1"
+HBM_PEAK_GBPS = 8000.0            # MI355X HBM3E
+ROTATION_BYTES = 512 << 20        # > 256 MB Infinity Cache
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "q4k_gemv_11008x2048_traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algo_bytes(qtype: int, n_out: int, n_in: int) -> int:
+    """Compulsory traffic of one matmul: weights once, fp32 x once, fp32 y once."""
+    return synth.row_nbytes(qtype, n_in) * n_out + 4 * n_in + 4 * n_out
+
+
+def bench_gemv(g, qtype: int, n_out: int, n_in: int, steps: int, warmup: int, seed: int) -> dict:
+    rng = np.random.default_rng(seed)
+    w = synth.weight(rng, qtype, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    copies = max(2, math.ceil(ROTATION_BYTES / w.nbytes))
+    dws = [g.upload(w) for _ in range(copies)]
+    dx, dout = g.upload(x), g.alloc(4 * n_out)
+
+    def capture(n):
+        g.capture_begin()
+        for k in range(n):
+            g.matmul(dout, dx, qtype, dws[k % copies], None, n_out, n_in)
+        return g.capture_end()
+
+    warm, timed = capture(max(warmup, 1)), capture(steps)
+    e0, e1 = g.event(), g.event()
+    g.graph_launch(warm)
+    g.sync()
+    g.record(e0)
+    g.graph_launch(timed)
+    g.record(e1)
+    ms = g.elapsed_ms(e0, e1)
+    # single-launch latency: one matmul between two events, median of 51
+    single = []
+    for k in range(51):
+        g.record(e0)
+        g.matmul(dout, dx, qtype, dws[k % copies], None, n_out, n_in)
+        g.record(e1)
+        single.append(g.elapsed_ms(e0, e1))
+    g.graph_destroy(warm)
+    g.graph_destroy(timed)
+    for b in dws + [dx, dout]:
+        b.free()
+    nbytes = algo_bytes(qtype, n_out, n_in)
+    per_launch_s = ms * 1e-3 / steps
+    return {"n_out": n_out, "n_in": n_in, "qtype": qtype, "weight_copies": copies,
+            "algo_bytes": nbytes, "ms_total": ms, "us_per_launch": per_launch_s * 1e6,
+            "gbps": nbytes / per_launch_s / 1e9,
+            "single_launch_us": float(np.median(single)) * 1e3}
+
+
+def cpu_baseline(seconds: float, seed: int) -> dict:
+    """The reference's matmul (src/nn.c:179-210, compiled unmodified with its
+    Makefile flags) on the headline shape, rotating 8 weight copies."""
+    from oracle.hako_oracle import REF_LIB, RefLib
+    threads = min(os.cpu_count() or 1, 16)        # the reference caps at 16 (src/nn.c:61)
+    ref = RefLib(REF_LIB, threads=threads)
+    rng = np.random.default_rng(seed)
+    n_out, n_in = 11008, 2048
+    ws = [synth.q4k_weight(rng, n_out, n_in) for _ in range(8)]
+    x = synth.activation(rng, n_in)
+    for k in range(3):
+        ref.matmul(synth.TYPE_Q4_K, ws[k], x, n_out, n_in)
+    times, t_end, k = [], time.perf_counter() + seconds, 0
+    while time.perf_counter() < t_end or len(times) < 20:
+        t0 = time.perf_counter()
+        ref.matmul(synth.TYPE_Q4_K, ws[k % 8], x, n_out, n_in)
+        times.append(time.perf_counter() - t0)
+        k += 1
+    med = float(np.median(times))
+    return {"value": algo_bytes(synth.TYPE_Q4_K, n_out, n_in) / med / 1e9, "unit": "GB/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"{len(times)} calls of the reference matmul on Q4_K 11008x2048 (8 rotating weight "
+                      f"copies), {threads} threads (HAKM_THREADS), median {med * 1e3:.3f} ms/call"}
+
+
+def read_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return float(t["fetch_bytes_per_launch"]) + float(t["write_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              f"(the hot path is a single-GPU GEMV; see the sharding note in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    from hako_amd.gpu import Gpu
+    g = Gpu(0)
+    info = g.info()
+    log(f"device {info.name.decode()} CUs={info.compute_units} HBM={info.hbm_bytes / 2**30:.0f} GiB")
+
+    head = bench_gemv(g, synth.TYPE_Q4_K, 11008, 2048, args.steps, args.warmup, seed=1)
+    log(f"Q4_K 11008x2048: {head['us_per_launch']:.2f} us/launch, {head['gbps']:.0f} GB/s")
+    extra = {}
+    if not args.no_extra:
+        for name, qt, n_out, n_in, steps in (("q4k_7b_ffn_up_18944x3584", synth.TYPE_Q4_K, 18944, 3584, 1000),
+                                            ("q6k_3b_ffn_down_2048x11008", synth.TYPE_Q6_K, 2048, 11008, 1000),
+                                            ("q6k_3b_vocab_151936x2048", synth.TYPE_Q6_K, 151936, 2048, 200),
+                                            ("q6k_7b_ffn_down_3584x18944", synth.TYPE_Q6_K, 3584, 18944, 500)):
+            r = bench_gemv(g, qt, n_out, n_in, steps, 20, seed=n_out)
+            log(f"{name}: {r['us_per_launch']:.2f} us/launch, {r['gbps']:.0f} GB/s")
+            extra[name] = {"us_per_launch": round(r["us_per_launch"], 3), "gbps": round(r["gbps"], 1),
+                           "hbm_frac": round(r["gbps"] / HBM_PEAK_GBPS, 4),
+                           "single_launch_us": round(r["single_launch_us"], 3)}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds, seed=2)
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s ({cpu['sample']})")
+
+    value = head["gbps"]
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["us_per_launch"] / 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded Q4_K blocks and N(0,1) activations)",
+        "config": {"workload": "Q4_K x q8 matmul (q8_32 quantize + GEMV, one launch), Qwen2.5-3B ffn_up "
+                               "11008x2048, batch 1", "n_out": 11008, "n_in": 2048,
+                   "weight_copies": head["weight_copies"], "algo_bytes_per_step": head["algo_bytes"],
+                   "timing": "HIP graph of K launches between two HIP events on the library stream"},
+        "hbm_frac": round(value / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": read_traffic()},
+        "cpu_baseline": cpu,
+        "single_launch_us": round(head["single_launch_us"], 3),
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+// hako_dev.h — device helpers shared by the gfx950 kernels.
+//
+// Wave64 throughout: reductions use DPP inside 16-lane rows and two
+// cross-row swaps, never 32-lane warp idioms.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hako {
+
+constexpr int kWave = 64;
+constexpr int kQK = 256;          // weights per super-block (reference quant.h:9)
+constexpr int kQ4Bytes = 144;     // block_q4_K (reference quant.h:12-17)
+constexpr int kQ6Bytes = 210;     // block_q6_K (reference quant.h:19-24)
+constexpr float kFltMin = 1.17549435e-38f;
+
+// Exact binary16 -> binary32 (v_cvt_f32_f16; fp16 denormals are kept in the
+// default HIP float mode, so every input converts exactly).
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+	return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// Binary32 subnormal -> 0: the reference runs with FTZ/DAZ (its -ffast-math
+// build links gcc's crtfastmath), so its q8 quantizer never sees or makes a
+// subnormal. Stated explicitly so the result does not depend on the GPU's
+// denormal mode.
+__device__ __forceinline__ float ftz(float v) { return __builtin_fabsf(v) < kFltMin ? 0.0f : v; }
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+	return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+	return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+// DPP controls (gfx9): quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror (lane i <-> 7-i within 8), row_mirror (i <-> 15-i within 16).
+constexpr int kDppQuadSwap1 = 0xB1;
+constexpr int kDppQuadSwap2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+// Sum over all 64 lanes; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+	v += dpp_f<kDppQuadSwap1>(v);
+	v += dpp_f<kDppQuadSwap2>(v);
+	v += dpp_f<kDppHalfMirror>(v);
+	v += dpp_f<kDppMirror>(v);
+	v += __shfl_xor(v, 16);
+	v += __shfl_xor(v, 32);
+	return v;
+}
+
+// Max over aligned groups of 8 lanes; every lane of the group receives it.
+__device__ __forceinline__ float max8(float v) {
+	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap1>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap2>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppHalfMirror>(v));
+	return v;
+}
+
+// v_dot4_i32_i8: c + sum of the four signed byte products of a and b.
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+	return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// Q4_K 6-bit (scale, min) of sub-block j in [0,8) from the 12 scale bytes held
+// as three little-endian dwords s0 = bytes 0-3, s1 = 4-7, s2 = 8-11
+// (layout of reference quant.c:57-66: sub-blocks 0-3 use the low six bits of
+// bytes j and j+4; sub-blocks 4-7 take a nibble of byte j+4 and the top two
+// bits of bytes j-4 and j).
+__device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t &s, uint32_t &m) {
+	const uint32_t sh = 8u * (j & 3u);
+	const uint32_t b0 = (s0 >> sh) & 0xFFu, b1 = (s1 >> sh) & 0xFFu, b2 = (s2 >> sh) & 0xFFu;
+	if (j < 4u) {
+		s = b0 & 63u;
+		m = b1 & 63u;
+	} else {
+		s = (b2 & 0xFu) | ((b0 >> 6) << 4);
+		m = (b2 >> 4) | ((b1 >> 6) << 4);
+	}
+}
+
+// q8_32 quantization of four consecutive floats held by one lane, eight lanes
+// per 32-block (lanes 8k..8k+7 of the wave own block k of the call). Returns
+// the four int8 results packed little-endian and the block scale in `scale`
+// (reference quant.c:127-144 as compiled with -ffast-math:
+// xs = amax*RN(1/127), inv = RN(127/amax) when xs > 0, round-half-even,
+// clamp to +-127).
+__device__ __forceinline__ uint32_t q8_quant4(float4 v, float &scale) {
+	const float a0 = ftz(v.x), a1 = ftz(v.y), a2 = ftz(v.z), a3 = ftz(v.w);
+	float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(a0), __builtin_fabsf(a1)),
+	                             __builtin_fmaxf(__builtin_fabsf(a2), __builtin_fabsf(a3)));
+	amax = max8(amax);
+	const float xs = ftz(amax * 0x1.020408p-7f);      // RN(1/127) = 0x3C010204
+	const float inv = xs > 0.0f ? 127.0f / amax : 0.0f;
+	scale = xs;
+	// A product that is not finite (only from inf/NaN inputs) converts to 0,
+	// as the reference's 64-bit conversion yields the "indefinite" value whose
+	// low 32 bits are 0. Clamping in float keeps the int conversion defined.
+	auto q = [inv](float a) -> uint32_t {
+		float r = __builtin_rintf(a * inv);
+		r = __builtin_isfinite(r) ? r : 0.0f;
+		r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+		return (uint32_t)((int)r & 0xFF);
+	};
+	return q(a0) | (q(a1) << 8) | (q(a2) << 16) | (q(a3) << 24);
+}
+
+}  // namespace hako

@@ -1,0 +1,34 @@
+// hako_rt.h — host-side internals shared by the library's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/hako_gpu.h"
+
+namespace hako {
+
+// Record `msg` (printf-style) as this thread's last error; returns `code`.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clear the thread's last error; returns HAKO_GPU_OK.
+int ok();
+// Map a failed HIP call to HAKO_GPU_EHIP with its text.
+int hip_fail(hipError_t e, const char *what, const char *file, int line);
+
+// The library stream, or nullptr before hako_gpu_init.
+hipStream_t stream();
+// HAKO_GPU_OK when a device is initialised, otherwise an ENODEV error.
+int require_device();
+// Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
+int workspace(int slot, size_t bytes, void **ptr);
+
+}  // namespace hako
+
+#define HK_HIP(call)                                                        \
+	do {                                                                    \
+		hipError_t hk_e_ = (call);                                          \
+		if (hk_e_ != hipSuccess) return hako::hip_fail(hk_e_, #call, __FILE__, __LINE__); \
+	} while (0)
+
+// After a kernel launch: report a launch failure as EHIP.
+#define HK_LAUNCHED(name) HK_HIP(hipGetLastError())

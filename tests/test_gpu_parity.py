@@ -1,0 +1,215 @@
+"""GPU parity: the gfx950 kernels behind the C ABI against the pinned oracle
+and the reference's own golden outputs.
+
+Bars: bit-exact for the q8 quantizer, the dequantizers and the per-sub-block
+int32 sums; max|Δ|/max|ref| <= 1e-5 for fp32 GEMV outputs.
+"""
+import numpy as np
+import pytest
+
+from hako_amd import synth
+from helpers import maxabs_rel
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+Q4, Q6 = synth.TYPE_Q4_K, synth.TYPE_Q6_K
+
+
+def gpu_q8(gpu, x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32)
+    rows = 1 if x.ndim == 1 else x.shape[0]
+    n = x.shape[-1]
+    dx = gpu.upload(x)
+    dq, ds = gpu.alloc(rows * n), gpu.alloc(rows * n // 32 * 4)
+    gpu.quantize_q8_32(dx, rows, n, dq, ds)
+    xq = gpu.download(dq, np.int8, x.shape)
+    xs = gpu.download(ds, np.float32, x.shape[:-1] + (n // 32,))
+    for b in (dx, dq, ds):
+        b.free()
+    return xq, xs
+
+
+def gpu_dequant(gpu, qtype, blocks, nelem):
+    db, do = gpu.upload(blocks), gpu.alloc(nelem * 4)
+    gpu.dequant(qtype, db, do, nelem)
+    y = gpu.download(do, np.float32, (nelem,))
+    db.free(); do.free()
+    return y
+
+
+def gpu_matmul(gpu, qtype, w, x, n_out, n_in, bias=None):
+    dw, dx, do = gpu.upload(w), gpu.upload(x), gpu.alloc(n_out * 4)
+    db = gpu.upload(bias) if bias is not None else None
+    gpu.matmul(do, dx, qtype, dw, db, n_out, n_in)
+    y = gpu.download(do, np.float32, (n_out,))
+    for b in (dw, dx, do, db):
+        if b is not None:
+            b.free()
+    return y
+
+
+# ── q8 activation quantizer ──
+
+def test_q8_golden(gpu, golden):
+    g = golden("q8.npz")
+    xq, xs = gpu_q8(gpu, g["x"])
+    assert np.array_equal(xq, g["xq"])
+    assert np.array_equal(xs.view(np.uint32), g["xs"].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,n", [(1, 2048), (1, 3584), (1, 32), (512, 3584), (7, 18944)])
+def test_q8_random_vs_oracle(gpu, oracle, rows, n):
+    rng = np.random.default_rng(rows * 100003 + n)
+    x = synth.activation(rng, n, rows=rows) * np.float32(rng.uniform(1e-3, 1e3))
+    xq, xs = gpu_q8(gpu, x)
+    for r in range(rows):
+        oq, os_ = oracle.quantize_q8_32(x[r])
+        assert np.array_equal(xq[r], oq), r
+        assert np.array_equal(xs[r].view(np.uint32), os_.view(np.uint32)), r
+
+
+# ── dequantizers ──
+
+@pytest.mark.parametrize("qtype,name", [(Q4, "q4k_dequant.npz"), (Q6, "q6k_dequant.npz")])
+def test_dequant_golden(gpu, golden, qtype, name):
+    g = golden(name)
+    n = g["blocks"].shape[0] * 256
+    y = gpu_dequant(gpu, qtype, g["blocks"], n)
+    assert np.array_equal(y.view(np.uint32), g["out"].view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype,n_blocks", [(Q4, 88064), (Q6, 88064), (Q6, 1)])
+def test_dequant_large_vs_oracle(gpu, oracle, qtype, n_blocks):
+    rng = np.random.default_rng(n_blocks + qtype)
+    b = synth.q4k_blocks(rng, n_blocks) if qtype == Q4 else synth.q6k_blocks(rng, n_blocks, scale_range=(-128, 127))
+    y = gpu_dequant(gpu, qtype, b, n_blocks * 256)
+    assert np.array_equal(y.view(np.uint32), oracle.dequant(qtype, b, n_blocks * 256).view(np.uint32))
+
+
+def test_dequant_f16(gpu):
+    h = np.arange(0, 65536, 1, dtype=np.uint32).astype(np.uint16)
+    y = gpu_dequant(gpu, synth.TYPE_F16, h, h.size)
+    want = h.view(np.float16).astype(np.float32)
+    ok = ~np.isnan(want)
+    assert np.array_equal(y[ok].view(np.uint32), want[ok].view(np.uint32))
+    assert np.all(np.isnan(y[~ok]))
+
+
+# ── Q4_K x q8: integer sums bit-exact ──
+
+def gpu_isums(gpu, w, xq, n_out, n_in):
+    dw, dq = gpu.upload(w), gpu.upload(xq)
+    di, dx = gpu.alloc(n_out * n_in // 32 * 4), gpu.alloc(n_out * n_in // 32 * 4)
+    gpu.q4k_isums(di, dx, dw, dq, n_out, n_in)
+    iqx = gpu.download(di, np.int32, (n_out, n_in // 32))
+    ix = gpu.download(dx, np.int32, (n_out, n_in // 32))
+    for b in (dw, dq, di, dx):
+        b.free()
+    return iqx, ix
+
+
+def test_isums_golden(gpu, golden):
+    g = golden("q4k_isums.npz")
+    for n_in in (2048, 3584):
+        w, xq = g[f"w_{n_in}"], g[f"xq_{n_in}"]
+        iqx, ix = gpu_isums(gpu, w, xq, w.shape[0], n_in)
+        assert np.array_equal(iqx, g[f"iqx_{n_in}"])
+        assert np.array_equal(ix, g[f"ix_{n_in}"])
+
+
+@pytest.mark.parametrize("n_out,n_in", [(11008, 2048), (18944, 3584), (37, 11008), (5, 256), (3, 18944)])
+def test_isums_vs_oracle(gpu, oracle, n_out, n_in):
+    rng = np.random.default_rng(n_out * 7 + n_in)
+    w = synth.q4k_weight(rng, n_out, n_in)
+    xq = rng.integers(-127, 128, n_in).astype(np.int8)
+    iqx, ix = gpu_isums(gpu, w, xq, n_out, n_in)
+    rows = np.unique(np.concatenate([np.arange(min(n_out, 64)), rng.integers(0, n_out, 64)]))
+    oi, ox = oracle.q4k_isums(w[rows], xq, rows.size, n_in)
+    assert np.array_equal(iqx[rows], oi)
+    assert np.array_equal(ix[rows], ox)
+
+
+# ── GEMV fp32 outputs ──
+
+Q4_SHAPES = [(11008, 2048), (2048, 2048), (256, 2048), (18944, 3584), (3584, 3584), (512, 3584),
+             (1, 256), (3, 512), (17, 11008), (5, 18944)]
+
+
+@pytest.mark.parametrize("n_out,n_in", Q4_SHAPES)
+def test_q4k_matmul_fused_vs_oracle(gpu, oracle, n_out, n_in):
+    rng = np.random.default_rng(n_out * 31 + n_in)
+    w = synth.q4k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    bias = 0.1 * synth.activation(rng, n_out)
+    got = gpu_matmul(gpu, Q4, w, x, n_out, n_in, bias)
+    want = oracle.matmul(Q4, w, x, n_out, n_in, bias=bias, f64=True)
+    assert maxabs_rel(got, want) < TOL
+
+
+@pytest.mark.parametrize("n_out,n_in", [(11008, 2048), (18944, 3584), (7, 11008)])
+def test_q4k_gemv_prequantized_vs_oracle(gpu, oracle, n_out, n_in):
+    rng = np.random.default_rng(n_out + n_in)
+    w = synth.q4k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    xq, xs = oracle.quantize_q8_32(x)
+    dw, dq, ds, do = gpu.upload(w), gpu.upload(xq), gpu.upload(xs), gpu.alloc(n_out * 4)
+    gpu.q4k_gemv(do, dw, dq, ds, None, n_out, n_in)
+    got = gpu.download(do, np.float32, (n_out,))
+    for b in (dw, dq, ds, do):
+        b.free()
+    want = np.array([oracle.q4k_vec_dot(w[r], n_in, xq, xs, f64=True) for r in range(n_out)])
+    assert maxabs_rel(got, want) < TOL
+
+
+Q6_SHAPES = [(2048, 11008), (151936, 2048), (3584, 18944), (256, 2048), (1, 256), (9, 768), (33, 11008)]
+
+
+@pytest.mark.parametrize("n_out,n_in", Q6_SHAPES)
+def test_q6k_gemv_vs_oracle(gpu, oracle, n_out, n_in):
+    rng = np.random.default_rng(n_out * 17 + n_in)
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    got = gpu_matmul(gpu, Q6, w, x, n_out, n_in)
+    want = oracle.matmul(Q6, w, x, n_out, n_in, f64=True, threads=16)
+    assert maxabs_rel(got, want) < TOL
+
+
+def test_q6k_full_int8_scales(gpu, oracle):
+    rng = np.random.default_rng(11)
+    w = synth.q6k_blocks(rng, 300 * 8, scale_range=(-128, 127)).reshape(300, -1)
+    x = synth.activation(rng, 2048)
+    got = gpu_matmul(gpu, Q6, w, x, 300, 2048)
+    assert maxabs_rel(got, oracle.matmul(Q6, w, x, 300, 2048)) < TOL
+
+
+@pytest.mark.parametrize("name", ["q4k", "q6k", "q6k_long", "f16", "f32"])
+def test_matmul_vs_reference_golden(gpu, golden, name):
+    g = golden("matmul.npz")
+    qt, n_out, n_in = (int(v) for v in g[f"{name}_shape"])
+    got = gpu_matmul(gpu, qt, g[f"{name}_w"], g[f"{name}_x"], n_out, n_in, g.get(f"{name}_bias"))
+    assert maxabs_rel(got, g[f"{name}_out"]) < TOL
+
+
+def test_matmul_host_uses_mirror(gpu, oracle):
+    rng = np.random.default_rng(21)
+    w = synth.q4k_weight(rng, 600, 2048)
+    x = synth.activation(rng, 2048)
+    gpu.mirror_upload(w)
+    out = np.empty(600, np.float32)
+    gpu.matmul_host(out, x, Q4, w, None, 600, 2048)
+    gpu.mirror_release(w)
+    assert maxabs_rel(out, oracle.matmul(Q4, w, x, 600, 2048)) < TOL
+
+
+def test_bad_shapes_are_rejected(gpu):
+    from hako_amd.gpu import HakoGpuError
+    dw, dx, do = gpu.alloc(4096), gpu.alloc(4096), gpu.alloc(4096)
+    with pytest.raises(HakoGpuError, match="256"):
+        gpu.matmul(do, dx, Q4, dw, None, 4, 100)
+    with pytest.raises(HakoGpuError, match="256"):
+        gpu.matmul(do, dx, Q6, dw, None, 4, 300)
+    with pytest.raises(HakoGpuError, match="type"):
+        gpu.matmul(do, dx, 7, dw, None, 4, 256)
+    for b in (dw, dx, do):
+        b.free()
