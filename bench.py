@@ -47,7 +47,8 @@ def algo_bytes(qtype: int, n_out: int, n_in: int) -> int:
     return synth.row_nbytes(qtype, n_in) * n_out + 4 * n_in + 4 * n_out
 
 
-def bench_gemv(g, qtype: int, n_out: int, n_in: int, steps: int, warmup: int, seed: int) -> dict:
+def bench_gemv(g, qtype: int, n_out: int, n_in: int, steps: int, warmup: int, seed: int,
+               eager: bool = False) -> dict:
     rng = np.random.default_rng(seed)
     w = synth.weight(rng, qtype, n_out, n_in)
     x = synth.activation(rng, n_in)
@@ -55,37 +56,70 @@ def bench_gemv(g, qtype: int, n_out: int, n_in: int, steps: int, warmup: int, se
     dws = [g.upload(w) for _ in range(copies)]
     dx, dout = g.upload(x), g.alloc(4 * n_out)
 
-    def capture(n):
-        g.capture_begin()
-        for k in range(n):
-            g.matmul(dout, dx, qtype, dws[k % copies], None, n_out, n_in)
-        return g.capture_end()
-
-    warm, timed = capture(max(warmup, 1)), capture(steps)
-    e0, e1 = g.event(), g.event()
-    g.graph_launch(warm)
-    g.sync()
-    g.record(e0)
-    g.graph_launch(timed)
-    g.record(e1)
-    ms = g.elapsed_ms(e0, e1)
-    # single-launch latency: one matmul between two events, median of 51
-    single = []
-    for k in range(51):
-        g.record(e0)
+    def launch(k):
         g.matmul(dout, dx, qtype, dws[k % copies], None, n_out, n_in)
-        g.record(e1)
-        single.append(g.elapsed_ms(e0, e1))
-    g.graph_destroy(warm)
-    g.graph_destroy(timed)
+
+    res = _time_launches(g, launch, steps, warmup, eager)
     for b in dws + [dx, dout]:
         b.free()
     nbytes = algo_bytes(qtype, n_out, n_in)
-    per_launch_s = ms * 1e-3 / steps
-    return {"n_out": n_out, "n_in": n_in, "qtype": qtype, "weight_copies": copies,
-            "algo_bytes": nbytes, "ms_total": ms, "us_per_launch": per_launch_s * 1e6,
-            "gbps": nbytes / per_launch_s / 1e9,
-            "single_launch_us": float(np.median(single)) * 1e3}
+    res.update({"n_out": n_out, "n_in": n_in, "qtype": qtype, "weight_copies": copies, "algo_bytes": nbytes,
+                "gbps": nbytes / (res["us_per_launch"] * 1e-6) / 1e9})
+    return res
+
+
+def bench_copy(g, nbytes: int, steps: int, warmup: int, eager: bool) -> dict:
+    """A plain 16-byte-per-lane copy of known size (the byte-counter calibration)."""
+    copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
+    srcs = [g.alloc(nbytes) for _ in range(copies)]
+    dst = g.alloc(nbytes)
+
+    def launch(k):
+        g.check(g.lib.hako_gpu_memcpy_d2d(dst.ptr, srcs[k % copies].ptr, nbytes), "d2d")
+
+    res = _time_launches(g, launch, steps, warmup, eager)
+    for b in srcs + [dst]:
+        b.free()
+    res.update({"algo_bytes": 2 * nbytes, "gbps": 2 * nbytes / (res["us_per_launch"] * 1e-6) / 1e9})
+    return res
+
+
+def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
+    """K launches between two events: replayed from a captured HIP graph, or
+    (eager) issued one by one from Python, as profilers' per-dispatch counter
+    collection needs. Also the median single-launch latency."""
+    e0, e1 = g.event(), g.event()
+    if eager:
+        for k in range(warmup):
+            launch(k)
+        g.sync()
+        g.record(e0)
+        for k in range(steps):
+            launch(k)
+        g.record(e1)
+        ms = g.elapsed_ms(e0, e1)
+    else:
+        def capture(n):
+            g.capture_begin()
+            for k in range(n):
+                launch(k)
+            return g.capture_end()
+        warm, timed = capture(max(warmup, 1)), capture(steps)
+        g.graph_launch(warm)
+        g.sync()
+        g.record(e0)
+        g.graph_launch(timed)
+        g.record(e1)
+        ms = g.elapsed_ms(e0, e1)
+        g.graph_destroy(warm)
+        g.graph_destroy(timed)
+    single = []
+    for k in range(51):
+        g.record(e0)
+        launch(k)
+        g.record(e1)
+        single.append(g.elapsed_ms(e0, e1))
+    return {"ms_total": ms, "us_per_launch": ms * 1e3 / steps, "single_launch_us": float(np.median(single)) * 1e3}
 
 
 def cpu_baseline(seconds: float, seed: int) -> dict:
@@ -122,6 +156,17 @@ def read_traffic():
         return None
 
 
+# name -> (type, n_out, n_in, default steps); the first is the headline.
+WORKLOADS = {
+    "q4k_3b_ffn_up_11008x2048": (synth.TYPE_Q4_K, 11008, 2048, None),
+    "q4k_7b_ffn_up_18944x3584": (synth.TYPE_Q4_K, 18944, 3584, 1000),
+    "q6k_3b_ffn_down_2048x11008": (synth.TYPE_Q6_K, 2048, 11008, 1000),
+    "q6k_3b_vocab_151936x2048": (synth.TYPE_Q6_K, 151936, 2048, 200),
+    "q6k_7b_ffn_down_3584x18944": (synth.TYPE_Q6_K, 3584, 18944, 500),
+}
+HEADLINE = "q4k_3b_ffn_up_11008x2048"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -130,6 +175,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy"],
+                    help="run one workload and print its timing only (profiling runs)")
+    ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -141,14 +189,24 @@ def main():
     info = g.info()
     log(f"device {info.name.decode()} CUs={info.compute_units} HBM={info.hbm_bytes / 2**30:.0f} GiB")
 
-    head = bench_gemv(g, synth.TYPE_Q4_K, 11008, 2048, args.steps, args.warmup, seed=1)
-    log(f"Q4_K 11008x2048: {head['us_per_launch']:.2f} us/launch, {head['gbps']:.0f} GB/s")
+    if args.only:
+        if args.only == "copy":
+            r = bench_copy(g, 64 << 20, args.steps, args.warmup, args.eager)
+        else:
+            qt, n_out, n_in, _ = WORKLOADS[args.only]
+            r = bench_gemv(g, qt, n_out, n_in, args.steps, args.warmup, seed=n_out, eager=args.eager)
+        r["workload"] = args.only
+        print(json.dumps(r), flush=True)
+        return
+
+    qt, n_out, n_in, _ = WORKLOADS[HEADLINE]
+    head = bench_gemv(g, qt, n_out, n_in, args.steps, args.warmup, seed=1)
+    log(f"{HEADLINE}: {head['us_per_launch']:.2f} us/launch, {head['gbps']:.0f} GB/s")
     extra = {}
     if not args.no_extra:
-        for name, qt, n_out, n_in, steps in (("q4k_7b_ffn_up_18944x3584", synth.TYPE_Q4_K, 18944, 3584, 1000),
-                                            ("q6k_3b_ffn_down_2048x11008", synth.TYPE_Q6_K, 2048, 11008, 1000),
-                                            ("q6k_3b_vocab_151936x2048", synth.TYPE_Q6_K, 151936, 2048, 200),
-                                            ("q6k_7b_ffn_down_3584x18944", synth.TYPE_Q6_K, 3584, 18944, 500)):
+        for name, (qt, n_out, n_in, steps) in WORKLOADS.items():
+            if name == HEADLINE:
+                continue
             r = bench_gemv(g, qt, n_out, n_in, steps, 20, seed=n_out)
             log(f"{name}: {r['us_per_launch']:.2f} us/launch, {r['gbps']:.0f} GB/s")
             extra[name] = {"us_per_launch": round(r["us_per_launch"], 3), "gbps": round(r["gbps"], 1),

@@ -4,28 +4,29 @@
 // src/quant.c:150-232). The weight matrix is the verbatim stream of 144-byte
 // super-blocks, n_in/256 per row.
 //
-// Work split. A row is cut into chunks of 16 qs bytes (8 per block, 32
-// weights each): chunk c covers block i = c/8, qs bytes 16*(c%8)..+16, whose
-// low nibbles belong to sub-block 2g (g = (c%8)/2) and high nibbles to
-// sub-block 2g+1. Lane l of a wave takes chunks l, l+64, ... of a row, so a
-// wave-wide load of a row's chunks is one contiguous 1 KiB run, and the
-// activation columns a lane needs never change from row to row. Each lane
-// also loads its block's 16-byte header (d, dmin, 12 scale bytes); the eight
-// lanes of a block hit the same 16 bytes.
+// Lane work. A "chunk" is one 64-weight group of a block: 32 qs bytes whose
+// low nibbles are sub-block 2g and high nibbles sub-block 2g+1 (g < 4), so a
+// lane owns whole sub-blocks: its integer sums are the reference's iqx/ix
+// exactly, and it decodes each (scale, min) pair once for 32 weights. Four
+// lanes cover a block; a row of NB blocks has C = 4*NB chunks. When C <= 64
+// a wave covers RT = 64/C' rows at once (C' = C rounded up to a power of two,
+// lanes past C idle); wider rows take ceil(C/64) wave passes ("parts").
 //
-// A workgroup is 4 waves. KS waves share a row group and split its 64-chunk
-// tiles between them (tile T goes to wave T % KS); each wave keeps R rows in
-// flight, issuing the next tile's loads before it computes the current one.
+// Grid. Persistent: about one workgroup of 8 waves per CU, each owning a
+// contiguous range of rows. A wave walks its items (row tiles, or row parts)
+// with four item loads in flight ahead of the one it computes, so HBM sees
+// the whole matrix requested within the first microsecond on small shapes and
+// a steady stream on large ones.
 //
-// The activation lives in LDS as q8: either quantized there by the workgroup
-// itself from the fp32 x (the fused path: quantize_row_q8_32 once per row, per
-// workgroup, while the first weight loads are in flight), or copied from a
-// pre-quantized xq/xs.
+// Activation. The workgroup's first memory operation loads x (fp32, fused
+// path) or xq/xs (pre-quantized path); the weight loads follow, and the q8_32
+// quantization into LDS (quantize_row_q8_32 once per workgroup) runs while
+// they are in flight. Each lane then keeps its 64 activation bytes, their two
+// scales and partial sums in registers across all the rows it visits.
 //
-// Integer work per chunk: 8 v_dot4_i32_i8 over the nibbles, exact in int32
-// (|sum| <= 15*127*32). The fp32 fold per sub-block is the reference's
-// xs*(d*s*iqx - dmin*m*ix); the lane partial sums are added in a wave tree,
-// so only the fold's association differs from the reference.
+// Arithmetic per chunk: 16 v_dot4_i32_i8 (exact int32: |Σ| <= 15*127*32),
+// then the reference's fold xs*(d*s*iqx - dmin*m*ix) for the two sub-blocks,
+// regrouped as d*(xsA*sA*iqxA + xsB*sB*iqxB) - dmin*(mA*xsA*ixA + mB*xsB*ixB).
 #include "hako_dev.h"
 #include "hako_rt.h"
 
@@ -34,258 +35,344 @@ namespace {
 
 enum Q4Mode { kFused = 0, kPreq = 1, kIsums = 2 };
 
-// The per-lane activation state of one chunk: the 16 xq values of each of its
-// two sub-blocks that pair with its 16 qs bytes, their scales and partial Σxq.
-struct Q4Col {
-	int xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
-	float xsa, xsb;
-	int ixa, ixb;
+constexpr int kQ4Depth = 4;   // item loads in flight per wave
+
+struct Q4Buf {
+	uint4 h, q0, q1;   // block header (d, dmin, scales), 32 qs bytes
 };
 
-__device__ __forceinline__ Q4Col q4_col(const int8_t *xq_s, const float *xs_s, int c) {
-	const int i = c >> 3, p = c & 7, g = p >> 1, half = p & 1;
-	const int base = kQK * i + 64 * g + 16 * half;
-	const int4 a = *(const int4 *)(xq_s + base);
-	const int4 b = *(const int4 *)(xq_s + base + 32);
+// Activation state of one chunk for this lane.
+struct Q4Col {
+	int xa[8], xb[8];   // xq of sub-blocks 2g (paired with low nibbles) and 2g+1
+	float xsa, xsb;     // their q8 scales
+	float ixa, ixb;     // xs * Σxq of each sub-block
+	int ia_sum, ib_sum; // Σxq of each sub-block (integer-sums mode)
+};
+
+__device__ __forceinline__ void q4_col(const int8_t *xq_s, const float *xs_s, int c, Q4Col &col) {
+	const int i = c >> 2, g = c & 3;
+	const int8_t *p = xq_s + kQK * i + 64 * g;
+	const int4 a0 = *(const int4 *)p, a1 = *(const int4 *)(p + 16);
+	const int4 b0 = *(const int4 *)(p + 32), b1 = *(const int4 *)(p + 48);
+	col.xa[0] = a0.x; col.xa[1] = a0.y; col.xa[2] = a0.z; col.xa[3] = a0.w;
+	col.xa[4] = a1.x; col.xa[5] = a1.y; col.xa[6] = a1.z; col.xa[7] = a1.w;
+	col.xb[0] = b0.x; col.xb[1] = b0.y; col.xb[2] = b0.z; col.xb[3] = b0.w;
+	col.xb[4] = b1.x; col.xb[5] = b1.y; col.xb[6] = b1.z; col.xb[7] = b1.w;
 	const float2 s = *(const float2 *)(xs_s + 8 * i + 2 * g);
-	Q4Col col;
-	col.xa0 = a.x; col.xa1 = a.y; col.xa2 = a.z; col.xa3 = a.w;
-	col.xb0 = b.x; col.xb1 = b.y; col.xb2 = b.z; col.xb3 = b.w;
 	col.xsa = s.x;
 	col.xsb = s.y;
-	const int ones = 0x01010101;
-	col.ixa = sdot4(a.w, ones, sdot4(a.z, ones, sdot4(a.y, ones, sdot4(a.x, ones, 0))));
-	col.ixb = sdot4(b.w, ones, sdot4(b.z, ones, sdot4(b.y, ones, sdot4(b.x, ones, 0))));
-	return col;
+	int sa = 0, sb = 0;
+#pragma unroll
+	for (int k = 0; k < 8; k++) {
+		sa = sdot4(col.xa[k], 0x01010101, sa);
+		sb = sdot4(col.xb[k], 0x01010101, sb);
+	}
+	col.ia_sum = sa;
+	col.ib_sum = sb;
+	col.ixa = s.x * (float)sa;
+	col.ixb = s.y * (float)sb;
 }
 
-// Σ q·xq over the chunk's 16 low nibbles (sub-block 2g) and 16 high nibbles
-// (sub-block 2g+1).
-__device__ __forceinline__ void q4_isum(uint4 q, const Q4Col &c, int &ia, int &ib) {
+// Σ q·xq over the 32 low nibbles (sub-block 2g) and 32 high nibbles (2g+1).
+__device__ __forceinline__ void q4_isum(const Q4Buf &b, const Q4Col &c, int &ia, int &ib) {
 	const uint32_t m = 0x0F0F0F0Fu;
-	ia = sdot4((int)(q.x & m), c.xa0, 0);
-	ia = sdot4((int)(q.y & m), c.xa1, ia);
-	ia = sdot4((int)(q.z & m), c.xa2, ia);
-	ia = sdot4((int)(q.w & m), c.xa3, ia);
-	ib = sdot4((int)((q.x >> 4) & m), c.xb0, 0);
-	ib = sdot4((int)((q.y >> 4) & m), c.xb1, ib);
-	ib = sdot4((int)((q.z >> 4) & m), c.xb2, ib);
-	ib = sdot4((int)((q.w >> 4) & m), c.xb3, ib);
+	const uint32_t q[8] = {b.q0.x, b.q0.y, b.q0.z, b.q0.w, b.q1.x, b.q1.y, b.q1.z, b.q1.w};
+	ia = 0;
+	ib = 0;
+#pragma unroll
+	for (int k = 0; k < 8; k++) {
+		ia = sdot4((int)(q[k] & m), c.xa[k], ia);
+		ib = sdot4((int)((q[k] >> 4) & m), c.xb[k], ib);
+	}
 }
 
-// xs·(d·s·iqx − dmin·m·ix) for both sub-blocks of the chunk (reference
-// quant.c:222-225); h is the block header (d, dmin, scales as 4 dwords).
-__device__ __forceinline__ float q4_fold(uint4 h, int g, int ia, int ib, const Q4Col &c) {
-	const float d = f16_to_f32(h.x & 0xFFFFu), dmin = f16_to_f32(h.x >> 16);
-	uint32_t sa, ma, sb, mb;
-	scale_min_k4(2u * g, h.y, h.z, h.w, sa, ma);
-	scale_min_k4(2u * g + 1u, h.y, h.z, h.w, sb, mb);
-	const float ta = d * (float)sa * (float)ia - dmin * (float)ma * (float)c.ixa;
-	const float tb = d * (float)sb * (float)ib - dmin * (float)mb * (float)c.ixb;
-	return c.xsa * ta + c.xsb * tb;
+// d*(xsA*sA*ia + xsB*sB*ib) - dmin*(mA*xsA*ixA + mB*xsB*ixB). `sh` = 16*(g&1)
+// brings scale bytes 2g&3, (2g+1)&3 to the bottom; `hi` = (g >= 2) selects the
+// split 6-bit layout of sub-blocks 4-7 (reference quant.c:57-66).
+// `hmask` is all ones for g >= 2, zero otherwise (a lane constant, blended
+// without branches).
+__device__ __forceinline__ float q4_fold(const Q4Buf &b, uint32_t sh, uint32_t hmask, int ia, int ib,
+                                         const Q4Col &c) {
+	const float d = f16_to_f32(b.h.x & 0xFFFFu), dmin = f16_to_f32(b.h.x >> 16);
+	const uint32_t a0 = b.h.y >> sh, a1 = b.h.z >> sh, a2 = b.h.w >> sh;
+	const uint32_t s_lo = a0 & 0x3F3Fu, m_lo = a1 & 0x3F3Fu;
+	const uint32_t s_hi = (a2 & 0x0F0Fu) | ((a0 >> 2) & 0x3030u);
+	const uint32_t m_hi = ((a2 >> 4) & 0x0F0Fu) | ((a1 >> 2) & 0x3030u);
+	const uint32_t S = s_lo ^ ((s_lo ^ s_hi) & hmask), M = m_lo ^ ((m_lo ^ m_hi) & hmask);
+	const float sA = (float)(S & 0xFFu), sB = (float)((S >> 8) & 0xFFu);
+	const float mA = (float)(M & 0xFFu), mB = (float)((M >> 8) & 0xFFu);
+	const float t1 = (c.xsa * sA) * (float)ia + (c.xsb * sB) * (float)ib;
+	const float t2 = mA * c.ixa + mB * c.ixb;
+	return d * t1 - dmin * t2;
 }
 
-template <int MODE, int R, int KS, bool MULTI>
-__global__ __launch_bounds__(256) void q4k_gemv_kernel(
+__device__ __forceinline__ int next_pow2(int v) {
+	int p = 1;
+	while (p < v) p <<= 1;
+	return p;
+}
+
+// WIDE: rows of more than 64 chunks (n_in > 4096), taken in 64-chunk parts.
+// XP: activation quads per thread (x: 4 floats, xq: 16 bytes each), enough
+// that the whole activation is fetched by straight-line loads.
+template <int MODE, bool WIDE, int XP, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void q4k_gemv_kernel(
     const uint8_t *__restrict__ w, const float *__restrict__ x, const int8_t *__restrict__ xq_g,
     const float *__restrict__ xs_g, const float *__restrict__ bias, float *__restrict__ out,
     int32_t *__restrict__ iqx_o, int32_t *__restrict__ ix_o, int n_out, int n_in) {
 	extern __shared__ __align__(16) uint8_t smem[];
 	int8_t *xq_s = (int8_t *)smem;
 	float *xs_s = (float *)(smem + n_in);
-	float *red_s = xs_s + (n_in >> 5);   // [4 waves][R]
+	float *sum_s = xs_s + (n_in >> 5);   // row sums awaiting their bias
 
+	constexpr int T = WAVES * kWave;
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-	const int wk = wave % KS, wr = wave / KS;
-	const int row0 = (blockIdx.x * (4 / KS) + wr) * R;
-	const int NB = n_in >> 8, C = NB << 3, tiles = (C + 63) >> 6;
+	const int NB = n_in >> 8, C = NB * 4;
+	const int r0 = (int)((int64_t)blockIdx.x * n_out / gridDim.x);
+	const int r1 = (int)((int64_t)(blockIdx.x + 1) * n_out / gridDim.x);
+	const int nrows = r1 - r0;
 	const size_t rb = (size_t)NB * kQ4Bytes;
 
-	auto load = [&](int T, uint4 *q, uint4 *h) {
-		const int c = (T << 6) + lane;
-		const int i = c >> 3, p = c & 7;
-#pragma unroll
-		for (int r = 0; r < R; r++) {
-			const int row = row0 + r;
-			if (c < C && row < n_out) {
-				const uint8_t *blk = w + (size_t)row * rb + (size_t)i * kQ4Bytes;
-				h[r] = *(const uint4 *)blk;
-				q[r] = *(const uint4 *)(blk + 16 + 16 * p);
-			} else {
-				h[r] = make_uint4(0, 0, 0, 0);
-				q[r] = make_uint4(0, 0, 0, 0);
-			}
-		}
+	// lane geometry
+	const int seg = WIDE ? 64 : next_pow2(C);
+	const int rt = 64 / seg;                 // rows per item
+	const int tpr = WIDE ? (C + 63) >> 6 : 1;   // parts per row
+	const int sub = lane & (seg - 1), rsub = lane / seg;
+	int nit;
+	if (WIDE) {
+		nit = nrows > wave ? ((nrows - wave + WAVES - 1) / WAVES) * tpr : 0;
+	} else {
+		const int ntiles = (nrows + rt - 1) / rt;
+		nit = ntiles > wave ? (ntiles - wave + WAVES - 1) / WAVES : 0;
+	}
+	auto item_row = [&](int it) -> int {
+		return WIDE ? r0 + wave + WAVES * (it / tpr) : r0 + rt * (wave + WAVES * it) + rsub;
+	};
+	auto item_chunk = [&](int it) -> int { return WIDE ? 64 * (it % tpr) + lane : sub; };
+
+	// Weight loads are raw buffer loads, never predicated: pipeline slots with
+	// no work (past the last item or row, idle lanes) use an offset past the
+	// stream, which the hardware answers with zeros and no memory traffic. A
+	// branch around a load would make the compiler wait for every outstanding
+	// load (vmcnt(0)) before the activation prologue.
+	const __amdgpu_buffer_rsrc_t wr = stream_rsrc(w, (uint32_t)(rb * n_out));
+	auto issue = [&](Q4Buf &b, int it) {
+		const int row = item_row(it), c = item_chunk(it);
+		const bool on = it < nit && row < r1 && c < C;
+		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + (size_t)(c >> 2) * kQ4Bytes) : kBufNone;
+		b.h = ld_b128(wr, blk);
+		b.q0 = ld_b128(wr, blk + 16 + 32 * (c & 3));
+		b.q1 = ld_b128(wr, blk + 32 + 32 * (c & 3));
 	};
 
-	// Weight loads for the first tile go out before the activation prologue.
-	uint4 qn[R], hn[R];
-	if (wk < tiles) load(wk, qn, hn);
-
+	// 1. activation loads first (they return first: loads complete in order).
+	// Straight-line and unpredicated (clamped), so that the compiler counts
+	// them exactly and waits only for them before quantizing.
+	float4 xv[XP];
+	int4 qv[XP];
+	float sv[2];
 	if (MODE == kFused) {
-		// 8 lanes per 32-block, 4 floats per lane.
-		for (int e = threadIdx.x * 4; e < n_in; e += 1024) {
-			const float4 v = *(const float4 *)(x + e);
+#pragma unroll
+		for (int k = 0; k < XP; k++)
+			xv[k] = *(const float4 *)(x + min((int)(threadIdx.x + k * T) * 4, n_in - 4));
+	} else {
+#pragma unroll
+		for (int k = 0; k < XP; k++)
+			qv[k] = *(const int4 *)(xq_g + min((int)(threadIdx.x + k * T) * 16, n_in - 16));
+		if (MODE == kPreq) {
+#pragma unroll
+			for (int k = 0; k < 2; k++) sv[k] = xs_g[min((int)(threadIdx.x + k * T), (n_in >> 5) - 1)];
+		}
+	}
+	// Keep the scheduler from moving the weight loads above the activation
+	// loads: completion is in issue order, so x must be first in the queue.
+	__builtin_amdgcn_sched_barrier(0);
+	// 2. weight loads for the first items
+	// Item loads go out in consumption order (the scheduler would otherwise
+	// interleave them, and the first item would wait for all four).
+	Q4Buf buf[kQ4Depth];
+#pragma unroll
+	for (int j = 0; j < kQ4Depth; j++) {
+		issue(buf[j], j);
+		__builtin_amdgcn_sched_barrier(0);
+	}
+
+	__builtin_amdgcn_sched_barrier(0);
+	// 3. activation into LDS while the weights are in flight; quantized
+	// unconditionally (clamped lanes repeat the last quad), stores predicated.
+	if (MODE == kFused) {
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			const int e = (threadIdx.x + k * T) * 4;
 			float sc;
-			const uint32_t packed = q8_quant4(v, sc);
-			*(uint32_t *)(xq_s + e) = packed;
-			if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
+			const uint32_t packed = q8_quant4(xv[k], sc);
+			if (e < n_in) {
+				*(uint32_t *)(xq_s + e) = packed;
+				if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
+			}
 		}
 	} else {
-		for (int e = threadIdx.x * 16; e < n_in; e += 4096)
-			*(int4 *)(xq_s + e) = *(const int4 *)(xq_g + e);
-		for (int e = threadIdx.x; e < (n_in >> 5); e += 256) xs_s[e] = xs_g[e];
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			const int e = (threadIdx.x + k * T) * 16;
+			const int4 v = qv[k];
+			if (e < n_in) *(int4 *)(xq_s + e) = v;
+		}
+#pragma unroll
+		for (int k = 0; k < 2; k++) {
+			const int e = threadIdx.x + k * T;
+			const float v = MODE == kPreq ? sv[k] : 0.0f;
+			if (e < (n_in >> 5)) xs_s[e] = v;
+		}
 	}
 	__syncthreads();
 
-	float acc[R];
-#pragma unroll
-	for (int r = 0; r < R; r++) acc[r] = 0.0f;
+	Q4Col col;
+	if (!WIDE) q4_col(xq_s, xs_s, min(sub, C - 1), col);
+	float acc = 0.0f;
 
-	for (int T = wk; T < tiles; T += KS) {
-		uint4 q[R], h[R];
+	// Whole groups of kQ4Depth items, so every iteration issues the same
+	// number of loads (slots past nit load nothing: out-of-range offsets).
+	// Their arithmetic is skipped by a wave-uniform branch that holds no loads.
+	for (int base = 0; base < nit; base += kQ4Depth) {
+		float rsum[kQ4Depth];
 #pragma unroll
-		for (int r = 0; r < R; r++) {
-			q[r] = qn[r];
-			h[r] = hn[r];
-		}
-		if (MULTI && T + KS < tiles) load(T + KS, qn, hn);
-		const int c = (T << 6) + lane;
-		if (c < C) {
-			const Q4Col col = q4_col(xq_s, xs_s, c);
-			const int g = (c & 7) >> 1;
-#pragma unroll
-			for (int r = 0; r < R; r++) {
-				int ia, ib;
-				q4_isum(q[r], col, ia, ib);
-				if (MODE == kIsums) {
-					// Lanes c and c^1 hold the two halves of each sub-block.
-					const int ia_t = ia + dpp_i<kDppQuadSwap1>(ia);
-					const int ib_t = ib + dpp_i<kDppQuadSwap1>(ib);
-					const int xa_t = col.ixa + dpp_i<kDppQuadSwap1>(col.ixa);
-					const int xb_t = col.ixb + dpp_i<kDppQuadSwap1>(col.ixb);
-					const int row = row0 + r;
-					if ((c & 1) == 0 && row < n_out) {
-						const size_t o = (size_t)row * (n_in >> 5) + 8 * (c >> 3) + 2 * g;
-						iqx_o[o] = ia_t;
-						iqx_o[o + 1] = ib_t;
-						ix_o[o] = xa_t;
-						ix_o[o + 1] = xb_t;
-					}
-				} else {
-					acc[r] += q4_fold(h[r], g, ia, ib, col);
+		for (int j = 0; j < kQ4Depth; j++) {
+			const int it = base + j;
+			const int row = item_row(it), c = item_chunk(it);
+			const bool valid = row < r1 && c < C;
+			float f = 0.0f;
+			int ia = 0, ib = 0;
+			if (it < nit) {
+				if (WIDE) q4_col(xq_s, xs_s, min(c, C - 1), col);
+				// Consume buf[j] in place, then reload it: a copy would have to be
+				// rotated back at the loop edge, waiting on the loads in flight.
+				q4_isum(buf[j], col, ia, ib);
+				if (MODE != kIsums) f = q4_fold(buf[j], 16u * (c & 1), (c & 3) >= 2 ? ~0u : 0u, ia, ib, col);
+			}
+			issue(buf[j], it + kQ4Depth);
+			__builtin_amdgcn_sched_barrier(0);
+			if (MODE == kIsums) {
+				if (it < nit && valid) {
+					const size_t o = (size_t)row * (n_in >> 5) + 2 * c;
+					iqx_o[o] = ia;
+					iqx_o[o + 1] = ib;
+					ix_o[o] = col.ia_sum;
+					ix_o[o + 1] = col.ib_sum;
 				}
+			} else if (WIDE) {
+				// a row spans tpr items: accumulate, reduce at its last part
+				acc += valid ? f : 0.0f;
+				if (it < nit && (it % tpr) == tpr - 1) {
+					const float tot = seg_sum(acc, 64);
+					if (lane == 0 && row < r1) {
+						if (bias)
+							sum_s[row - r0] = tot;
+						else
+							out[row] = tot;
+					}
+					acc = 0.0f;
+				}
+			} else {
+				rsum[j] = valid ? f : 0.0f;
+			}
+		}
+		if (MODE != kIsums && !WIDE) {
+			// lane with sub == j holds item j's row sum
+			const float tot = seg_sum4(rsum, seg, lane);
+			const int j = sub & 3;
+			const int row = item_row(base + j);
+			if (sub < kQ4Depth && base + j < nit && row < r1) {
+				if (bias)
+					sum_s[row - r0] = tot;
+				else
+					out[row] = tot;
 			}
 		}
 	}
-
-	if (MODE != kIsums) {
-		float tot[R];
-#pragma unroll
-		for (int r = 0; r < R; r++) tot[r] = wave_sum(acc[r]);
-		if (KS == 1) {
-			float v = tot[0];
-#pragma unroll
-			for (int r = 1; r < R; r++) v = (lane == r) ? tot[r] : v;
-			const int row = row0 + lane;
-			if (lane < R && row < n_out) out[row] = bias ? v + bias[row] : v;
-		} else {
-			if (lane == 0) {
-#pragma unroll
-				for (int r = 0; r < R; r++) red_s[wave * R + r] = tot[r];
-			}
-			__syncthreads();
-			if (wk == 0 && lane < R) {
-				float v = 0.0f;
-#pragma unroll
-				for (int k = 0; k < KS; k++) v += red_s[(wr * KS + k) * R + lane];
-				const int row = row0 + lane;
-				if (row < n_out) out[row] = bias ? v + bias[row] : v;
-			}
-		}
+	// The bias is added after the weight stream: a bias load in the loop
+	// would wait for every weight load in flight (loads complete in order).
+	if (MODE != kIsums && bias) {
+		__syncthreads();
+		for (int r = threadIdx.x; r < nrows; r += T) out[r0 + r] = sum_s[r] + bias[r0 + r];
 	}
 }
-
-struct Q4Plan {
-	int R, KS, wgs;
-	bool multi;
-	size_t lds;
-};
 
 constexpr int kMaxQ4Lds = 64 * 1024;
-
-int q4_plan(int n_out, int n_in, Q4Plan &p) {
-	if (n_out <= 0 || n_in <= 0 || n_in % kQK != 0)
-		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMV needs n_out > 0 and n_in %% 256 == 0 (got %d x %d)",
-		                 n_out, n_in);
-	const int tiles = (n_in / kQK * 8 + 63) / 64;
-	p.KS = tiles >= 4 ? 4 : (tiles >= 2 ? 2 : 1);
-	p.multi = tiles > p.KS;
-	p.R = 1;
-	for (int R : {4, 2}) {
-		const int rows_per_wg = R * 4 / p.KS;
-		if ((n_out + rows_per_wg - 1) / rows_per_wg >= 512) {
-			p.R = R;
-			break;
-		}
-	}
-	const int rows_per_wg = p.R * 4 / p.KS;
-	p.wgs = (n_out + rows_per_wg - 1) / rows_per_wg;
-	p.lds = (size_t)n_in + (size_t)(n_in / 32) * 4 + 16 * 4 * sizeof(float);
-	if (p.lds > (size_t)kMaxQ4Lds)
-		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMV n_in %d exceeds the LDS-resident limit", n_in);
-	return HAKO_GPU_OK;
-}
-
-template <int MODE, int R, int KS, bool MULTI>
-int q4_launch_rkm(const Q4Plan &p, const uint8_t *w, const float *x, const int8_t *xq,
-                  const float *xs, const float *bias, float *out, int32_t *iqx, int32_t *ix,
-                  int n_out, int n_in) {
-	hipLaunchKernelGGL((q4k_gemv_kernel<MODE, R, KS, MULTI>), dim3(p.wgs), dim3(256), p.lds, stream(),
-	                   w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
-	HK_LAUNCHED("q4k_gemv");
-	return ok();
-}
-
-template <int MODE, int R, int KS>
-int q4_launch_rk(const Q4Plan &p, const uint8_t *w, const float *x, const int8_t *xq, const float *xs,
-                 const float *bias, float *out, int32_t *iqx, int32_t *ix, int n_out, int n_in) {
-	return p.multi ? q4_launch_rkm<MODE, R, KS, true>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in)
-	               : q4_launch_rkm<MODE, R, KS, false>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
-}
-
-template <int MODE, int R>
-int q4_launch_r(const Q4Plan &p, const uint8_t *w, const float *x, const int8_t *xq, const float *xs,
-                const float *bias, float *out, int32_t *iqx, int32_t *ix, int n_out, int n_in) {
-	switch (p.KS) {
-	case 1: return q4_launch_rk<MODE, R, 1>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
-	case 2: return q4_launch_rk<MODE, R, 2>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
-	default: return q4_launch_rk<MODE, R, 4>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
-	}
-}
+int g_q4_wgs_per_cu = 1;
+int g_q4_waves = 4;
 
 template <int MODE>
 int q4_launch(const uint8_t *w, const float *x, const int8_t *xq, const float *xs, const float *bias,
               float *out, int32_t *iqx, int32_t *ix, int n_out, int n_in) {
 	if (int rc = require_device()) return rc;
+	if (n_out <= 0 || n_in <= 0 || n_in % kQK != 0)
+		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMV needs n_out > 0 and n_in %% 256 == 0 (got %d x %d)",
+		                 n_out, n_in);
 	if (((uintptr_t)w & 15) || ((uintptr_t)x & 15) || ((uintptr_t)xq & 15) || ((uintptr_t)xs & 3))
 		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMV needs w, x and xq 16-byte aligned");
-	Q4Plan p;
-	if (int rc = q4_plan(n_out, n_in, p)) return rc;
-	switch (p.R) {
-	case 4: return q4_launch_r<MODE, 4>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
-	case 2: return q4_launch_r<MODE, 2>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
-	default: return q4_launch_r<MODE, 1>(p, w, x, xq, xs, bias, out, iqx, ix, n_out, n_in);
+	// 4-wave workgroups keep more of them in flight; very wide activations
+	// need 8 waves to stage x in straight-line loads.
+	const int waves = (g_q4_waves == 8 || n_in > 16 * 4 * 4 * kWave) ? 8 : 4, threads = waves * kWave;
+	const size_t lds = (size_t)n_in + (size_t)(n_in / 32) * 4 + 2 * threads * sizeof(float);   // + row sums
+	if (lds > (size_t)kMaxQ4Lds || n_in > 16 * 4 * threads)
+		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMV n_in %d exceeds the LDS-resident limit", n_in);
+	if ((size_t)n_out * (n_in / kQK) * kQ4Bytes >= kBufNone)
+		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMV weight of %d x %d exceeds 2 GiB", n_out, n_in);
+	const int C = n_in / kQK * 4;
+	const bool wide = C > 64;
+	int rows_per_item = 1;
+	if (!wide) {
+		int seg = 1;
+		while (seg < C) seg <<= 1;
+		rows_per_item = 64 / seg;
 	}
+	// Persistent-style grid: a fixed number of workgroups per CU, each with a
+	// contiguous row range, never more workgroups than give one item per wave.
+	const int max_wgs = g_q4_wgs_per_cu * cu_count();
+	const int min_rows = waves * rows_per_item;
+	int wgs = (n_out + min_rows - 1) / min_rows;
+	if (wgs > max_wgs) wgs = max_wgs;
+	const int max_rows_per_wg = 2 * threads;   // row sums awaiting a bias, in LDS
+	if ((n_out + wgs - 1) / wgs > max_rows_per_wg) wgs = (n_out + max_rows_per_wg - 1) / max_rows_per_wg;
+	// activation quads per thread: 4 floats (fused) / 16 bytes per thread and round
+	const int per_round = MODE == kFused ? 4 * threads : 16 * threads;
+	const int xp = (n_in + per_round - 1) / per_round;
+#define HK_Q4_LAUNCH(W, XP, WV)                                                                          \
+	hipLaunchKernelGGL((q4k_gemv_kernel<MODE, W, XP, WV>), dim3(wgs), dim3(WV * kWave), lds, stream(), w, x, \
+	                   xq, xs, bias, out, iqx, ix, n_out, n_in)
+#define HK_Q4_LAUNCH_W(WV)                           \
+	do {                                             \
+		if (wide) {                                  \
+			if (xp <= 4) HK_Q4_LAUNCH(true, 4, WV);  \
+			else if (xp <= 8) HK_Q4_LAUNCH(true, 8, WV); \
+			else HK_Q4_LAUNCH(true, 16, WV);         \
+		} else {                                     \
+			if (xp <= 1) HK_Q4_LAUNCH(false, 1, WV); \
+			else if (xp <= 2) HK_Q4_LAUNCH(false, 2, WV); \
+			else HK_Q4_LAUNCH(false, 4, WV);         \
+		}                                            \
+	} while (0)
+	if (waves == 8)
+		HK_Q4_LAUNCH_W(8);
+	else
+		HK_Q4_LAUNCH_W(4);
+#undef HK_Q4_LAUNCH_W
+#undef HK_Q4_LAUNCH
+	HK_LAUNCHED("q4k_gemv");
+	return ok();
 }
 
 }  // namespace
 
 // Fused quantize + GEMV on device pointers (used by hako_gpu_matmul).
 int q4k_matmul_fused(float *out, const float *x, const void *w, const float *bias, int n_out, int n_in) {
-	return q4_launch<kFused>((const uint8_t *)w, x, nullptr, nullptr, bias, out, nullptr, nullptr,
-	                         n_out, n_in);
+	return q4_launch<kFused>((const uint8_t *)w, x, nullptr, nullptr, bias, out, nullptr, nullptr, n_out,
+	                         n_in);
 }
+
+void q4k_set_wgs_per_cu(int v) { g_q4_wgs_per_cu = v < 1 ? 1 : (v > 8 ? 8 : v); }
+void q4k_set_waves(int v) { g_q4_waves = v >= 8 ? 8 : 4; }
 
 }  // namespace hako
 
@@ -297,8 +384,7 @@ extern "C" int hako_gpu_q4k_gemv(float *out, const void *w, const int8_t *xq, co
 
 extern "C" int hako_gpu_q4k_isums(int32_t *iqx, int32_t *ix, const void *w, const int8_t *xq,
                                   int n_out, int n_in) {
-	// The integer path never reads xs; any readable buffer of n_in/32 floats
-	// serves, and xq itself is at least that long.
-	return hako::q4_launch<hako::kIsums>((const uint8_t *)w, nullptr, xq, (const float *)xq, nullptr,
-	                                     nullptr, iqx, ix, n_out, n_in);
+	// The integer path reads no scales.
+	return hako::q4_launch<hako::kIsums>((const uint8_t *)w, nullptr, xq, nullptr, nullptr, nullptr, iqx,
+	                                     ix, n_out, n_in);
 }

@@ -10,33 +10,34 @@
 // is nibble (k>>1) of ql[64n + 32(k&1) + l] with bits 2k..2k+1 of qh[32n + l]
 // on top, minus 32, times d*scales[8n + 2k + l/16].
 //
-// Work split: 8 lanes per block. Lane sub-index s = c%8 takes half n = s/4
-// and l in [l0, l0+8), l0 = 8*(s%4): 8-byte loads of ql at 64n+l0 and
-// 64n+32+l0 and of qh at 32n+l0 give its 32 weights (k = 0..3, 8 each), all
-// in four 16-wide scale groups. Blocks are only 2-byte aligned in the
-// verbatim stream (210 = 2*105), so those loads are unaligned; gfx950 serves
-// them in the HSA unaligned-access mode the compiler assumes for byte copies.
+// Lane work. Chunk c = 8i + s of a row is block i, half n = s/4, l in
+// [l0, l0+8) with l0 = 8*(s%4): 8-byte loads of ql at 64n+l0 and 64n+32+l0
+// and of qh at 32n+l0 give 32 weights (k = 0..3, 8 each), each k inside one
+// 16-wide scale group. Blocks are only 2-byte aligned in the verbatim stream
+// (210 = 2*105), so those loads are unaligned; gfx950 serves them in the HSA
+// unaligned-access mode the compiler itself assumes for byte copies. The
+// 6-bit values are assembled four to a dword (nibbles | qh bits moved to bits
+// 4-5 of each byte), converted per byte (v_cvt_f32_ubyteN) and multiplied into
+// the lane's fp32 activations; per scale group the sum is Σq·x − 32·Σx with
+// −32·Σx precomputed.
 //
-// The 6-bit values are assembled four at a time in a dword (nibbles | qh bits
-// shifted to bits 4-5 of each byte), converted per byte (v_cvt_f32_ubyteN)
-// and multiplied into the lane's fp32 activations; per scale group the sum is
-// Σ q·x − 32·Σx with Σx precomputed once per lane.
-//
-// Workgroups of 4 waves; KS waves split a row group's 64-chunk tiles, R rows
-// per wave, next tile's loads issued before the current tile is computed.
+// Grid. Persistent: about one workgroup per CU, each owning a contiguous row
+// range. A row of C = 8*NB chunks is cut into ceil(C/64) parts; the
+// workgroup has one wave group per part (W = parts x row-slices waves, at
+// most 16), and wave (part p, slice r) visits rows r, r+RW, ... of the range
+// with part p's activations hoisted in registers for all of them. Partial sums
+// of a row meet in LDS. Each wave keeps four row loads in flight ahead of the
+// row it computes.
 #include "hako_dev.h"
 #include "hako_rt.h"
 
 namespace hako {
 namespace {
 
-__device__ __forceinline__ uint2 ld_u2(const uint8_t *p) {
-	uint2 v;
-	__builtin_memcpy(&v, p, 8);
-	return v;
-}
+constexpr int kQ6Depth = 4;
+constexpr int kQ6MaxWaves = 16;
 
-struct Q6W {
+struct Q6Buf {
 	uint2 a, b, h, s;
 	uint32_t d;
 };
@@ -48,7 +49,7 @@ struct Q6Col {
 	float nsx[4];
 };
 
-__device__ __forceinline__ void q6_col(const float *__restrict__ x, int c, Q6Col &col) {
+__device__ __forceinline__ void q6_col_load(const float *__restrict__ x, int c, Q6Col &col) {
 	const int i = c >> 3, s = c & 7, n = s >> 2, l0 = 8 * (s & 3);
 	const float *xb = x + kQK * i + 128 * n + l0;
 #pragma unroll
@@ -57,6 +58,12 @@ __device__ __forceinline__ void q6_col(const float *__restrict__ x, int c, Q6Col
 		const float4 v = *(const float4 *)(xb + 32 * k + 4);
 		col.xv[k][0] = u.x; col.xv[k][1] = u.y; col.xv[k][2] = u.z; col.xv[k][3] = u.w;
 		col.xv[k][4] = v.x; col.xv[k][5] = v.y; col.xv[k][6] = v.z; col.xv[k][7] = v.w;
+	}
+}
+
+__device__ __forceinline__ void q6_col_sums(Q6Col &col) {
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
 		float t = 0.0f;
 #pragma unroll
 		for (int j = 0; j < 8; j++) t += col.xv[k][j];
@@ -67,7 +74,7 @@ __device__ __forceinline__ void q6_col(const float *__restrict__ x, int c, Q6Col
 __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 
 // d · Σ_k sc_k · (Σ_j q_kj·x_kj − 32·Σ_j x_kj) over the lane's 32 weights.
-__device__ __forceinline__ float q6_dot(const Q6W &W, const Q6Col &col, int sel) {
+__device__ __forceinline__ float q6_dot(const Q6Buf &W, const Q6Col &col, int sel) {
 	float acc0 = col.nsx[0], acc1 = col.nsx[1], acc2 = col.nsx[2], acc3 = col.nsx[3];
 	const uint32_t lo = 0x0F0F0F0Fu, hi = 0x30303030u;
 #pragma unroll
@@ -95,112 +102,132 @@ __device__ __forceinline__ float q6_dot(const Q6W &W, const Q6Col &col, int sel)
 	return f16_to_f32(W.d) * part;
 }
 
-template <int R, int KS, bool MULTI>
-__global__ __launch_bounds__(256) void q6k_gemv_kernel(const uint8_t *__restrict__ w,
-                                                       const float *__restrict__ x,
-                                                       const float *__restrict__ bias,
-                                                       float *__restrict__ out, int n_out, int n_in) {
-	__shared__ float red_s[4 * R];
-	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-	const int wk = wave % KS, wr = wave / KS;
-	const int row0 = (blockIdx.x * (4 / KS) + wr) * R;
-	const int NB = n_in >> 8, C = NB << 3, tiles = (C + 63) >> 6;
-	const size_t rb = (size_t)NB * kQ6Bytes;
+struct Q6Geom {
+	int C, seg, rt, tpr, rw, waves;
+};
 
-	auto load = [&](int T, Q6W *W) {
-		const int c = (T << 6) + lane;
-		const int i = c >> 3, s = c & 7, n = s >> 2, l0 = 8 * (s & 3);
-#pragma unroll
-		for (int r = 0; r < R; r++) {
-			const int row = row0 + r;
-			if (c < C && row < n_out) {
-				const uint8_t *blk = w + (size_t)row * rb + (size_t)i * kQ6Bytes;
-				W[r].a = ld_u2(blk + 64 * n + l0);
-				W[r].b = ld_u2(blk + 64 * n + 32 + l0);
-				W[r].h = ld_u2(blk + 128 + 32 * n + l0);
-				W[r].s = ld_u2(blk + 192 + 8 * n);
-				W[r].d = *(const uint16_t *)(blk + 208);
-			} else {
-				W[r].a = W[r].b = W[r].h = W[r].s = make_uint2(0, 0);
-				W[r].d = 0;
-			}
-		}
+// `target` waves per workgroup (4 or 8): row slices = target / parts, >= 1.
+__host__ __device__ inline Q6Geom q6_geom(int n_in, int target) {
+	Q6Geom g;
+	g.C = n_in / kQK * 8;
+	if (g.C <= 64) {
+		g.seg = 1;
+		while (g.seg < g.C) g.seg <<= 1;
+		g.rt = 64 / g.seg;
+		g.tpr = 1;
+		g.rw = target;
+	} else {
+		g.seg = 64;
+		g.rt = 1;
+		g.tpr = (g.C + 63) / 64;
+		g.rw = target / g.tpr > 1 ? target / g.tpr : 1;
+	}
+	g.waves = g.tpr * g.rw;
+	return g;
+}
+
+// One workgroup: waves = parts x row-slices (see q6_geom).
+__global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uint8_t *__restrict__ w,
+                                                                       const float *__restrict__ x,
+                                                                       const float *__restrict__ bias,
+                                                                       float *__restrict__ out, int n_out,
+                                                                       int n_in, int target) {
+	extern __shared__ float red_s[];   // [rows of this workgroup][parts]: partial row sums
+	const Q6Geom G = q6_geom(n_in, target);
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const int part = wave % G.tpr, slice = wave / G.tpr;
+	const int r0 = (int)((int64_t)blockIdx.x * n_out / gridDim.x);
+	const int r1 = (int)((int64_t)(blockIdx.x + 1) * n_out / gridDim.x);
+	const int nrows = r1 - r0;
+	const size_t rb = (size_t)(n_in >> 8) * kQ6Bytes;
+	const int sub = lane & (G.seg - 1), rsub = lane / G.seg;
+	const int c = 64 * part + sub;              // this lane's chunk, fixed for every row
+	const bool lane_on = c < G.C;
+	const int ntiles = (nrows + G.rt - 1) / G.rt;
+	const int nit = ntiles > slice ? (ntiles - slice + G.rw - 1) / G.rw : 0;
+	auto item_row = [&](int it) -> int { return r0 + G.rt * (slice + G.rw * it) + rsub; };
+
+	const int cc = min(c, G.C - 1);           // in-bounds chunk for idle lanes' loads
+	const int i = cc >> 3, s = cc & 7, hn = s >> 2, l0 = 8 * (s & 3), sel = (s & 3) >> 1;
+	const size_t in_row = (size_t)i * kQ6Bytes;
+	// Weight loads are raw buffer loads, never predicated: slots with no work
+	// use an offset past the stream (zeros, no memory traffic). A branch
+	// around a load would make the compiler wait for all outstanding loads.
+	const __amdgpu_buffer_rsrc_t wr = stream_rsrc(w, (uint32_t)(rb * n_out));
+	auto issue = [&](Q6Buf &b, int it) {
+		const int row = item_row(it);
+		const bool on = it < nit && row < r1 && lane_on;
+		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + in_row) : kBufNone;
+		b.a = ld_b64(wr, blk + 64 * hn + l0);
+		b.b = ld_b64(wr, blk + 64 * hn + 32 + l0);
+		b.h = ld_b64(wr, blk + 128 + 32 * hn + l0);
+		b.s = ld_b64(wr, blk + 192 + 8 * hn);
+		b.d = ld_b16(wr, blk + 208);
 	};
 
-	Q6W Wn[R];
-	if (wk < tiles) load(wk, Wn);
+	Q6Col col;
+	q6_col_load(x, cc, col);   // issued first: these loads return first
+	// Keep every weight load below the activation loads (completion is in
+	// issue order).
+	__builtin_amdgcn_sched_barrier(0);
+	// Item loads go out in consumption order (the scheduler would otherwise
+	// interleave them, and the first item would wait for all four).
+	Q6Buf buf[kQ6Depth];
+#pragma unroll
+	for (int j = 0; j < kQ6Depth; j++) {
+		issue(buf[j], j);
+		__builtin_amdgcn_sched_barrier(0);
+	}
+	q6_col_sums(col);   // waits for x only: it was loaded first
 
-	float acc[R];
+	// Whole groups of kQ6Depth items (same load count every iteration; slots
+	// past nit load nothing). Their arithmetic is skipped by a wave-uniform
+	// branch that holds no loads; the group's four rows are reduced together.
+	for (int base = 0; base < nit; base += kQ6Depth) {
+		float rsum[kQ6Depth];
 #pragma unroll
-	for (int r = 0; r < R; r++) acc[r] = 0.0f;
-
-	for (int T = wk; T < tiles; T += KS) {
-		Q6W W[R];
-#pragma unroll
-		for (int r = 0; r < R; r++) W[r] = Wn[r];
-		if (MULTI && T + KS < tiles) load(T + KS, Wn);
-		const int c = (T << 6) + lane;
-		if (c < C) {
-			Q6Col col;
-			q6_col(x, c, col);
-			const int sel = (c & 3) >> 1;   // l0 / 16
-#pragma unroll
-			for (int r = 0; r < R; r++) acc[r] += q6_dot(W[r], col, sel);
+		for (int j = 0; j < kQ6Depth; j++) {
+			const int it = base + j;
+			const int row = item_row(it);
+			float d = 0.0f;
+			// Consume buf[j] in place, then reload it (no register rotation).
+			if (it < nit) d = q6_dot(buf[j], col, sel);
+			issue(buf[j], it + kQ6Depth);
+			__builtin_amdgcn_sched_barrier(0);
+			rsum[j] = (lane_on && row < r1) ? d : 0.0f;
+		}
+		// Rows with a bias, and split rows, finish after the weight stream: a
+		// bias load in the loop would wait for every weight load in flight.
+		const float tot = seg_sum4(rsum, G.seg, lane);
+		const int j = sub & 3;
+		const int row = item_row(base + j);
+		if (sub < kQ6Depth && base + j < nit && row < r1) {
+			if (G.tpr > 1)
+				red_s[(row - r0) * G.tpr + part] = tot;
+			else if (bias)
+				red_s[row - r0] = tot;
+			else
+				out[row] = tot;
 		}
 	}
-
-	float tot[R];
-#pragma unroll
-	for (int r = 0; r < R; r++) tot[r] = wave_sum(acc[r]);
-	if (KS == 1) {
-		float v = tot[0];
-#pragma unroll
-		for (int r = 1; r < R; r++) v = (lane == r) ? tot[r] : v;
-		const int row = row0 + lane;
-		if (lane < R && row < n_out) out[row] = bias ? v + bias[row] : v;
-	} else {
-		if (lane == 0) {
-#pragma unroll
-			for (int r = 0; r < R; r++) red_s[wave * R + r] = tot[r];
-		}
+	if (G.tpr > 1 || bias) {
 		__syncthreads();
-		if (wk == 0 && lane < R) {
+		for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
 			float v = 0.0f;
-#pragma unroll
-			for (int k = 0; k < KS; k++) v += red_s[(wr * KS + k) * R + lane];
-			const int row = row0 + lane;
-			if (row < n_out) out[row] = bias ? v + bias[row] : v;
+			for (int p = 0; p < G.tpr; p++) v += red_s[r * G.tpr + p];
+			out[r0 + r] = bias ? v + bias[r0 + r] : v;
 		}
 	}
 }
 
-template <int R, int KS, bool MULTI>
-int q6_launch3(int wgs, const uint8_t *w, const float *x, const float *bias, float *out, int n_out,
-               int n_in) {
-	hipLaunchKernelGGL((q6k_gemv_kernel<R, KS, MULTI>), dim3(wgs), dim3(256), 0, stream(), w, x, bias,
-	                   out, n_out, n_in);
-	HK_LAUNCHED("q6k_gemv");
-	return ok();
-}
-
-template <int R, int KS>
-int q6_launch2(bool multi, int wgs, const uint8_t *w, const float *x, const float *bias, float *out,
-               int n_out, int n_in) {
-	return multi ? q6_launch3<R, KS, true>(wgs, w, x, bias, out, n_out, n_in)
-	             : q6_launch3<R, KS, false>(wgs, w, x, bias, out, n_out, n_in);
-}
-
-template <int R>
-int q6_launch1(int KS, bool multi, int wgs, const uint8_t *w, const float *x, const float *bias,
-               float *out, int n_out, int n_in) {
-	switch (KS) {
-	case 1: return q6_launch2<R, 1>(multi, wgs, w, x, bias, out, n_out, n_in);
-	case 2: return q6_launch2<R, 2>(multi, wgs, w, x, bias, out, n_out, n_in);
-	default: return q6_launch2<R, 4>(multi, wgs, w, x, bias, out, n_out, n_in);
-	}
-}
+int g_q6_wgs_per_cu = 1;
+int g_q6_waves = 4;
 
 }  // namespace
+
+void q6k_set_wgs_per_cu(int v) { g_q6_wgs_per_cu = v < 1 ? 1 : (v > 8 ? 8 : v); }
+void q6k_set_waves(int v) { g_q6_waves = v >= 8 ? 8 : 4; }
+
 }  // namespace hako
 
 extern "C" int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, const float *bias,
@@ -212,23 +239,22 @@ extern "C" int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, cons
 		                 n_out, n_in);
 	if (((uintptr_t)w & 1) || ((uintptr_t)x & 15))
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV needs w 2-byte and x 16-byte aligned");
-	const int tiles = (n_in / kQK * 8 + 63) / 64;
-	const int KS = tiles >= 4 ? 4 : (tiles >= 2 ? 2 : 1);
-	const bool multi = tiles > KS;
-	int R = 1;
-	for (int r : {4, 2}) {
-		const int rows_per_wg = r * 4 / KS;
-		if ((n_out + rows_per_wg - 1) / rows_per_wg >= 512) {
-			R = r;
-			break;
-		}
-	}
-	const int rows_per_wg = R * 4 / KS;
-	const int wgs = (n_out + rows_per_wg - 1) / rows_per_wg;
-	const uint8_t *wb = (const uint8_t *)w;
-	switch (R) {
-	case 4: return q6_launch1<4>(KS, multi, wgs, wb, x, bias, out, n_out, n_in);
-	case 2: return q6_launch1<2>(KS, multi, wgs, wb, x, bias, out, n_out, n_in);
-	default: return q6_launch1<1>(KS, multi, wgs, wb, x, bias, out, n_out, n_in);
-	}
+	const Q6Geom G = q6_geom(n_in, g_q6_waves);
+	if ((size_t)n_out * (n_in / kQK) * kQ6Bytes >= kBufNone)
+		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV weight of %d x %d exceeds 2 GiB", n_out, n_in);
+	if (G.waves > kQ6MaxWaves)
+		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV n_in %d exceeds %d", n_in, kQ6MaxWaves * 64 * 32);
+	const int min_rows = G.rt * G.rw;
+	int wgs = (n_out + min_rows - 1) / min_rows;
+	const int max_wgs = g_q6_wgs_per_cu * cu_count();
+	if (wgs > max_wgs) wgs = max_wgs;
+	// partial row sums in LDS: at most 8192 rows x parts per workgroup
+	const int max_rows_per_wg = 8192 / G.tpr;
+	if ((n_out + wgs - 1) / wgs > max_rows_per_wg) wgs = (n_out + max_rows_per_wg - 1) / max_rows_per_wg;
+	const int rows_per_wg = (n_out + wgs - 1) / wgs;
+	const size_t lds = (size_t)rows_per_wg * G.tpr * sizeof(float);
+	hipLaunchKernelGGL(q6k_gemv_kernel, dim3(wgs), dim3(G.waves * kWave), lds, stream(), (const uint8_t *)w, x,
+	                   bias, out, n_out, n_in, g_q6_waves);
+	HK_LAUNCHED("q6k_gemv");
+	return ok();
 }

@@ -41,6 +41,8 @@ constexpr int kDppQuadSwap1 = 0xB1;
 constexpr int kDppQuadSwap2 = 0x4E;
 constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppMirror = 0x140;
+constexpr int kDppRowRor4 = 0x124;   // row_ror:4 (rotate within 16 lanes)
+constexpr int kDppRowRor8 = 0x128;   // row_ror:8
 
 // Sum over all 64 lanes; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
@@ -53,12 +55,65 @@ __device__ __forceinline__ float wave_sum(float v) {
 	return v;
 }
 
+// Sum over aligned segments of `seg` lanes (a power of two, 4..64); every
+// lane of a segment receives the segment's sum.
+__device__ __forceinline__ float seg_sum(float v, int seg) {
+	v += dpp_f<kDppQuadSwap1>(v);
+	v += dpp_f<kDppQuadSwap2>(v);
+	if (seg >= 8) v += dpp_f<kDppHalfMirror>(v);
+	if (seg >= 16) v += dpp_f<kDppMirror>(v);
+	if (seg >= 32) v += __shfl_xor(v, 16);
+	if (seg >= 64) v += __shfl_xor(v, 32);
+	return v;
+}
+
+// Four segment sums at once: v[j] is this lane's share of item j; lane L
+// receives the sum of item (L & 3) over its segment of `seg` lanes (a power of
+// two, 4..64). Two transposing swaps inside the quad halve the values each
+// time, then one value per lane is summed over the lanes of equal L & 3 —
+// one cross-row exchange per four items instead of one per item.
+__device__ __forceinline__ float seg_sum4(const float v[4], int seg, int lane) {
+	const bool odd = lane & 1, hi = lane & 2;
+	const float ka = odd ? v[1] : v[0], kb = odd ? v[3] : v[2];
+	const float sa = odd ? v[0] : v[1], sb = odd ? v[2] : v[3];
+	const float wa = ka + dpp_f<kDppQuadSwap1>(sa), wb = kb + dpp_f<kDppQuadSwap1>(sb);
+	float u = (hi ? wb : wa) + dpp_f<kDppQuadSwap2>(hi ? wa : wb);
+	if (seg == 8) u += __shfl_xor(u, 4);
+	if (seg >= 16) {
+		u += dpp_f<kDppRowRor4>(u);
+		u += dpp_f<kDppRowRor8>(u);
+	}
+	if (seg >= 32) u += __shfl_xor(u, 16);
+	if (seg >= 64) u += __shfl_xor(u, 32);
+	return u;
+}
+
 // Max over aligned groups of 8 lanes; every lane of the group receives it.
 __device__ __forceinline__ float max8(float v) {
 	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap1>(v));
 	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap2>(v));
 	v = __builtin_fmaxf(v, dpp_f<kDppHalfMirror>(v));
 	return v;
+}
+
+// Raw buffer access to a weight stream. Buffer loads are range-checked by
+// the hardware: an offset at or past `bytes` returns zeros without touching
+// memory, so pipeline slots with no work (past the last row, idle lanes) can
+// issue their loads unconditionally at no bandwidth cost.
+constexpr int kBufFlags = 0x00020000;      // raw (stride 0) 32-bit-format descriptor word 3
+constexpr uint32_t kBufNone = 0x80000000u; // an offset past every stream (streams < 2 GiB)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const void *base, uint32_t bytes) {
+	return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufFlags);
+}
+__device__ __forceinline__ uint4 ld_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+	return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint2 ld_b64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+	return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint32_t ld_b16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+	return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
 }
 
 // v_dot4_i32_i8: c + sum of the four signed byte products of a and b.

@@ -19,6 +19,13 @@ int hip_fail(hipError_t e, const char *what, const char *file, int line);
 hipStream_t stream();
 // HAKO_GPU_OK when a device is initialised, otherwise an ENODEV error.
 int require_device();
+// Compute units of the initialised device.
+int cu_count();
+// Workgroups per CU of the persistent GEMV grids (tuning; default 1).
+void q4k_set_wgs_per_cu(int v);
+void q6k_set_wgs_per_cu(int v);
+void q4k_set_waves(int v);
+void q6k_set_waves(int v);
 // Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
 int workspace(int slot, size_t bytes, void **ptr);
 

@@ -15,6 +15,15 @@ namespace {
 
 thread_local char g_err[512] = "";
 
+// Plain streaming copy, 16 bytes per lane per step (also the known-size
+// kernel that calibrates the HBM byte counters).
+__global__ __launch_bounds__(256) void copy16_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                                                     int64_t n16) {
+	for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+	     i += (int64_t)gridDim.x * blockDim.x)
+		dst[i] = src[i];
+}
+
 struct Mirror {
 	const uint8_t *host;
 	size_t bytes;
@@ -56,6 +65,11 @@ int hip_fail(hipError_t e, const char *what, const char *file, int line) {
 }
 
 hipStream_t stream() { return st().stream; }
+
+int cu_count() {
+	const int n = st().prop.multiProcessorCount;
+	return n > 0 ? n : 256;
+}
 
 int require_device() {
 	if (st().device < 0) return set_error(HAKO_GPU_ENODEV, "hako_gpu_init has not been called");
@@ -129,6 +143,16 @@ int hako_gpu_shutdown(void) {
 
 const char *hako_gpu_last_error(void) { return g_err; }
 
+int hako_gpu_tune(int knob, int value) {
+	switch (knob) {
+	case HAKO_TUNE_Q4K_WGS_PER_CU: q4k_set_wgs_per_cu(value); return ok();
+	case HAKO_TUNE_Q6K_WGS_PER_CU: q6k_set_wgs_per_cu(value); return ok();
+	case HAKO_TUNE_Q4K_WAVES: q4k_set_waves(value); return ok();
+	case HAKO_TUNE_Q6K_WAVES: q6k_set_waves(value); return ok();
+	default: return set_error(HAKO_GPU_EINVAL, "unknown tuning knob %d", knob);
+	}
+}
+
 int hako_gpu_device_info(hako_gpu_info *out) {
 	if (int rc = require_device()) return rc;
 	const hipDeviceProp_t &p = st().prop;
@@ -175,6 +199,16 @@ int hako_gpu_memcpy_d2h(void *dst, const void *src, size_t bytes) {
 
 int hako_gpu_memcpy_d2d(void *dst, const void *src, size_t bytes) {
 	if (int rc = require_device()) return rc;
+	if (bytes == 0) return ok();
+	if ((((uintptr_t)dst | (uintptr_t)src | bytes) & 15) == 0) {
+		const int64_t n16 = (int64_t)(bytes / 16);
+		int64_t grid = (n16 + 255) / 256;
+		if (grid > 8192) grid = 8192;
+		hipLaunchKernelGGL(copy16_kernel, dim3((unsigned)grid), dim3(256), 0, st().stream,
+		                   (const uint4 *)src, (uint4 *)dst, n16);
+		HK_LAUNCHED("copy16");
+		return ok();
+	}
 	HK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st().stream));
 	return ok();
 }

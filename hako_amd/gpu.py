@@ -25,6 +25,7 @@ SIGNATURES = {
     "hako_gpu_init": (_i, [_i]),
     "hako_gpu_shutdown": (_i, []),
     "hako_gpu_last_error": (C.c_char_p, []),
+    "hako_gpu_tune": (_i, [_i, _i]),
     "hako_gpu_device_info": (_i, [_vp]),
     "hako_gpu_malloc": (_i, [C.POINTER(_vp), _sz]),
     "hako_gpu_free": (_i, [_vp]),
@@ -121,6 +122,9 @@ class Gpu:
         if rc != 0:
             msg = self.lib.hako_gpu_last_error().decode(errors="replace")
             raise HakoGpuError(f"hako_gpu {what}: rc={rc}: {msg}")
+
+    def tune(self, knob: int, value: int):
+        self.check(self.lib.hako_gpu_tune(knob, value), "tune")
 
     def info(self) -> DeviceInfo:
         d = DeviceInfo()

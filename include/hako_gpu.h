@@ -50,6 +50,15 @@ int hako_gpu_shutdown(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char *hako_gpu_last_error(void);
 
+/* Launch-shape knobs of the GEMV kernels (for sweeps; results do not depend
+ * on them): workgroups per compute unit of the persistent grids (1..8) and
+ * waves per workgroup (4 or 8). */
+#define HAKO_TUNE_Q4K_WGS_PER_CU 1
+#define HAKO_TUNE_Q6K_WGS_PER_CU 2
+#define HAKO_TUNE_Q4K_WAVES      3
+#define HAKO_TUNE_Q6K_WAVES      4
+int hako_gpu_tune(int knob, int value);
+
 typedef struct {
 	char     name[64];        /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
 	int      compute_units;
