@@ -181,7 +181,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              f"(the hot path is a single-GPU GEMV; see the sharding note in DESIGN.md)", file=sys.stderr)
+              f"(the GEMV shards by rows; this build runs and measures one GPU)", file=sys.stderr)
         sys.exit(2)
 
     from hako_amd.gpu import Gpu
