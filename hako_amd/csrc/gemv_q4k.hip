@@ -106,12 +106,6 @@ __device__ __forceinline__ float q4_fold(const Q4Buf &b, uint32_t sh, uint32_t h
 	return d * t1 - dmin * t2;
 }
 
-__device__ __forceinline__ int next_pow2(int v) {
-	int p = 1;
-	while (p < v) p <<= 1;
-	return p;
-}
-
 // WIDE: rows of more than 64 chunks (n_in > 4096), taken in 64-chunk parts.
 // XP: activation quads per thread (x: 4 floats, xq: 16 bytes each), enough
 // that the whole activation is fetched by straight-line loads.
@@ -298,9 +292,134 @@ __global__ __launch_bounds__(WAVES * kWave) void q4k_gemv_kernel(
 	}
 }
 
+// Flat grid for rows of at most 64 chunks (n_in <= 4096): a workgroup owns
+// WAVES*ITEMS row items, a wave ITEMS consecutive ones, and every weight load
+// of the wave is issued at once, right after the activation (and bias) loads.
+// There is no loop: latency is hidden by the many workgroups resident on each
+// CU rather than by a software pipeline.
+template <int MODE, int XP, int WAVES, int ITEMS>
+__global__ __launch_bounds__(WAVES * kWave) void q4k_gemv_flat_kernel(
+    const uint8_t *__restrict__ w, const float *__restrict__ x, const int8_t *__restrict__ xq_g,
+    const float *__restrict__ xs_g, const float *__restrict__ bias, float *__restrict__ out,
+    int32_t *__restrict__ iqx_o, int32_t *__restrict__ ix_o, int n_out, int n_in) {
+	extern __shared__ __align__(16) uint8_t smem[];
+	int8_t *xq_s = (int8_t *)smem;
+	float *xs_s = (float *)(smem + n_in);
+	constexpr int T = WAVES * kWave;
+	constexpr int NG = (ITEMS + 3) / 4;   // groups of four items reduced together
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const int NB = n_in >> 8, C = NB * 4;
+	const int seg = next_pow2(C), rt = 64 / seg;
+	const int sub = lane & (seg - 1), rsub = lane / seg;
+	const size_t rb = (size_t)NB * kQ4Bytes;
+	const int wrow0 = (blockIdx.x * WAVES + wave) * ITEMS * rt;
+	auto item_row = [&](int it) -> int { return wrow0 + rt * it + rsub; };
+
+	// 1. activation, then bias, loads (they complete first).
+	float4 xv[XP];
+	int4 qv[XP];
+	float sv[2];
+	if (MODE == kFused) {
+#pragma unroll
+		for (int k = 0; k < XP; k++)
+			xv[k] = *(const float4 *)(x + min((int)(threadIdx.x + k * T) * 4, n_in - 4));
+	} else {
+#pragma unroll
+		for (int k = 0; k < XP; k++)
+			qv[k] = *(const int4 *)(xq_g + min((int)(threadIdx.x + k * T) * 16, n_in - 16));
+		if (MODE == kPreq) {
+#pragma unroll
+			for (int k = 0; k < 2; k++) sv[k] = xs_g[min((int)(threadIdx.x + k * T), (n_in >> 5) - 1)];
+		}
+	}
+	// The lane that writes item 4g + (sub & 3) loads that row's bias now; a
+	// null bias reads out[] (in bounds, discarded).
+	float bv[NG];
+	if (MODE != kIsums) {
+		const float *bsrc = bias ? bias : out;
+#pragma unroll
+		for (int g = 0; g < NG; g++) bv[g] = bsrc[min(item_row(4 * g + (sub & 3)), n_out - 1)];
+	}
+	__builtin_amdgcn_sched_barrier(0);
+	// 2. every weight load of the wave, in consumption order
+	const __amdgpu_buffer_rsrc_t wr = stream_rsrc(w, (uint32_t)(rb * n_out));
+	Q4Buf buf[ITEMS];
+#pragma unroll
+	for (int j = 0; j < ITEMS; j++) {
+		const int row = item_row(j);
+		const bool on = row < n_out && sub < C;
+		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + (size_t)(sub >> 2) * kQ4Bytes) : kBufNone;
+		buf[j].h = ld_b128(wr, blk);
+		buf[j].q0 = ld_b128(wr, blk + 16 + 32 * (sub & 3));
+		buf[j].q1 = ld_b128(wr, blk + 32 + 32 * (sub & 3));
+		__builtin_amdgcn_sched_barrier(0);
+	}
+	// 3. activation into LDS while the weights are in flight
+	if (MODE == kFused) {
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			const int e = (threadIdx.x + k * T) * 4;
+			float sc;
+			const uint32_t packed = q8_quant4(xv[k], sc);
+			if (e < n_in) {
+				*(uint32_t *)(xq_s + e) = packed;
+				if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
+			}
+		}
+	} else {
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			const int e = (threadIdx.x + k * T) * 16;
+			if (e < n_in) *(int4 *)(xq_s + e) = qv[k];
+		}
+#pragma unroll
+		for (int k = 0; k < 2; k++) {
+			const int e = threadIdx.x + k * T;
+			if (e < (n_in >> 5)) xs_s[e] = MODE == kPreq ? sv[k] : 0.0f;
+		}
+	}
+	__syncthreads();
+	Q4Col col;
+	q4_col(xq_s, xs_s, min(sub, C - 1), col);
+
+	float rsum[4 * NG];
+#pragma unroll
+	for (int j = 0; j < 4 * NG; j++) {
+		rsum[j] = 0.0f;
+		if (j >= ITEMS) continue;
+		const int row = item_row(j);
+		const bool valid = row < n_out && sub < C;
+		int ia, ib;
+		q4_isum(buf[j], col, ia, ib);
+		if (MODE == kIsums) {
+			if (valid) {
+				const size_t o = (size_t)row * (n_in >> 5) + 2 * sub;
+				iqx_o[o] = ia;
+				iqx_o[o + 1] = ib;
+				ix_o[o] = col.ia_sum;
+				ix_o[o + 1] = col.ib_sum;
+			}
+		} else {
+			const float f = q4_fold(buf[j], 16u * (sub & 1), (sub & 3) >= 2 ? ~0u : 0u, ia, ib, col);
+			rsum[j] = valid ? f : 0.0f;
+		}
+	}
+	if (MODE != kIsums) {
+#pragma unroll
+		for (int g = 0; g < NG; g++) {
+			const float tot = seg_sum4(rsum + 4 * g, seg, lane);
+			const int j = 4 * g + (sub & 3);
+			const int row = item_row(j);
+			if ((sub >> 2) == 0 && j < ITEMS && row < n_out) out[row] = bias ? tot + bv[g] : tot;
+		}
+	}
+}
+
 constexpr int kMaxQ4Lds = 64 * 1024;
 int g_q4_wgs_per_cu = 1;
 int g_q4_waves = 4;
+// -1: by shape (below); 0: persistent grid; 1, 2, 4, 8: flat grid with that many items per wave
+int g_q4_flat_items = -1;
 
 template <int MODE>
 int q4_launch(const uint8_t *w, const float *x, const int8_t *xq, const float *xs, const float *bias,
@@ -326,6 +445,44 @@ int q4_launch(const uint8_t *w, const float *x, const int8_t *xq, const float *x
 		int seg = 1;
 		while (seg < C) seg <<= 1;
 		rows_per_item = 64 / seg;
+	}
+	// By shape: the flat grid wins wherever the per-workgroup activation work
+	// is small — always for a pre-quantized activation, and for the fused
+	// quantization up to n_in = 2048; wider fused rows amortize the
+	// quantization better over the persistent grid's longer row ranges.
+	int items = g_q4_flat_items;
+	if (items < 0) items = (MODE != kFused || n_in <= 2048) ? 2 : 0;
+	if (!wide && items > 0) {
+		const int per_wg = waves * items * rows_per_item;
+		const int fwgs = (n_out + per_wg - 1) / per_wg;
+		const size_t flds = (size_t)n_in + (size_t)(n_in / 32) * 4;
+		const int per_round = MODE == kFused ? 4 * threads : 16 * threads;
+		const int fxp = (n_in + per_round - 1) / per_round;
+#define HK_Q4F(XP, WV, IT)                                                                                   \
+	hipLaunchKernelGGL((q4k_gemv_flat_kernel<MODE, XP, WV, IT>), dim3(fwgs), dim3(WV * kWave), flds, stream(), \
+	                   w, x, xq, xs, bias, out, iqx, ix, n_out, n_in)
+#define HK_Q4F_IT(XP, WV)                         \
+	do {                                          \
+		if (items <= 1) HK_Q4F(XP, WV, 1);        \
+		else if (items <= 2) HK_Q4F(XP, WV, 2);   \
+		else if (items <= 4) HK_Q4F(XP, WV, 4);   \
+		else HK_Q4F(XP, WV, 8);                   \
+	} while (0)
+#define HK_Q4F_XP(WV)                               \
+	do {                                            \
+		if (fxp <= 1) HK_Q4F_IT(1, WV);             \
+		else if (fxp <= 2) HK_Q4F_IT(2, WV);        \
+		else HK_Q4F_IT(4, WV);                      \
+	} while (0)
+		if (waves == 8)
+			HK_Q4F_XP(8);
+		else
+			HK_Q4F_XP(4);
+#undef HK_Q4F_XP
+#undef HK_Q4F_IT
+#undef HK_Q4F
+		HK_LAUNCHED("q4k_gemv_flat");
+		return ok();
 	}
 	// Persistent-style grid: a fixed number of workgroups per CU, each with a
 	// contiguous row range, never more workgroups than give one item per wave.
@@ -373,6 +530,7 @@ int q4k_matmul_fused(float *out, const float *x, const void *w, const float *bia
 
 void q4k_set_wgs_per_cu(int v) { g_q4_wgs_per_cu = v < 1 ? 1 : (v > 8 ? 8 : v); }
 void q4k_set_waves(int v) { g_q4_waves = v >= 8 ? 8 : 4; }
+void q4k_set_flat_items(int v) { g_q4_flat_items = v < 0 ? -1 : (v == 0 ? 0 : (v <= 1 ? 1 : (v <= 2 ? 2 : (v <= 4 ? 4 : 8)))); }
 
 }  // namespace hako
 

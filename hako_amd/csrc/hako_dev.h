@@ -116,6 +116,12 @@ __device__ __forceinline__ uint32_t ld_b16(__amdgpu_buffer_rsrc_t r, uint32_t of
 	return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
 }
 
+__host__ __device__ __forceinline__ int next_pow2(int v) {
+	int p = 1;
+	while (p < v) p <<= 1;
+	return p;
+}
+
 // v_dot4_i32_i8: c + sum of the four signed byte products of a and b.
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
 	return __builtin_amdgcn_sdot4(a, b, c, false);

@@ -26,6 +26,7 @@ void q4k_set_wgs_per_cu(int v);
 void q6k_set_wgs_per_cu(int v);
 void q4k_set_waves(int v);
 void q6k_set_waves(int v);
+void q4k_set_flat_items(int v);
 // Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
 int workspace(int slot, size_t bytes, void **ptr);
 

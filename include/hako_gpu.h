@@ -57,6 +57,7 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_Q6K_WGS_PER_CU 2
 #define HAKO_TUNE_Q4K_WAVES      3
 #define HAKO_TUNE_Q6K_WAVES      4
+#define HAKO_TUNE_Q4K_FLAT_ITEMS 5   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
 int hako_gpu_tune(int knob, int value);
 
 typedef struct {

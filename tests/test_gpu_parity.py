@@ -162,6 +162,47 @@ def test_q4k_gemv_prequantized_vs_oracle(gpu, oracle, n_out, n_in):
     assert maxabs_rel(got, want) < TOL
 
 
+HAKO_TUNE_Q4K_WAVES, HAKO_TUNE_Q4K_FLAT_ITEMS = 3, 5
+
+
+@pytest.mark.parametrize("n_out,n_in", [(11008, 2048), (1000, 3584), (37, 256), (300, 1280)])
+def test_q4k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
+    """Persistent and flat grids, 4 or 8 waves, 1..8 row items per wave: the
+    lane work and reduction order are the same, so outputs are identical."""
+    rng = np.random.default_rng(n_out + 3 * n_in)
+    w = synth.q4k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    bias = synth.activation(rng, n_out)
+    xq, xs = oracle.quantize_q8_32(x)
+    dw, dx, db, do = gpu.upload(w), gpu.upload(x), gpu.upload(bias), gpu.alloc(n_out * 4)
+    dq, ds = gpu.upload(xq), gpu.upload(xs)
+    di, dix = gpu.alloc(n_out * n_in // 32 * 4), gpu.alloc(n_out * n_in // 32 * 4)
+    seen = {}
+    try:
+        for items in (-1, 0, 1, 2, 4, 8):
+            for waves in (4, 8):
+                gpu.tune(HAKO_TUNE_Q4K_FLAT_ITEMS, items)
+                gpu.tune(HAKO_TUNE_Q4K_WAVES, waves)
+                gpu.matmul(do, dx, Q4, dw, db, n_out, n_in)
+                fused = gpu.download(do, np.float32, (n_out,))
+                gpu.q4k_gemv(do, dw, dq, ds, None, n_out, n_in)
+                preq = gpu.download(do, np.float32, (n_out,))
+                gpu.q4k_isums(di, dix, dw, dq, n_out, n_in)
+                sums = gpu.download(di, np.int32, (n_out, n_in // 32))
+                for k, v in (("fused", fused), ("preq", preq), ("isums", sums)):
+                    if k in seen:
+                        assert np.array_equal(seen[k].view(np.uint32), v.view(np.uint32)), (k, items, waves)
+                    else:
+                        seen[k] = v
+    finally:
+        gpu.tune(HAKO_TUNE_Q4K_FLAT_ITEMS, -1)
+        gpu.tune(HAKO_TUNE_Q4K_WAVES, 4)
+        for b in (dw, dx, db, do, dq, ds, di, dix):
+            b.free()
+    want = oracle.matmul(Q4, w, x, n_out, n_in, bias=bias, f64=True)
+    assert maxabs_rel(seen["fused"], want) < TOL
+
+
 Q6_SHAPES = [(2048, 11008), (151936, 2048), (3584, 18944), (256, 2048), (1, 256), (9, 768), (33, 11008)]
 
 
