@@ -1,0 +1,475 @@
+// gemm.hip — multi-token matmuls (prompt prefill) on the gfx950 matrix cores.
+//
+// The reference has no batched matmul: a prompt runs token by token, each
+// token one matmul per weight (cli/main.c:56-60, src/nn.c:179-210). These
+// kernels compute the same M independent products at once, Y[t][r] for
+// tokens t < M and weight rows r < n_out, with the weight stream read once per
+// 64-token tile instead of once per token.
+//
+// Q4_K x q8 (reference src/quant.c:150-232 per token and row). The activation
+// rows are quantized with the q8_32 scheme first (one launch over all rows).
+// One v_mfma_i32_32x32x32_i8 covers exactly one 32-wide sub-block, so its
+// int32 results are the reference's own per-sub-block sums iqx = Σ q·xq
+// (|iqx| <= 15*127*32, exact); they are folded per sub-block as
+// xs*(d*s*iqx − dmin*m*ix), written iqx*(xs*ds) + (−xs*ix)*dm with
+// ds = d*s and dm = dmin*m (exact fp32 products) precomputed per row. The
+// first term takes three VALU ops per output and sub-block against 32 int8
+// MACs of matrix-core work, so this kernel is bounded by the vector ALUs; the
+// second term is a product over sub-blocks and runs on fp32 MFMA.
+//
+// Q6_K x fp32 (reference src/nn.c:84-95: dequantized rows, fp32 dot). The
+// 6-bit values q−32 are exact in fp16 and so are the scales' products
+// d*sc in fp32; the fp32 activation is carried as two fp16 halves
+// hi + lo after scaling each token row by an exact power of two that brings
+// its largest magnitude into [1, 2). One v_mfma_f32_32x32x16_f16 covers one
+// 16-wide scale group: two of them (hi, lo) accumulate exact products in
+// fp32, the group result is scaled by d*sc and added, and the power of two is
+// applied at the end. The activation is thus represented to ~2^-22 relative,
+// well inside the 1e-5 output tolerance.
+//
+// Tiles: 64 tokens x 64 rows per workgroup of 4 waves (2 x 2, one 32 x 32
+// MFMA tile each); K advances one super-block (Q4_K) or half a super-block
+// (Q6_K) per stage, staged through LDS with the next stage's global loads in
+// flight during the current stage's arithmetic. Workgroup b runs on XCD
+// b % 8, and each XCD is given a contiguous run of tiles in token-tile-major
+// order: the workgroups resident on one XCD share one token tile, whose
+// activations then stay in that XCD's L2.
+#include "hako_dev.h"
+#include "hako_rt.h"
+
+namespace hako {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+constexpr int kTM = 64, kTN = 64;   // tokens, weight rows per workgroup tile
+constexpr int kGT = 256;            // threads per workgroup
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int xcd_tile(int b, int ntiles) {
+	const int per = (ntiles + kXcds - 1) / kXcds;
+	return (b % kXcds) * per + b / kXcds;
+}
+
+__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+	return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// ── Q4_K x q8 ──
+
+constexpr int kAPad = 272;   // bytes per staged token row: 256 + 16 (conflict-free 16-byte reads)
+
+__global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const uint8_t *__restrict__ w,
+                                                       const int8_t *__restrict__ xq,
+                                                       const float *__restrict__ xs,
+                                                       const float *__restrict__ bias,
+                                                       float *__restrict__ y, int M, int N, int K) {
+	__shared__ __align__(16) uint8_t w_s[kTN * kQ4Bytes];   // this stage's block of each row
+	__shared__ __align__(16) int8_t a_s[kTM * kAPad];       // this stage's 256 xq of each token
+	__shared__ __align__(16) float ds_s[8][kTN];            // d*s   [sub-block][row]
+	__shared__ __align__(16) float dm_s[8][kTN];            // dmin*m
+	__shared__ __align__(16) float2 xn_s[8][kTM];           // (xs, -xs*Σxq) [sub-block][token]
+
+	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
+	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
+	if (tile >= mtiles * ntiles) return;
+	const int m0 = (tile / ntiles) * kTM, n0 = (tile % ntiles) * kTN;
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int wr = wave & 1, wt = wave >> 1, li = lane & 31, kh = lane >> 5;
+	const int NB = K >> 8, NS = K >> 5;
+	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
+	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(w, rb * (uint32_t)N);
+	const __amdgpu_buffer_rsrc_t ars = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
+	const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
+
+	// Stage map: weights 64 rows x 9 pieces of 16 B (3 per thread), xq 64
+	// tokens x 16 pieces (4 per thread), xs 64 tokens x 8 (2 per thread).
+	uint4 wreg[3], areg[4];
+	float sreg[2];
+	auto load_stage = [&](int kb) {
+#pragma unroll
+		for (int u = 0; u < 3; u++) {
+			const int c = tid + kGT * u, row = c / 9, piece = c - row * 9;
+			const bool on = c < kTN * 9 && n0 + row < N;
+			wreg[u] = ld_b128(wrs, on ? (uint32_t)(n0 + row) * rb + (uint32_t)kb * kQ4Bytes + 16u * piece : kBufNone);
+		}
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
+			const bool on = m0 + tok < M;
+			areg[u] = ld_b128(ars, on ? (uint32_t)(m0 + tok) * K + 256u * kb + 16u * piece : kBufNone);
+		}
+#pragma unroll
+		for (int u = 0; u < 2; u++) {
+			const int c = tid + kGT * u, tok = c >> 3, sb = c & 7;
+			const bool on = m0 + tok < M;
+			sreg[u] = ld_f32(srs, on ? 4u * ((uint32_t)(m0 + tok) * NS + 8u * kb + sb) : kBufNone);
+		}
+	};
+	auto store_stage = [&]() {
+#pragma unroll
+		for (int u = 0; u < 3; u++) {
+			const int c = tid + kGT * u, row = c / 9, piece = c - row * 9;
+			if (c < kTN * 9) *(uint4 *)(w_s + row * kQ4Bytes + 16 * piece) = wreg[u];
+		}
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
+			*(uint4 *)(a_s + tok * kAPad + 16 * piece) = areg[u];
+		}
+	};
+	// per (row, sub-block): ds, dm; per (token, sub-block): xs, -xs*Σxq
+	auto derive = [&]() {
+#pragma unroll
+		for (int u = 0; u < 2; u++) {
+			const int c = tid + kGT * u, r = c >> 3, sb = c & 7;
+			const uint4 h = *(const uint4 *)(w_s + r * kQ4Bytes);
+			uint32_t s, m;
+			scale_min_k4((uint32_t)sb, h.y, h.z, h.w, s, m);
+			ds_s[sb][r] = f16_to_f32(h.x & 0xFFFFu) * (float)s;
+			dm_s[sb][r] = f16_to_f32(h.x >> 16) * (float)m;
+			const int4 *p = (const int4 *)(a_s + r * kAPad + 32 * sb);   // r doubles as the token here
+			const int4 p0 = p[0], p1 = p[1];
+			int ix = 0;
+			ix = sdot4(p0.x, 0x01010101, ix); ix = sdot4(p0.y, 0x01010101, ix);
+			ix = sdot4(p0.z, 0x01010101, ix); ix = sdot4(p0.w, 0x01010101, ix);
+			ix = sdot4(p1.x, 0x01010101, ix); ix = sdot4(p1.y, 0x01010101, ix);
+			ix = sdot4(p1.z, 0x01010101, ix); ix = sdot4(p1.w, 0x01010101, ix);
+			xn_s[sb][r] = make_float2(sreg[u], -sreg[u] * (float)ix);
+		}
+	};
+
+	v16f acc = {}, accm = {};
+	const v16i zero = {};
+	const uint32_t lo4 = 0x0F0F0F0Fu;
+	load_stage(0);
+	for (int kb = 0; kb < NB; kb++) {
+		store_stage();
+		__syncthreads();
+		derive();
+		__syncthreads();
+		if (kb + 1 < NB) load_stage(kb + 1);   // in flight during this stage's arithmetic
+		// The min term Σ_sb dm[row][sb] * (−xs*Σxq)[token][sb] is a small fp32
+		// product over the block's 8 sub-blocks: four v_mfma_f32_32x32x2_f32
+		// into their own accumulator (K index = sub-block, one per lane half).
+#pragma unroll
+		for (int p = 0; p < 4; p++) {
+			const int sb = 2 * p + kh;
+			accm = __builtin_amdgcn_mfma_f32_32x32x2f32(dm_s[sb][32 * wr + li], xn_s[sb][32 * wt + li].y, accm, 0,
+			                                           0, 0);
+		}
+#pragma unroll
+		for (int g = 0; g < 4; g++) {
+			// weight row 32wr+li: qs bytes 32g+16kh.. hold K 16kh.. of sub-blocks 2g (low
+			// nibbles) and 2g+1 (high nibbles)
+			const uint4 q = *(const uint4 *)(w_s + (32 * wr + li) * kQ4Bytes + 16 + 32 * g + 16 * kh);
+			const v4i qlo = {(int)(q.x & lo4), (int)(q.y & lo4), (int)(q.z & lo4), (int)(q.w & lo4)};
+			const v4i qhi = {(int)((q.x >> 4) & lo4), (int)((q.y >> 4) & lo4), (int)((q.z >> 4) & lo4),
+			                 (int)((q.w >> 4) & lo4)};
+#pragma unroll
+			for (int h = 0; h < 2; h++) {
+				const int sb = 2 * g + h;
+				const v4i b = *(const v4i *)(a_s + (32 * wt + li) * kAPad + 32 * sb + 16 * kh);
+				const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? qhi : qlo, b, zero, 0, 0, 0);
+				const float xsj = xn_s[sb][32 * wt + li].x;
+#pragma unroll
+				for (int q4 = 0; q4 < 4; q4++) {
+					const float4 dsv = *(const float4 *)&ds_s[sb][32 * wr + 8 * q4 + 4 * kh];
+					const float dsa[4] = {dsv.x, dsv.y, dsv.z, dsv.w};
+#pragma unroll
+					for (int r = 0; r < 4; r++) {
+						const int v = 4 * q4 + r;
+						acc[v] = __builtin_fmaf((float)d[v], xsj * dsa[r], acc[v]);
+					}
+				}
+			}
+		}
+		__syncthreads();   // before the next stage overwrites LDS
+	}
+	// lane: token m0+32wt+li, rows n0+32wr+8q4+4kh+r
+	const int tok = m0 + 32 * wt + li;
+	if (tok >= M) return;
+	float *yr = y + (size_t)tok * N;
+#pragma unroll
+	for (int q4 = 0; q4 < 4; q4++) {
+		const int row = n0 + 32 * wr + 8 * q4 + 4 * kh;
+#pragma unroll
+		for (int r = 0; r < 4; r++)
+			if (row + r < N) {
+				const float v = acc[4 * q4 + r] + accm[4 * q4 + r];
+				yr[row + r] = bias ? v + bias[row + r] : v;
+			}
+	}
+}
+
+// ── Q6_K x fp32 ──
+
+// Token row t of x (K floats): s = 2^-e with max|x_t| in [2^e, 2^(e+1)),
+// hi = fp16(x*s), lo = fp16(x*s - hi), esc[t] = 2^e. The scaling is exact,
+// and x*s - hi is exact in fp32.
+__global__ __launch_bounds__(kGT) void f16_split_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
+                                                        _Float16 *__restrict__ xl, float *__restrict__ esc,
+                                                        int K) {
+	__shared__ float red[kGT / kWave];
+	const size_t base = (size_t)blockIdx.x * K;
+	const float *xr = x + base;
+	float a = 0.0f;
+	for (int i = threadIdx.x * 4; i < K; i += kGT * 4) {
+		const float4 v = *(const float4 *)(xr + i);
+		a = __builtin_fmaxf(a, __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+		                                       __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
+	}
+	a = __builtin_fmaxf(a, dpp_f<kDppQuadSwap1>(a));
+	a = __builtin_fmaxf(a, dpp_f<kDppQuadSwap2>(a));
+	a = __builtin_fmaxf(a, dpp_f<kDppHalfMirror>(a));
+	a = __builtin_fmaxf(a, dpp_f<kDppMirror>(a));
+	a = __builtin_fmaxf(a, __shfl_xor(a, 16));
+	a = __builtin_fmaxf(a, __shfl_xor(a, 32));
+	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
+	__syncthreads();
+	a = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+	int e = 0;
+	if (a > 0.0f && __builtin_isfinite(a)) {
+		// exponent of a normal a; subnormal rows clamp to -126, which keeps 2^-e
+		// finite and loses nothing that matters at that size
+		e = (int)((__builtin_bit_cast(uint32_t, a) >> 23) & 0xFFu) - 127;
+		e = e < -126 ? -126 : e;
+	}
+	const float s = __builtin_ldexpf(1.0f, -e);
+	if (threadIdx.x == 0) esc[blockIdx.x] = __builtin_ldexpf(1.0f, e);
+	for (int i = threadIdx.x * 4; i < K; i += kGT * 4) {
+		const float4 v = *(const float4 *)(xr + i);
+		const float f[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
+#pragma unroll
+		for (int j = 0; j < 4; j++) {
+			const _Float16 h = (_Float16)f[j];
+			xh[base + i + j] = h;
+			xl[base + i + j] = (_Float16)(f[j] - (float)h);
+		}
+	}
+}
+
+// Two of the 6-bit values in `v` (bytes picked by the v_perm selector `sel`
+// into the low byte of each half) as the fp16 pair (q0 - 32, q1 - 32):
+// 0x6400 | q is 1024 + q exactly, and 1024 + q - 1056 is exact.
+__device__ __forceinline__ uint32_t q6_pair(uint32_t v, uint32_t sel) {
+	typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+	const uint32_t t = __builtin_amdgcn_perm(v, v, sel) | 0x64006400u;
+	const v2h r = __builtin_bit_cast(v2h, t) - (v2h){(_Float16)1056.0f, (_Float16)1056.0f};
+	return __builtin_bit_cast(uint32_t, r);
+}
+
+constexpr int kQ6Stage = 128;        // K per stage: half a super-block
+constexpr int kHPad = kQ6Stage + 8;  // fp16 per staged row (272 B: conflict-free 16-byte reads)
+
+__global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict__ w,
+                                                       const _Float16 *__restrict__ xh,
+                                                       const _Float16 *__restrict__ xl,
+                                                       const float *__restrict__ esc,
+                                                       const float *__restrict__ bias,
+                                                       float *__restrict__ y, int M, int N, int K) {
+	__shared__ __align__(16) _Float16 ah_s[kTM * kHPad];   // activation hi [token][k]
+	__shared__ __align__(16) _Float16 al_s[kTM * kHPad];   // activation lo
+	__shared__ __align__(16) _Float16 wq_s[kTN * kHPad];   // q - 32 [row][k]
+	__shared__ __align__(16) float dsc_s[8][kTN];          // d*sc [group][row]
+
+	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
+	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
+	if (tile >= mtiles * ntiles) return;
+	const int m0 = (tile / ntiles) * kTM, n0 = (tile % ntiles) * kTN;
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int wr = wave & 1, wt = wave >> 1, li = lane & 31, kh = lane >> 5;
+	const int NB = K >> 8;
+	const uint32_t rb = (uint32_t)NB * kQ6Bytes;
+	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(w, rb * (uint32_t)N);
+	const __amdgpu_buffer_rsrc_t hrs = stream_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
+	const __amdgpu_buffer_rsrc_t lrs = stream_rsrc(xl, (uint32_t)M * (uint32_t)K * 2u);
+
+	// Stage st = half n of block st/2. Activations: 64 tokens x 16 pieces of
+	// 16 B (8 fp16) for hi and lo, 4 + 4 per thread. Weights: thread (row
+	// tid/4, part p = tid%4) takes ql[64n+16p, +16) — K 32(p/2)+16(p%2)+b
+	// (low nibbles) and that + 64 (high nibbles) of the half — with qh
+	// [32n+16(p%2), +16), and the scales 8n+2p, 8n+2p+1 and d.
+	const int wrow = tid >> 2, part = tid & 3;
+	uint4 hreg[4], lreg[4];
+	uint2 qlr[2], qhr[2];
+	uint32_t scr, dr;
+	auto load_stage = [&](int st) {
+		const int kb = st >> 1, n = st & 1;
+		const uint32_t k0 = (uint32_t)kQ6Stage * st;
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
+			const bool on = m0 + tok < M;
+			const uint32_t off = on ? 2u * ((uint32_t)(m0 + tok) * K + k0 + 8u * piece) : kBufNone;
+			hreg[u] = ld_b128(hrs, off);
+			lreg[u] = ld_b128(lrs, off);
+		}
+		const bool on = n0 + wrow < N;
+		const uint32_t blk = on ? (uint32_t)(n0 + wrow) * rb + (uint32_t)kb * kQ6Bytes : kBufNone;
+		const uint32_t oql = 64u * n + 16u * part, oqh = 128u + 32u * n + 16u * (part & 1);
+		qlr[0] = ld_b64(wrs, blk + oql);
+		qlr[1] = ld_b64(wrs, blk + oql + 8);
+		qhr[0] = ld_b64(wrs, blk + oqh);
+		qhr[1] = ld_b64(wrs, blk + oqh + 8);
+		scr = ld_b16(wrs, blk + 192u + 8u * n + 2u * part);
+		dr = ld_b16(wrs, blk + 208u);
+	};
+	auto store_stage = [&]() {
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
+			*(uint4 *)(ah_s + tok * kHPad + 8 * piece) = hreg[u];
+			*(uint4 *)(al_s + tok * kHPad + 8 * piece) = lreg[u];
+		}
+		// 6-bit values: low nibble | qh bits 2k1 (k1 = part/2) -> K 32k1 + l,
+		// high nibble | qh bits 2k1+4 -> K 32(k1+2) + l, with l = 16(part%2) + b.
+		const int k1 = part >> 1, l0 = 16 * (part & 1);
+		const uint32_t ql[4] = {qlr[0].x, qlr[0].y, qlr[1].x, qlr[1].y};
+		const uint32_t qh[4] = {qhr[0].x, qhr[0].y, qhr[1].x, qhr[1].y};
+		uint32_t lo[8], hi[8];   // fp16 pairs
+#pragma unroll
+		for (int j = 0; j < 4; j++) {
+			const uint32_t vlo = (ql[j] & 0x0F0F0F0Fu) | (((qh[j] >> (2 * k1)) & 0x03030303u) << 4);
+			const uint32_t vhi = ((ql[j] >> 4) & 0x0F0F0F0Fu) | (((qh[j] >> (2 * k1 + 4)) & 0x03030303u) << 4);
+			lo[2 * j] = q6_pair(vlo, 0x0C010C00u);
+			lo[2 * j + 1] = q6_pair(vlo, 0x0C030C02u);
+			hi[2 * j] = q6_pair(vhi, 0x0C010C00u);
+			hi[2 * j + 1] = q6_pair(vhi, 0x0C030C02u);
+		}
+		uint8_t *wrow_s = (uint8_t *)(wq_s + wrow * kHPad);
+		*(uint4 *)(wrow_s + 2 * (32 * k1 + l0)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+		*(uint4 *)(wrow_s + 2 * (32 * k1 + l0 + 8)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+		*(uint4 *)(wrow_s + 2 * (32 * (k1 + 2) + l0)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+		*(uint4 *)(wrow_s + 2 * (32 * (k1 + 2) + l0 + 8)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+		// group gg = 2*part + i covers K [16gg, 16gg+16): scale 8n + gg
+		const float d = f16_to_f32(dr);
+		dsc_s[2 * part][wrow] = d * (float)(int8_t)(scr & 0xFFu);
+		dsc_s[2 * part + 1][wrow] = d * (float)(int8_t)(scr >> 8);
+	};
+
+	v16f acc = {};
+	const v16f zero = {};
+	const int NSt = NB * 2;
+	load_stage(0);
+	for (int st = 0; st < NSt; st++) {
+		store_stage();
+		__syncthreads();
+		if (st + 1 < NSt) load_stage(st + 1);
+		const _Float16 *ah = ah_s + (32 * wt + li) * kHPad + 8 * kh;
+		const _Float16 *al = al_s + (32 * wt + li) * kHPad + 8 * kh;
+		const _Float16 *wq = wq_s + (32 * wr + li) * kHPad + 8 * kh;
+#pragma unroll
+		for (int gg = 0; gg < 8; gg++) {
+			const v8h b = *(const v8h *)(wq + 16 * gg);
+			v16f p = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const v8h *)(ah + 16 * gg), b, zero, 0, 0, 0);
+			p = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const v8h *)(al + 16 * gg), b, p, 0, 0, 0);
+			const float s = dsc_s[gg][32 * wr + li];
+#pragma unroll
+			for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf(p[v], s, acc[v]);
+		}
+		__syncthreads();
+	}
+	// lane: row n0+32wr+li, tokens m0+32wt+8q4+4kh+r
+	const int row = n0 + 32 * wr + li;
+	if (row >= N) return;
+	const float bv = bias ? bias[row] : 0.0f;
+#pragma unroll
+	for (int v = 0; v < 16; v++) {
+		const int tok = m0 + 32 * wt + 8 * (v >> 2) + 4 * kh + (v & 3);
+		if (tok < M) y[(size_t)tok * N + row] = acc[v] * esc[tok] + bv;
+	}
+}
+
+int gemm_grid(int M, int N) {
+	const int tiles = ((M + kTM - 1) / kTM) * ((N + kTN - 1) / kTN);
+	return kXcds * ((tiles + kXcds - 1) / kXcds);
+}
+
+int check_gemm(const char *what, int m, int n_out, int n_in, size_t row_bytes, const void *w) {
+	if (int rc = require_device()) return rc;
+	if (m <= 0 || n_out <= 0 || n_in <= 0 || n_in % kQK != 0)
+		return set_error(HAKO_GPU_EINVAL, "%s needs m, n_out > 0 and n_in %% 256 == 0 (got %d x %d x %d)", what,
+		                 m, n_out, n_in);
+	if (row_bytes * (size_t)n_out >= kBufNone || (size_t)m * n_in * 2 >= kBufNone)
+		return set_error(HAKO_GPU_EINVAL, "%s operands exceed 2 GiB (%d x %d x %d)", what, m, n_out, n_in);
+	if ((uintptr_t)w & 1) return set_error(HAKO_GPU_EINVAL, "%s needs a 2-byte aligned weight", what);
+	return HAKO_GPU_OK;
+}
+
+}  // namespace
+
+int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const float *bias, int m, int n_out,
+             int n_in) {
+	if (int rc = check_gemm("Q4_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ4Bytes, w)) return rc;
+	if (((uintptr_t)w & 15) || ((uintptr_t)xq & 15) || ((uintptr_t)xs & 3))
+		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM needs w and xq 16-byte aligned");
+	hipLaunchKernelGGL(q4k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
+	                   xq, xs, bias, y, m, n_out, n_in);
+	HK_LAUNCHED("q4k_gemm");
+	return ok();
+}
+
+int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, int n_out, int n_in) {
+	if (int rc = check_gemm("Q6_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ6Bytes, w)) return rc;
+	if ((uintptr_t)x & 15) return set_error(HAKO_GPU_EINVAL, "Q6_K GEMM needs x 16-byte aligned");
+	// workspace: fp16 hi and lo of x, one power of two per token
+	const size_t half_bytes = (size_t)m * n_in * 2, esc_off = 2 * ((half_bytes + 255) & ~(size_t)255);
+	void *ws = nullptr;
+	if (int rc = workspace(3, esc_off + (size_t)m * 4, &ws)) return rc;
+	_Float16 *xh = (_Float16 *)ws;
+	_Float16 *xl = (_Float16 *)((uint8_t *)ws + esc_off / 2);
+	float *esc = (float *)((uint8_t *)ws + esc_off);
+	hipLaunchKernelGGL(f16_split_kernel, dim3(m), dim3(kGT), 0, stream(), x, xh, xl, esc, n_in);
+	HK_LAUNCHED("f16_split");
+	hipLaunchKernelGGL(q6k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
+	                   xh, xl, esc, bias, y, m, n_out, n_in);
+	HK_LAUNCHED("q6k_gemm");
+	return ok();
+}
+
+}  // namespace hako
+
+extern "C" int hako_gpu_q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const float *bias,
+                                 int m, int n_out, int n_in) {
+	return hako::q4k_gemm(y, w, xq, xs, bias, m, n_out, n_in);
+}
+
+extern "C" int hako_gpu_q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, int n_out,
+                                 int n_in) {
+	return hako::q6k_gemm(y, w, x, bias, m, n_out, n_in);
+}
+
+extern "C" int hako_gpu_matmul_batch(float *y, const float *x, int type, const void *w, const float *bias, int m,
+                                     int n_out, int n_in) {
+	using namespace hako;
+	if (int rc = require_device()) return rc;
+	if (m <= 0) return set_error(HAKO_GPU_EINVAL, "matmul_batch needs m > 0 (got %d)", m);
+	if (m == 1) return hako_gpu_matmul(y, x, type, w, bias, n_out, n_in);
+	switch (type) {
+	case HAKO_TYPE_Q4_K: {
+		if (n_in <= 0 || n_in % kQK != 0)
+			return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM needs n_in %% 256 == 0 (got %d)", n_in);
+		const size_t qbytes = ((size_t)m * n_in + 255) & ~(size_t)255;
+		void *ws = nullptr;
+		if (int rc = workspace(4, qbytes + (size_t)m * (n_in / 32) * 4, &ws)) return rc;
+		int8_t *xq = (int8_t *)ws;
+		float *xs = (float *)((uint8_t *)ws + qbytes);
+		if (int rc = hako_gpu_quantize_q8_32(x, m, n_in, xq, xs)) return rc;
+		return q4k_gemm(y, w, xq, xs, bias, m, n_out, n_in);
+	}
+	case HAKO_TYPE_Q6_K:
+		return q6k_gemm(y, w, x, bias, m, n_out, n_in);
+	case HAKO_TYPE_F32:
+	case HAKO_TYPE_F16:
+		for (int t = 0; t < m; t++)
+			if (int rc = hako_gpu_dense_gemv(y + (size_t)t * n_out, type, w, x + (size_t)t * n_in, bias, n_out, n_in))
+				return rc;
+		return ok();
+	default:
+		return set_error(HAKO_GPU_ETYPE, "unsupported tensor type %d", type);
+	}
+}

@@ -53,6 +53,9 @@ SIGNATURES = {
     "hako_gpu_dense_gemv": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i]),
     "hako_gpu_matmul": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i]),
     "hako_gpu_matmul_host": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i]),
+    "hako_gpu_q4k_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "hako_gpu_q6k_gemm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "hako_gpu_matmul_batch": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _i]),
 }
 
 
@@ -204,6 +207,17 @@ class Gpu:
     def matmul(self, out, x, qtype: int, w, bias, n_out: int, n_in: int):
         self.check(self.lib.hako_gpu_matmul(_ptr(out), _ptr(x), qtype, _ptr(w), _ptr(bias), n_out, n_in),
                    "matmul")
+
+    def q4k_gemm(self, y, w, xq, xs, bias, m: int, n_out: int, n_in: int):
+        self.check(self.lib.hako_gpu_q4k_gemm(_ptr(y), _ptr(w), _ptr(xq), _ptr(xs), _ptr(bias), m, n_out, n_in),
+                   "q4k_gemm")
+
+    def q6k_gemm(self, y, w, x, bias, m: int, n_out: int, n_in: int):
+        self.check(self.lib.hako_gpu_q6k_gemm(_ptr(y), _ptr(w), _ptr(x), _ptr(bias), m, n_out, n_in), "q6k_gemm")
+
+    def matmul_batch(self, y, x, qtype: int, w, bias, m: int, n_out: int, n_in: int):
+        self.check(self.lib.hako_gpu_matmul_batch(_ptr(y), _ptr(x), qtype, _ptr(w), _ptr(bias), m, n_out, n_in),
+                   "matmul_batch")
 
     def matmul_host(self, out: np.ndarray, x: np.ndarray, qtype: int, w_host: np.ndarray,
                     bias: np.ndarray | None, n_out: int, n_in: int):

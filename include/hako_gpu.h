@@ -143,6 +143,30 @@ int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, const float *bi
 int hako_gpu_dense_gemv(float *out, int type, const void *w, const float *x,
                         const float *bias, int n_out, int n_in);
 
+/* ── multi-token matmuls (prompt prefill) ──
+ * Y[t][r] for tokens t < m: the m independent products the reference computes
+ * with one matmul call per token (src/nn.c:179-210, once per prompt token as
+ * cli/main.c:56-60 feeds them). y is [m][n_out], x / xq are [m][n_in],
+ * xs is [m][n_in/32]. */
+
+/* Q4_K x q8 on int8 matrix cores: per 32-wide sub-block integer sums exactly
+ * as q4k_vec_dot (src/quant.c:150-232), folded in fp32. bias may be NULL. */
+int hako_gpu_q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs,
+                      const float *bias, int m, int n_out, int n_in);
+
+/* Q6_K x fp32 (the reference's generic row path, src/nn.c:84-95) on fp16
+ * matrix cores, the activation carried as two fp16 halves. Uses a library
+ * workspace (grown on first use: not inside a graph capture). */
+int hako_gpu_q6k_gemm(float *y, const void *w, const float *x, const float *bias,
+                      int m, int n_out, int n_in);
+
+/* matmul over m activation rows for any supported type: Q4_K quantizes the
+ * rows with the q8_32 scheme (library workspace) then runs the Q4_K GEMM;
+ * Q6_K runs the Q6_K GEMM; F32/F16 run one GEMV per row; m == 1 is
+ * hako_gpu_matmul. */
+int hako_gpu_matmul_batch(float *y, const float *x, int type, const void *w,
+                          const float *bias, int m, int n_out, int n_in);
+
 /* matmul (reference src/nn.c:179-210) on device pointers: out[n_out] =
  * W x (+bias) for a weight of any supported type. For Q4_K the activation is
  * quantized with the q8_32 scheme inside the GEMV's workgroups (in LDS), so
