@@ -1,0 +1,929 @@
+// decode.hip — device-resident Qwen2 decode step (include/hako_decode.h).
+//
+// One step is the reference's hakm_forward (src/model.c:93-165) plus its
+// greedy pick (src/sample.c:28-32), as a fixed sequence of launches that
+// reads the token and position from device memory, so it is captured once as
+// a HIP graph and replayed for every token. Per layer, with the Q4_K_M mix:
+//
+//   1. q/k/v: rmsnorm + q8_32 quantization in the workgroup prologue, the
+//      three Q4_K matrices as row segments of one GEMV, biases added;
+//   2. attention: NeoX rope of the group's query heads and of the new key,
+//      KV-cache append, softmax attention over 64-position chunks of the cache
+//      (one workgroup per chunk and KV head), partial results merged by the
+//      last workgroup of each head group to finish;
+//   3. output projection (q8 prologue) added into the residual stream;
+//   4. gate/up: rmsnorm + q8 prologue, gate and up rows interleaved so each
+//      wave holds both sums of a row and writes silu(gate)*up;
+//   5. down projection (Q6_K x fp32) added into the residual stream.
+//
+// Then the final rmsnorm, the lm_head GEMV and the argmax, which writes the
+// next token, appends it to the output ring and advances the position.
+// Other weight types run the same step through the generic matmul and
+// separate elementwise launches.
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/hako_decode.h"
+#include "dequant_dev.h"
+#include "hako_dev.h"
+#include "hako_rt.h"
+#include "q4k_dev.h"
+
+namespace hako {
+
+int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n_out, int n_in, bool acc_out);
+
+namespace {
+
+constexpr int kChunk = 64;   // cache positions per attention workgroup
+constexpr int kMaxG = 8;     // query heads per KV head
+constexpr int kArgBlocks = 64;
+constexpr int kDecItems = 2; // row items per wave of the fused GEMV
+
+__device__ __forceinline__ float wave_max(float v) {
+	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap1>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap2>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppHalfMirror>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppMirror>(v));
+	v = __builtin_fmaxf(v, __shfl_xor(v, 16));
+	v = __builtin_fmaxf(v, __shfl_xor(v, 32));
+	return v;
+}
+
+// silu (reference src/nn.c:29)
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// ── embedding row (deq_row, reference src/nn.c:55-59) ──
+
+__global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ emb, int type, size_t row_bytes,
+                                                    const int *__restrict__ tok, float *__restrict__ x, int D,
+                                                    int vocab) {
+	const int sq = blockIdx.x;
+	int t = tok[sq];
+	t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+	const uint8_t *row = emb + (size_t)t * row_bytes;
+	float *y = x + (size_t)sq * D;
+	if (type == HAKO_TYPE_Q6_K || type == HAKO_TYPE_Q4_K) {
+		for (int c = threadIdx.x; c < D / 32; c += blockDim.x) {
+			if (type == HAKO_TYPE_Q6_K)
+				dq6_chunk(row, c, y);
+			else
+				dq4_chunk(row, c, y);
+		}
+	} else if (type == HAKO_TYPE_F16) {
+		for (int i = threadIdx.x; i < D; i += blockDim.x) y[i] = f16_to_f32(((const uint16_t *)row)[i]);
+	} else {
+		for (int i = threadIdx.x; i < D; i += blockDim.x) y[i] = ((const float *)row)[i];
+	}
+}
+
+// ── rmsnorm (reference src/nn.c:13-18) and the elementwise fallbacks ──
+
+// ss over the row, scale = 1/sqrt(ss/n + eps), y = x*scale*w.
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+	v = wave_sum(v);
+	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+	__syncthreads();
+	const float t = red[0] + red[1] + red[2] + red[3];
+	__syncthreads();
+	return t;
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                      float *__restrict__ y, int n, float eps) {
+	__shared__ float red[4];
+	const float *xr = x + (size_t)blockIdx.x * n;
+	float ss = 0.0f;
+	for (int i = threadIdx.x; i < n; i += 256) ss = __builtin_fmaf(xr[i], xr[i], ss);
+	ss = block_sum256(ss, red);
+	const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+	for (int i = threadIdx.x; i < n; i += 256) y[(size_t)blockIdx.x * n + i] = xr[i] * scale * w[i];
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float *__restrict__ x, const float *__restrict__ y, int n) {
+	const int i = blockIdx.x * 256 + threadIdx.x;
+	if (i < n) x[i] += y[i];
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ h, const float *__restrict__ g,
+                                                       const float *__restrict__ u, int n) {
+	const int i = blockIdx.x * 256 + threadIdx.x;
+	if (i < n) h[i] = silu(g[i]) * u[i];
+}
+
+// ── fused Q4_K GEMV of the decode step ──
+
+struct DecSeg {
+	const uint8_t *w;    // weight rows of the segment
+	const float *bias;   // F32 bias or null
+	float *out;          // output rows of the segment
+	int row0, rows;      // first row in the launch's row space, row count
+};
+struct DecSegs {
+	DecSeg s[3];
+	int n;
+};
+
+enum { kProQ8 = 0, kProNorm = 1 };
+enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2 };
+
+// Flat grid (as the standalone Q4_K GEMV): a wave owns ITEMS row items of
+// rt rows, every weight load issued at once behind the activation loads.
+// Row space: segments one after the other (Store, Add; a wave never
+// straddles two), or for SwiGLU gate row r = 2r and up row r = 2r+1, so the
+// two sums of a row land in one wave. The activation x (n_in floats) is
+// quantized with the q8_32 scheme in the prologue, after rmsnorm with weight
+// nw for kProNorm.
+template <int PRO, int EPI, int XP, int ITEMS>
+__global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float *__restrict__ x,
+                                                      const float *__restrict__ nw, float eps, int n_in,
+                                                      int vrows) {
+	extern __shared__ __align__(16) uint8_t smem[];
+	int8_t *xq_s = (int8_t *)smem;
+	float *xs_s = (float *)(smem + n_in);
+	float *red_s = xs_s + (n_in >> 5);
+	constexpr int T = 256, WAVES = 4;
+	constexpr int NG = (ITEMS + 3) / 4;
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const int NB = n_in >> 8, C = NB * 4;
+	const int seg = next_pow2(C), rt = 64 / seg;
+	const int sub = lane & (seg - 1), rsub = lane / seg;
+	const size_t rb = (size_t)NB * kQ4Bytes;
+	const int wrow0 = (blockIdx.x * WAVES + wave) * ITEMS * rt;
+
+	// this wave's segment (Store / Add)
+	const int si = EPI == kEpiSwiGLU ? 0
+	               : (segs.n > 2 && wrow0 >= segs.s[2].row0) ? 2
+	               : (segs.n > 1 && wrow0 >= segs.s[1].row0) ? 1 : 0;
+	const uint8_t *sw = si == 0 ? segs.s[0].w : (si == 1 ? segs.s[1].w : segs.s[2].w);
+	const float *sbias = si == 0 ? segs.s[0].bias : (si == 1 ? segs.s[1].bias : segs.s[2].bias);
+	float *sout = si == 0 ? segs.s[0].out : (si == 1 ? segs.s[1].out : segs.s[2].out);
+	const int srow0 = si == 0 ? segs.s[0].row0 : (si == 1 ? segs.s[1].row0 : segs.s[2].row0);
+	const int srows = si == 0 ? segs.s[0].rows : (si == 1 ? segs.s[1].rows : segs.s[2].rows);
+
+	// item it, this lane: row of its matrix, weight base, validity
+	auto item_row = [&](int it) -> int {
+		const int v = wrow0 + rt * it + rsub;
+		return EPI == kEpiSwiGLU ? (v >> 1) : v - srow0;
+	};
+	auto item_w = [&](int it) -> const uint8_t * {
+		if (EPI != kEpiSwiGLU) return sw;
+		return ((wrow0 + rt * it + rsub) & 1) ? segs.s[1].w : segs.s[0].w;
+	};
+	auto item_ok = [&](int it) -> bool {
+		const int v = wrow0 + rt * it + rsub;
+		return v < vrows && item_row(it) < srows;
+	};
+
+	// 1. activation (and norm weight) loads, then residual / bias, then weights
+	float4 xv[XP], nv[XP];
+#pragma unroll
+	for (int k = 0; k < XP; k++) {
+		const int e = min((int)(threadIdx.x + k * T) * 4, n_in - 4);
+		xv[k] = *(const float4 *)(x + e);
+		if (PRO == kProNorm) nv[k] = *(const float4 *)(nw + e);
+	}
+	float pre[NG];   // bias (Store) or the residual (Add) of the row this lane writes
+	if (EPI != kEpiSwiGLU) {
+#pragma unroll
+		for (int g = 0; g < NG; g++) {
+			const int r = min(item_row(4 * g + (sub & 3)), srows - 1);
+			const float *src = EPI == kEpiAdd ? sout : (sbias ? sbias : x);
+			pre[g] = src[EPI == kEpiAdd || sbias ? r : 0];
+		}
+	}
+	__builtin_amdgcn_sched_barrier(0);
+	Q4Buf buf[ITEMS];
+#pragma unroll
+	for (int j = 0; j < ITEMS; j++) {
+		const bool on = item_ok(j) && sub < C;
+		const uint8_t *p = item_w(j) + (on ? (size_t)item_row(j) * rb + (size_t)(sub >> 2) * kQ4Bytes : 0);
+		buf[j].h = *(const uint4 *)p;
+		buf[j].q0 = *(const uint4 *)(p + 16 + 32 * (sub & 3));
+		buf[j].q1 = *(const uint4 *)(p + 32 + 32 * (sub & 3));
+		__builtin_amdgcn_sched_barrier(0);
+	}
+
+	// 2. prologue: (rmsnorm and) q8_32 quantization into LDS
+	float scale = 1.0f;
+	if (PRO == kProNorm) {
+		float ss = 0.0f;
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			if ((int)(threadIdx.x + k * T) * 4 < n_in) {
+				ss = __builtin_fmaf(xv[k].x, xv[k].x, ss);
+				ss = __builtin_fmaf(xv[k].y, xv[k].y, ss);
+				ss = __builtin_fmaf(xv[k].z, xv[k].z, ss);
+				ss = __builtin_fmaf(xv[k].w, xv[k].w, ss);
+			}
+		}
+		ss = wave_sum(ss);
+		if (lane == 0) red_s[wave] = ss;
+		__syncthreads();
+		ss = red_s[0] + red_s[1] + red_s[2] + red_s[3];
+		scale = 1.0f / sqrtf(ss / (float)n_in + eps);
+	}
+#pragma unroll
+	for (int k = 0; k < XP; k++) {
+		const int e = (threadIdx.x + k * T) * 4;
+		float4 v = xv[k];
+		if (PRO == kProNorm) {
+			v.x = v.x * scale * nv[k].x;
+			v.y = v.y * scale * nv[k].y;
+			v.z = v.z * scale * nv[k].z;
+			v.w = v.w * scale * nv[k].w;
+		}
+		float sc;
+		const uint32_t packed = q8_quant4(v, sc);
+		if (e < n_in) {
+			*(uint32_t *)(xq_s + e) = packed;
+			if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
+		}
+	}
+	__syncthreads();
+	Q4Col col;
+	q4_col(xq_s, xs_s, min(sub, C - 1), col);
+
+	// 3. the row sums
+	float rsum[4 * NG];
+#pragma unroll
+	for (int j = 0; j < 4 * NG; j++) {
+		rsum[j] = 0.0f;
+		if (j >= ITEMS) continue;
+		int ia, ib;
+		q4_isum(buf[j], col, ia, ib);
+		const float f = q4_fold(buf[j], 16u * (sub & 1), (sub & 3) >= 2 ? ~0u : 0u, ia, ib, col);
+		rsum[j] = (item_ok(j) && sub < C) ? f : 0.0f;
+	}
+	// 4. epilogue: lane sub = j (< 4) of each segment holds item 4g + j
+#pragma unroll
+	for (int g = 0; g < NG; g++) {
+		const float tot = seg_sum4(rsum + 4 * g, seg, lane);
+		const int j = 4 * g + (sub & 3);
+		const bool writer = (sub >> 2) == 0 && j < ITEMS && item_ok(j);
+		if (EPI == kEpiSwiGLU) {
+			// partner holding the up row: the next segment (rt >= 2) or the next item (rt == 1)
+			const float other = rt >= 2 ? __shfl(tot, lane + seg) : dpp_f<kDppQuadSwap1>(tot);
+			const bool gate = rt >= 2 ? (rsub & 1) == 0 : (j & 1) == 0;
+			if (writer && gate) segs.s[0].out[item_row(j)] = silu(tot) * other;
+		} else if (writer) {
+			sout[item_row(j)] = EPI == kEpiAdd ? pre[g] + tot : (sbias ? tot + pre[g] : tot);
+		}
+	}
+}
+
+// ── attention (reference src/model.c:105-137) ──
+
+// Workgroup (chunk c, KV head kvh, sequence sq) of 256 threads: positions
+// [64c, 64c+64) up to pos. Every key and value load of the chunk is issued
+// first (thread = position x quarter of the head dims for keys, value dims x
+// 16-position group for values), so the chunk costs one memory latency. The
+// group's query heads are rotated into LDS (NeoX, the rope table holding
+// cos/sin of pos*theta^(-2i/hd)); the workgroup whose chunk holds pos also
+// rotates the new key, appends it and the new value to the caches and uses
+// them from LDS. Scores, chunk-local softmax (max m, sum l) and the weighted
+// value sum o go to `part`; the last workgroup of the (sq, kvh) group to
+// finish merges the chunks: out = Σ o_c e^(m_c-M) / Σ l_c e^(m_c-M).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv, const float2 *__restrict__ rope,
+                                                   float *kc, float *vc, const int *__restrict__ posv,
+                                                   float *part, int *cnt, float *__restrict__ att, int H, int KVH,
+                                                   int max_seq, int max_chunks, size_t kv_seq_stride,
+                                                   int qkv_stride, float scale) {
+	constexpr int HALF = HD / 2;
+	constexpr int REC = HD + 2;      // partial record: o[HD], m, l
+	constexpr int KQ = HD / 16;      // float4 of a key row per thread (4 threads per position)
+	constexpr int DV = HD / 64;      // value dims per thread
+	constexpr int PG = 16;           // positions per value group (4 groups)
+	__shared__ float q_s[kMaxG][HD];
+	__shared__ float s_s[kMaxG][kChunk];        // scores, then e^(score - m)
+	__shared__ float ml_s[kMaxG][2];
+	__shared__ float o_s[4][kMaxG][HD];         // value sums per position group
+	__shared__ float kn_s[HD], vn_s[HD];
+	__shared__ int last_s;
+	const int c = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z;
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int G = H / KVH, KV = KVH * HD, D = H * HD;
+	const int pos = posv[sq];
+	if (pos < 0 || pos >= max_seq) return;   // no room left: the host refuses such steps
+	const int nact = pos / kChunk + 1;
+	if (c >= nact) return;
+	const bool has_pos = c == nact - 1;
+	const float *q = qkv + (size_t)sq * qkv_stride;
+	float *kcs = kc + (size_t)sq * kv_seq_stride + kvh * HD;
+	float *vcs = vc + (size_t)sq * kv_seq_stride + kvh * HD;
+
+	// 1. every key and value load of the chunk (rows past pos read row pos:
+	//    in bounds, discarded)
+	const int kp = tid >> 2, kq = tid & 3;
+	const int ks = c * kChunk + kp;
+	const float *krow = kcs + (size_t)min(ks, pos) * KV + kq * (HD / 4);
+	float4 kr[KQ];
+#pragma unroll
+	for (int j = 0; j < KQ; j++) kr[j] = *(const float4 *)(krow + 4 * j);
+	const int vd = DV * lane, vg = wave;
+	float vr[PG][DV];
+#pragma unroll
+	for (int j = 0; j < PG; j++) {
+		const float *row = vcs + (size_t)min(c * kChunk + PG * vg + j, pos) * KV + vd;
+		if (DV == 2) {
+			const float2 t = *(const float2 *)row;
+			vr[j][0] = t.x;
+			vr[j][DV - 1] = t.y;
+		} else {
+			vr[j][0] = row[0];
+		}
+	}
+	// rows past pos carry weight 0; zero them too, so no stale value reaches a sum
+#pragma unroll
+	for (int j = 0; j < PG; j++)
+		if (c * kChunk + PG * vg + j > pos)
+#pragma unroll
+			for (int u = 0; u < DV; u++) vr[j][u] = 0.0f;
+
+	// 2. rotated query heads (and the new key, value) into LDS
+	const float2 *rp = rope + (size_t)pos * HALF;
+	for (int t = tid; t < G * HALF; t += 256) {
+		const int g = t / HALF, i = t - g * HALF;
+		const float2 cs = rp[i];
+		const float a = q[(kvh * G + g) * HD + i], b = q[(kvh * G + g) * HD + i + HALF];
+		q_s[g][i] = a * cs.x - b * cs.y;
+		q_s[g][i + HALF] = a * cs.y + b * cs.x;
+	}
+	if (has_pos) {
+		for (int i = tid; i < HALF; i += 256) {
+			const float2 cs = rp[i];
+			const float a = q[D + kvh * HD + i], b = q[D + kvh * HD + i + HALF];
+			const float k0 = a * cs.x - b * cs.y, k1 = a * cs.y + b * cs.x;
+			kn_s[i] = k0;
+			kn_s[i + HALF] = k1;
+			kcs[(size_t)pos * KV + i] = k0;
+			kcs[(size_t)pos * KV + i + HALF] = k1;
+		}
+		for (int i = tid; i < HD; i += 256) {
+			const float v = q[D + KV + kvh * HD + i];
+			vn_s[i] = v;
+			vcs[(size_t)pos * KV + i] = v;
+		}
+	}
+	__syncthreads();
+
+	// 3. scores: 4 threads per position, a quarter of the dims each
+	if (ks == pos) {
+#pragma unroll
+		for (int j = 0; j < KQ; j++) kr[j] = *(const float4 *)(kn_s + kq * (HD / 4) + 4 * j);
+	}
+#pragma unroll
+	for (int g = 0; g < kMaxG; g++) {
+		if (g < G) {
+			float a = 0.0f;
+			const float *qg = q_s[g] + kq * (HD / 4);
+#pragma unroll
+			for (int j = 0; j < KQ; j++) {
+				a = __builtin_fmaf(qg[4 * j], kr[j].x, a);
+				a = __builtin_fmaf(qg[4 * j + 1], kr[j].y, a);
+				a = __builtin_fmaf(qg[4 * j + 2], kr[j].z, a);
+				a = __builtin_fmaf(qg[4 * j + 3], kr[j].w, a);
+			}
+			a += dpp_f<kDppQuadSwap1>(a);
+			a += dpp_f<kDppQuadSwap2>(a);
+			if (kq == 0) s_s[g][kp] = ks <= pos ? a * scale : -INFINITY;
+		}
+	}
+	__syncthreads();
+
+	// 4. chunk-local softmax: wave w takes heads w, w+4
+#pragma unroll
+	for (int h = 0; h < kMaxG / 4; h++) {
+		const int g = wave + 4 * h;
+		if (g < G) {
+			const float v = s_s[g][lane];
+			const float m = wave_max(v);
+			const float e = v == -INFINITY ? 0.0f : expf(v - m);
+			const float l = wave_sum(e);
+			s_s[g][lane] = e;
+			if (lane == 0) {
+				ml_s[g][0] = m;
+				ml_s[g][1] = l;
+			}
+		}
+	}
+	__syncthreads();
+
+	// 5. weighted values over this thread's 16 positions, then over the 4 groups
+	if (has_pos) {
+		const int j = pos - c * kChunk - PG * vg;
+		if (j >= 0 && j < PG) {
+#pragma unroll
+			for (int jj = 0; jj < PG; jj++)
+				if (jj == j)
+#pragma unroll
+					for (int u = 0; u < DV; u++) vr[jj][u] = vn_s[vd + u];
+		}
+	}
+#pragma unroll
+	for (int g = 0; g < kMaxG; g++) {
+		if (g < G) {
+			float o[DV];
+#pragma unroll
+			for (int u = 0; u < DV; u++) o[u] = 0.0f;
+#pragma unroll
+			for (int j = 0; j < PG; j++) {
+				const float w = s_s[g][PG * vg + j];
+#pragma unroll
+				for (int u = 0; u < DV; u++) o[u] = __builtin_fmaf(w, vr[j][u], o[u]);
+			}
+#pragma unroll
+			for (int u = 0; u < DV; u++) o_s[vg][g][vd + u] = o[u];
+		}
+	}
+	__syncthreads();
+	float *rec0 = part + (((size_t)(sq * KVH + kvh) * max_chunks + c) * kMaxG) * REC;
+	for (int t = tid; t < G * HD; t += 256) {
+		const int g = t / HD, d = t - g * HD;
+		rec0[(size_t)g * REC + d] = o_s[0][g][d] + o_s[1][g][d] + o_s[2][g][d] + o_s[3][g][d];
+	}
+	if (tid < G) {
+		rec0[(size_t)tid * REC + HD] = ml_s[tid][0];
+		rec0[(size_t)tid * REC + HD + 1] = ml_s[tid][1];
+	}
+	__threadfence();
+	__syncthreads();
+	if (tid == 0) last_s = atomicAdd(&cnt[sq * KVH + kvh], 1) == nact - 1;
+	__syncthreads();
+	if (!last_s) return;
+	__threadfence();
+
+	// 6. merge the chunks: M, L per head (wave w: heads w, w+4), then the sums
+	const float *grp = part + ((size_t)(sq * KVH + kvh) * max_chunks) * kMaxG * REC;
+#pragma unroll
+	for (int h = 0; h < kMaxG / 4; h++) {
+		const int g = wave + 4 * h;
+		if (g < G) {
+			float mx = -INFINITY;
+			for (int cc = lane; cc < nact; cc += 64) mx = __builtin_fmaxf(mx, grp[((size_t)cc * kMaxG + g) * REC + HD]);
+			mx = wave_max(mx);
+			float lsum = 0.0f;
+			for (int cc = lane; cc < nact; cc += 64) {
+				const float *r = grp + ((size_t)cc * kMaxG + g) * REC;
+				lsum += r[HD + 1] * expf(r[HD] - mx);
+			}
+			lsum = wave_sum(lsum);
+			if (lane == 0) {
+				ml_s[g][0] = mx;
+				ml_s[g][1] = lsum;
+			}
+		}
+	}
+	__syncthreads();
+	for (int t = tid; t < G * HD; t += 256) {
+		const int g = t / HD, d = t - g * HD;
+		const float mx = ml_s[g][0];
+		float acc = 0.0f;
+		int cc = 0;
+		for (; cc + 4 <= nact; cc += 4) {
+			const float *r0 = grp + ((size_t)cc * kMaxG + g) * REC;
+			const float *r1 = r0 + kMaxG * REC, *r2 = r1 + kMaxG * REC, *r3 = r2 + kMaxG * REC;
+			const float o0 = r0[d], o1 = r1[d], o2 = r2[d], o3 = r3[d];
+			const float m0 = r0[HD], m1 = r1[HD], m2 = r2[HD], m3 = r3[HD];
+			acc = __builtin_fmaf(o0, expf(m0 - mx), acc);
+			acc = __builtin_fmaf(o1, expf(m1 - mx), acc);
+			acc = __builtin_fmaf(o2, expf(m2 - mx), acc);
+			acc = __builtin_fmaf(o3, expf(m3 - mx), acc);
+		}
+		for (; cc < nact; cc++) {
+			const float *r = grp + ((size_t)cc * kMaxG + g) * REC;
+			acc = __builtin_fmaf(r[d], expf(r[HD] - mx), acc);
+		}
+		att[(size_t)sq * D + (size_t)(kvh * G + g) * HD + d] = acc / ml_s[g][1];
+	}
+	if (tid == 0) atomicExch(&cnt[sq * KVH + kvh], 0);   // ready for the next step
+}
+
+// ── greedy pick (reference src/sample.c:28-32) ──
+
+// (value, index) order: larger value first, then lower index (the reference's
+// ascending scan with a strict >); NaN never wins.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+	if (v != v) return false;
+	if (bv != bv) return true;
+	return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void argmax_wave(float &v, int &i) {
+#pragma unroll
+	for (int off = 1; off < 64; off <<= 1) {
+		const float ov = __shfl_xor(v, off);
+		const int oi = __shfl_xor(i, off);
+		if (better(ov, oi, v, i)) {
+			v = ov;
+			i = oi;
+		}
+	}
+}
+
+// Grid (kArgBlocks, n_seq). The last block of a sequence writes the token,
+// appends it to the ring and advances the position.
+__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int V, int *tok, int *posv,
+                                                     int *ring, int ring_len, int *nout, float2 *part, int *cnt) {
+	__shared__ float bv_s[4];
+	__shared__ int bi_s[4];
+	__shared__ int last_s;
+	const int b = blockIdx.x, sq = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	const float *lg = logits + (size_t)sq * V;
+	const int i0 = (int)((int64_t)b * V / kArgBlocks), i1 = (int)((int64_t)(b + 1) * V / kArgBlocks);
+	float bv = NAN;
+	int bi = 0x7FFFFFFF;
+	for (int i = i0 + threadIdx.x; i < i1; i += 256)
+		if (better(lg[i], i, bv, bi)) {
+			bv = lg[i];
+			bi = i;
+		}
+	argmax_wave(bv, bi);
+	if (lane == 0) {
+		bv_s[wave] = bv;
+		bi_s[wave] = bi;
+	}
+	__syncthreads();
+	if (threadIdx.x == 0) {
+		for (int w = 1; w < 4; w++)
+			if (better(bv_s[w], bi_s[w], bv, bi)) {
+				bv = bv_s[w];
+				bi = bi_s[w];
+			}
+		part[sq * kArgBlocks + b] = make_float2(bv, __builtin_bit_cast(float, bi));
+		__threadfence();
+		last_s = atomicAdd(&cnt[sq], 1) == kArgBlocks - 1;
+	}
+	__syncthreads();
+	if (!last_s || wave != 0) return;
+	__threadfence();
+	const float2 p = part[sq * kArgBlocks + lane];
+	float v = p.x;
+	int i = __builtin_bit_cast(int, p.y);
+	argmax_wave(v, i);
+	if (lane == 0) {
+		const int t = i == 0x7FFFFFFF ? 0 : i;   // all NaN: index 0, as the reference
+		tok[sq] = t;
+		const int n = nout[sq];
+		if (n < ring_len) ring[(size_t)sq * ring_len + n] = t;
+		nout[sq] = n + 1;
+		posv[sq] += 1;
+		atomicExch(&cnt[sq], 0);
+	}
+}
+
+size_t row_bytes(int type, int n) {
+	switch (type) {
+	case HAKO_TYPE_Q4_K: return (size_t)n / kQK * kQ4Bytes;
+	case HAKO_TYPE_Q6_K: return (size_t)n / kQK * kQ6Bytes;
+	case HAKO_TYPE_F16: return (size_t)n * 2;
+	case HAKO_TYPE_F32: return (size_t)n * 4;
+	default: return 0;
+	}
+}
+
+bool known_type(int t) {
+	return t == HAKO_TYPE_Q4_K || t == HAKO_TYPE_Q6_K || t == HAKO_TYPE_F16 || t == HAKO_TYPE_F32;
+}
+
+}  // namespace
+}  // namespace hako
+
+using namespace hako;
+
+struct hako_gpu_decoder {
+	hako_gpu_model m{};
+	std::vector<hako_gpu_block> blocks;
+	int n_seq = 0, max_seq = 0, max_chunks = 0, kv_dim = 0, qkv_dim = 0;
+	// device state
+	float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *g = nullptr, *u = nullptr,
+	      *tmp = nullptr, *logits = nullptr, *part = nullptr, *kc = nullptr, *vc = nullptr;
+	float2 *rope = nullptr, *apart = nullptr;
+	int *tok = nullptr, *pos = nullptr, *acnt = nullptr, *mcnt = nullptr, *ring = nullptr, *nout = nullptr;
+	std::vector<void *> allocs;
+	hipGraphExec_t exec = nullptr;
+	hipGraph_t graph = nullptr;
+};
+
+namespace {
+
+int dalloc(hako_gpu_decoder *d, size_t bytes, void **p) {
+	if (hipMalloc(p, bytes < 256 ? 256 : bytes) != hipSuccess) {
+		(void)hipGetLastError();
+		return set_error(HAKO_GPU_ENOMEM, "decoder allocation of %zu bytes", bytes);
+	}
+	d->allocs.push_back(*p);
+	return HAKO_GPU_OK;
+}
+
+// Launch helpers of the fused Q4_K GEMV: XP activation quads per thread.
+template <int PRO, int EPI>
+int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, int n_in, int vrows) {
+	const int C = n_in / kQK * 4;
+	const int rt = 64 / next_pow2(C);
+	const int rows_wg = 4 * kDecItems * rt;
+	const int wgs = (vrows + rows_wg - 1) / rows_wg;
+	const size_t lds = (size_t)n_in + (size_t)(n_in / 32) * 4 + 16;
+	const int xp = (n_in + 1023) / 1024;
+#define HK_DEC(XP) \
+	hipLaunchKernelGGL((q4k_dec_kernel<PRO, EPI, XP, kDecItems>), dim3(wgs), dim3(256), lds, stream(), segs, x, nw, eps, \
+	                   n_in, vrows)
+	if (xp <= 1) HK_DEC(1);
+	else if (xp <= 2) HK_DEC(2);
+	else HK_DEC(4);
+#undef HK_DEC
+	HK_LAUNCHED("q4k_dec");
+	return HAKO_GPU_OK;
+}
+
+// rows per wave of the fused GEMV at this n_in (segment starts must be multiples)
+int dec_rows_per_wave(int n_in) { return kDecItems * (64 / next_pow2(n_in / kQK * 4)); }
+
+bool fusable_q4(int n_in) { return n_in % kQK == 0 && n_in / kQK * 4 <= 64; }
+
+int rmsnorm(const float *x, const float *w, float *y, int n, float eps, int rows) {
+	hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream(), x, w, y, n, eps);
+	HK_LAUNCHED("rmsnorm");
+	return HAKO_GPU_OK;
+}
+
+int add(float *x, const float *y, int n) {
+	hipLaunchKernelGGL(add_kernel, dim3((n + 255) / 256), dim3(256), 0, stream(), x, y, n);
+	HK_LAUNCHED("add");
+	return HAKO_GPU_OK;
+}
+
+// One decode step on the library stream (n_seq == 1).
+int enqueue_step(hako_gpu_decoder *d) {
+	const hako_gpu_model &m = d->m;
+	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, HD = m.head_dim;
+	hipLaunchKernelGGL(embed_kernel, dim3(d->n_seq), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
+	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
+	HK_LAUNCHED("embed");
+	const float scale = 1.0f / sqrtf((float)HD);
+	const size_t kv_seq_stride = (size_t)m.n_layers * d->max_seq * KV;
+	for (int l = 0; l < m.n_layers; l++) {
+		const hako_gpu_block &B = d->blocks[l];
+		float *q = d->qkv, *k = d->qkv + D, *v = d->qkv + D + KV;
+		// 1. q, k, v
+		const int rpw = dec_rows_per_wave(D);
+		if (B.t_q == HAKO_TYPE_Q4_K && B.t_k == HAKO_TYPE_Q4_K && B.t_v == HAKO_TYPE_Q4_K && fusable_q4(D) &&
+		    D % rpw == 0 && KV % rpw == 0) {
+			DecSegs s{};
+			s.n = 3;
+			s.s[0] = {(const uint8_t *)B.wq, B.bq, q, 0, D};
+			s.s[1] = {(const uint8_t *)B.wk, B.bk, k, D, KV};
+			s.s[2] = {(const uint8_t *)B.wv, B.bv, v, D + KV, KV};
+			if (int rc = launch_dec<kProNorm, kEpiStore>(s, d->x, B.attn_norm, m.rms_eps, D, D + 2 * KV)) return rc;
+		} else {
+			if (int rc = rmsnorm(d->x, B.attn_norm, d->xn, D, m.rms_eps, 1)) return rc;
+			if (int rc = hako_gpu_matmul(q, d->xn, B.t_q, B.wq, B.bq, D, D)) return rc;
+			if (int rc = hako_gpu_matmul(k, d->xn, B.t_k, B.wk, B.bk, KV, D)) return rc;
+			if (int rc = hako_gpu_matmul(v, d->xn, B.t_v, B.wv, B.bv, KV, D)) return rc;
+		}
+		// 2. rope, cache append, attention
+		float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
+		const dim3 ag(d->max_chunks, m.n_kv_heads, d->n_seq);
+		if (HD == 128)
+			hipLaunchKernelGGL(attn_kernel<128>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim,
+			                   scale);
+		else
+			hipLaunchKernelGGL(attn_kernel<64>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim,
+			                   scale);
+		HK_LAUNCHED("attention");
+		// 3. output projection + residual
+		if (B.t_o == HAKO_TYPE_Q4_K && fusable_q4(D) && D % rpw == 0) {
+			DecSegs s{};
+			s.n = 1;
+			s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D};
+			if (int rc = launch_dec<kProQ8, kEpiAdd>(s, d->att, nullptr, 0.0f, D, D)) return rc;
+		} else {
+			if (int rc = hako_gpu_matmul(d->tmp, d->att, B.t_o, B.wo, nullptr, D, D)) return rc;
+			if (int rc = add(d->x, d->tmp, D)) return rc;
+		}
+		// 4. gate, up, SwiGLU
+		if (B.t_gate == HAKO_TYPE_Q4_K && B.t_up == HAKO_TYPE_Q4_K && fusable_q4(D)) {
+			DecSegs s{};
+			s.n = 2;
+			s.s[0] = {(const uint8_t *)B.gate, nullptr, d->h, 0, F};
+			s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, 0, F};
+			if (int rc = launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)) return rc;
+		} else {
+			if (int rc = rmsnorm(d->x, B.ffn_norm, d->xn, D, m.rms_eps, 1)) return rc;
+			if (int rc = hako_gpu_matmul(d->g, d->xn, B.t_gate, B.gate, nullptr, F, D)) return rc;
+			if (int rc = hako_gpu_matmul(d->u, d->xn, B.t_up, B.up, nullptr, F, D)) return rc;
+			hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, stream(), d->h, d->g, d->u, F);
+			HK_LAUNCHED("silu_mul");
+		}
+		// 5. down projection + residual
+		if (B.t_down == HAKO_TYPE_Q6_K) {
+			if (int rc = q6k_gemv(d->x, B.down, d->h, nullptr, D, F, true)) return rc;
+		} else {
+			if (int rc = hako_gpu_matmul(d->tmp, d->h, B.t_down, B.down, nullptr, D, F)) return rc;
+			if (int rc = add(d->x, d->tmp, D)) return rc;
+		}
+	}
+	if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, 1)) return rc;
+	if (int rc = hako_gpu_matmul(d->logits, d->xn, m.t_out, m.out_weight, nullptr, m.vocab, D)) return rc;
+	hipLaunchKernelGGL(argmax_kernel, dim3(kArgBlocks, d->n_seq), dim3(256), 0, stream(), d->logits, m.vocab, d->tok,
+	                   d->pos, d->ring, d->max_seq, d->nout, d->apart, d->mcnt);
+	HK_LAUNCHED("argmax");
+	return HAKO_GPU_OK;
+}
+
+int capture(hako_gpu_decoder *d) {
+	if (d->exec) return HAKO_GPU_OK;
+	HK_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeThreadLocal));
+	const int rc = enqueue_step(d);
+	hipGraph_t g = nullptr;
+	const hipError_t e = hipStreamEndCapture(stream(), &g);
+	if (rc) {
+		if (g) (void)hipGraphDestroy(g);
+		return rc;
+	}
+	if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+	d->graph = g;
+	HK_HIP(hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0));
+	return HAKO_GPU_OK;
+}
+
+int set_tokens(hako_gpu_decoder *d, const int *tokens) {
+	for (int s = 0; s < d->n_seq; s++)
+		if (tokens[s] < 0 || tokens[s] >= d->m.vocab)
+			return set_error(HAKO_GPU_EINVAL, "token %d of sequence %d outside the vocabulary", tokens[s], s);
+	HK_HIP(hipMemcpyAsync(d->tok, tokens, sizeof(int) * d->n_seq, hipMemcpyHostToDevice, stream()));
+	return HAKO_GPU_OK;
+}
+
+// positions must leave room for n more steps
+int check_room(hako_gpu_decoder *d, int n) {
+	std::vector<int> pos(d->n_seq);
+	HK_HIP(hipMemcpyAsync(pos.data(), d->pos, sizeof(int) * d->n_seq, hipMemcpyDeviceToHost, stream()));
+	HK_HIP(hipStreamSynchronize(stream()));
+	for (int s = 0; s < d->n_seq; s++)
+		if (pos[s] < 0 || pos[s] + n > d->max_seq)
+			return set_error(HAKO_GPU_EINVAL, "sequence %d at position %d has no room for %d steps (max_seq %d)", s,
+			                 pos[s], n, d->max_seq);
+	return HAKO_GPU_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hako_gpu_decoder **out) {
+	if (int rc = require_device()) return rc;
+	if (!m || !out || !m->blocks) return set_error(HAKO_GPU_EINVAL, "null model or output");
+	*out = nullptr;
+	if (n_seq != 1) return set_error(HAKO_GPU_EINVAL, "decoder supports one sequence per step (got %d)", n_seq);
+	if (m->n_layers <= 0 || m->n_heads <= 0 || m->n_kv_heads <= 0 || m->n_heads % m->n_kv_heads != 0 ||
+	    m->n_heads / m->n_kv_heads > kMaxG || (m->head_dim != 64 && m->head_dim != 128) ||
+	    m->d_model != m->n_heads * m->head_dim || m->d_model % kQK != 0 || m->ffn_dim % kQK != 0 || m->vocab <= 0 ||
+	    max_seq <= 0)
+		return set_error(HAKO_GPU_EINVAL,
+		                 "unsupported decoder shape: layers %d d_model %d heads %d/%d head_dim %d ffn %d vocab %d "
+		                 "max_seq %d",
+		                 m->n_layers, m->d_model, m->n_heads, m->n_kv_heads, m->head_dim, m->ffn_dim, m->vocab,
+		                 max_seq);
+	if (!known_type(m->t_embd) || !known_type(m->t_out) || !m->tok_embd || !m->out_weight || !m->out_norm)
+		return set_error(HAKO_GPU_ETYPE, "embedding / output types %d / %d", m->t_embd, m->t_out);
+	for (int l = 0; l < m->n_layers; l++) {
+		const hako_gpu_block &B = m->blocks[l];
+		const int ts[7] = {B.t_q, B.t_k, B.t_v, B.t_o, B.t_gate, B.t_up, B.t_down};
+		for (int t : ts)
+			if (!known_type(t)) return set_error(HAKO_GPU_ETYPE, "layer %d: unsupported tensor type %d", l, t);
+		if (!B.attn_norm || !B.ffn_norm || !B.wq || !B.wk || !B.wv || !B.wo || !B.gate || !B.up || !B.down)
+			return set_error(HAKO_GPU_EINVAL, "layer %d: missing tensor", l);
+	}
+	hako_gpu_decoder *d = new hako_gpu_decoder();
+	d->m = *m;
+	d->blocks.assign(m->blocks, m->blocks + m->n_layers);
+	d->m.blocks = nullptr;
+	d->n_seq = n_seq;
+	d->max_seq = max_seq;
+	d->max_chunks = (max_seq + kChunk - 1) / kChunk;
+	d->kv_dim = m->n_kv_heads * m->head_dim;
+	d->qkv_dim = m->d_model + 2 * d->kv_dim;
+	const int D = m->d_model, F = m->ffn_dim, HD = m->head_dim;
+	const size_t kvn = (size_t)n_seq * m->n_layers * max_seq * d->kv_dim;
+	int rc = 0;
+#define HK_ALLOC(ptr, bytes) \
+	if (!rc) rc = dalloc(d, (bytes), (void **)&(ptr))
+	HK_ALLOC(d->x, sizeof(float) * n_seq * D);
+	HK_ALLOC(d->xn, sizeof(float) * n_seq * D);
+	HK_ALLOC(d->qkv, sizeof(float) * n_seq * d->qkv_dim);
+	HK_ALLOC(d->att, sizeof(float) * n_seq * D);
+	HK_ALLOC(d->h, sizeof(float) * n_seq * F);
+	HK_ALLOC(d->g, sizeof(float) * n_seq * F);
+	HK_ALLOC(d->u, sizeof(float) * n_seq * F);
+	HK_ALLOC(d->tmp, sizeof(float) * n_seq * D);
+	HK_ALLOC(d->logits, sizeof(float) * n_seq * m->vocab);
+	HK_ALLOC(d->part, sizeof(float) * n_seq * m->n_kv_heads * d->max_chunks * kMaxG * (HD + 2));
+	HK_ALLOC(d->kc, sizeof(float) * kvn);
+	HK_ALLOC(d->vc, sizeof(float) * kvn);
+	HK_ALLOC(d->rope, sizeof(float2) * (size_t)max_seq * (HD / 2));
+	HK_ALLOC(d->apart, sizeof(float2) * n_seq * kArgBlocks);
+	HK_ALLOC(d->tok, sizeof(int) * n_seq);
+	HK_ALLOC(d->pos, sizeof(int) * n_seq);
+	HK_ALLOC(d->acnt, sizeof(int) * n_seq * m->n_kv_heads);
+	HK_ALLOC(d->mcnt, sizeof(int) * n_seq);
+	HK_ALLOC(d->ring, sizeof(int) * n_seq * max_seq);
+	HK_ALLOC(d->nout, sizeof(int) * n_seq);
+#undef HK_ALLOC
+	if (rc) {
+		hako_gpu_decoder_destroy(d);
+		return rc;
+	}
+	// rope table with the reference's expression (src/nn.c:31-41)
+	std::vector<float2> rope((size_t)max_seq * (HD / 2));
+	for (int p = 0; p < max_seq; p++)
+		for (int i = 0; i < HD / 2; i++) {
+			const float freq = powf(m->rope_theta, -((float)(2 * i) / (float)HD));
+			const float ang = (float)p * freq;
+			rope[(size_t)p * (HD / 2) + i] = make_float2(cosf(ang), sinf(ang));
+		}
+	hipError_t e = hipMemcpy(d->rope, rope.data(), sizeof(float2) * rope.size(), hipMemcpyHostToDevice);
+	if (e == hipSuccess) e = hipMemset(d->kc, 0, sizeof(float) * kvn);
+	if (e == hipSuccess) e = hipMemset(d->vc, 0, sizeof(float) * kvn);
+	if (e == hipSuccess) e = hipMemset(d->acnt, 0, sizeof(int) * n_seq * m->n_kv_heads);
+	if (e == hipSuccess) e = hipMemset(d->mcnt, 0, sizeof(int) * n_seq);
+	if (e == hipSuccess) e = hipMemset(d->pos, 0, sizeof(int) * n_seq);
+	if (e == hipSuccess) e = hipMemset(d->nout, 0, sizeof(int) * n_seq);
+	if (e == hipSuccess) e = hipDeviceSynchronize();
+	if (e != hipSuccess) {
+		hako_gpu_decoder_destroy(d);
+		return hip_fail(e, "decoder init", __FILE__, __LINE__);
+	}
+	*out = d;
+	return ok();
+}
+
+int hako_gpu_decoder_destroy(hako_gpu_decoder *d) {
+	if (!d) return ok();
+	if (stream()) (void)hipStreamSynchronize(stream());
+	if (d->exec) (void)hipGraphExecDestroy(d->exec);
+	if (d->graph) (void)hipGraphDestroy(d->graph);
+	for (void *p : d->allocs) (void)hipFree(p);
+	delete d;
+	return ok();
+}
+
+int hako_gpu_decoder_kv(hako_gpu_decoder *d, float **k_cache, float **v_cache) {
+	if (!d) return set_error(HAKO_GPU_EINVAL, "null decoder");
+	if (k_cache) *k_cache = d->kc;
+	if (v_cache) *v_cache = d->vc;
+	return ok();
+}
+
+int hako_gpu_decoder_set_pos(hako_gpu_decoder *d, const int *pos) {
+	if (!d || !pos) return set_error(HAKO_GPU_EINVAL, "null decoder or positions");
+	for (int s = 0; s < d->n_seq; s++)
+		if (pos[s] < 0 || pos[s] >= d->max_seq)
+			return set_error(HAKO_GPU_EINVAL, "position %d of sequence %d outside [0, %d)", pos[s], s, d->max_seq);
+	HK_HIP(hipMemcpyAsync(d->pos, pos, sizeof(int) * d->n_seq, hipMemcpyHostToDevice, stream()));
+	HK_HIP(hipStreamSynchronize(stream()));
+	return ok();
+}
+
+int hako_gpu_decoder_step(hako_gpu_decoder *d, const int *tokens, float *logits, int *next) {
+	if (!d || !tokens) return set_error(HAKO_GPU_EINVAL, "null decoder or tokens");
+	if (int rc = check_room(d, 1)) return rc;
+	if (int rc = set_tokens(d, tokens)) return rc;
+	if (int rc = enqueue_step(d)) return rc;
+	if (logits)
+		HK_HIP(hipMemcpyAsync(logits, d->logits, sizeof(float) * d->n_seq * d->m.vocab, hipMemcpyDeviceToHost,
+		                      stream()));
+	if (next) HK_HIP(hipMemcpyAsync(next, d->tok, sizeof(int) * d->n_seq, hipMemcpyDeviceToHost, stream()));
+	HK_HIP(hipStreamSynchronize(stream()));
+	return ok();
+}
+
+int hako_gpu_decoder_generate(hako_gpu_decoder *d, const int *tokens, int n, int *out) {
+	if (!d || !tokens || !out || n <= 0) return set_error(HAKO_GPU_EINVAL, "null argument or n <= 0");
+	if (int rc = check_room(d, n)) return rc;
+	if (int rc = set_tokens(d, tokens)) return rc;
+	HK_HIP(hipMemsetAsync(d->nout, 0, sizeof(int) * d->n_seq, stream()));
+	if (int rc = capture(d)) return rc;
+	for (int i = 0; i < n; i++) HK_HIP(hipGraphLaunch(d->exec, stream()));
+	std::vector<int> ring((size_t)d->n_seq * d->max_seq);
+	HK_HIP(hipMemcpyAsync(ring.data(), d->ring, sizeof(int) * ring.size(), hipMemcpyDeviceToHost, stream()));
+	HK_HIP(hipStreamSynchronize(stream()));
+	for (int i = 0; i < n; i++)
+		for (int s = 0; s < d->n_seq; s++) out[(size_t)i * d->n_seq + s] = ring[(size_t)s * d->max_seq + i];
+	return ok();
+}
+
+int hako_gpu_decoder_replay(hako_gpu_decoder *d, int n) {
+	if (!d || n < 0) return set_error(HAKO_GPU_EINVAL, "null decoder or n < 0");
+	if (int rc = check_room(d, n)) return rc;
+	if (int rc = capture(d)) return rc;
+	for (int i = 0; i < n; i++) HK_HIP(hipGraphLaunch(d->exec, stream()));
+	return ok();
+}
+
+}  // extern "C"

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
                                                                        const float *__restrict__ x,
                                                                        const float *__restrict__ bias,
                                                                        float *__restrict__ out, int n_out,
-                                                                       int n_in, int target) {
+                                                                       int n_in, int target, int acc_out) {
 	extern __shared__ float red_s[];   // [rows of this workgroup][parts]: partial row sums
 	const Q6Geom G = q6_geom(n_in, target);
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -204,18 +204,21 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 		if (sub < kQ6Depth && base + j < nit && row < r1) {
 			if (G.tpr > 1)
 				red_s[(row - r0) * G.tpr + part] = tot;
-			else if (bias)
+			else if (bias || acc_out)
 				red_s[row - r0] = tot;
 			else
 				out[row] = tot;
 		}
 	}
-	if (G.tpr > 1 || bias) {
+	// Rows with a bias or a residual to add, and split rows, finish here: a
+	// load of either inside the loop would wait for every weight load in flight.
+	if (G.tpr > 1 || bias || acc_out) {
 		__syncthreads();
 		for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
 			float v = 0.0f;
 			for (int p = 0; p < G.tpr; p++) v += red_s[r * G.tpr + p];
-			out[r0 + r] = bias ? v + bias[r0 + r] : v;
+			if (bias) v += bias[r0 + r];
+			out[r0 + r] = acc_out ? out[r0 + r] + v : v;
 		}
 	}
 }
@@ -230,9 +233,10 @@ void q6k_set_waves(int v) { g_q6_waves = v >= 8 ? 8 : 4; }
 
 }  // namespace hako
 
-extern "C" int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, const float *bias,
-                                 int n_out, int n_in) {
-	using namespace hako;
+namespace hako {
+
+// out = W x (+ bias), or out += W x (+ bias) when acc_out (a residual add).
+int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n_out, int n_in, bool acc_out) {
 	if (int rc = require_device()) return rc;
 	if (n_out <= 0 || n_in <= 0 || n_in % kQK != 0)
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV needs n_out > 0 and n_in %% 256 == 0 (got %d x %d)",
@@ -254,7 +258,14 @@ extern "C" int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, cons
 	const int rows_per_wg = (n_out + wgs - 1) / wgs;
 	const size_t lds = (size_t)rows_per_wg * G.tpr * sizeof(float);
 	hipLaunchKernelGGL(q6k_gemv_kernel, dim3(wgs), dim3(G.waves * kWave), lds, stream(), (const uint8_t *)w, x,
-	                   bias, out, n_out, n_in, g_q6_waves);
+	                   bias, out, n_out, n_in, g_q6_waves, acc_out ? 1 : 0);
 	HK_LAUNCHED("q6k_gemv");
 	return ok();
+}
+
+}  // namespace hako
+
+extern "C" int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, const float *bias,
+                                 int n_out, int n_in) {
+	return hako::q6k_gemv(out, w, x, bias, n_out, n_in, false);
 }

@@ -1,0 +1,91 @@
+/*
+ * hako_decode.h — device-resident Qwen2 decode step (C ABI).
+ *
+ * Replaces, for a whole token step, the reference's hakm_forward
+ * (src/model.c:93-165) with its greedy pick (src/sample.c:28-32): embedding
+ * row, then per layer rmsnorm, q/k/v projections with bias, NeoX rope,
+ * KV-cache append, GQA softmax attention, output projection and residual,
+ * rmsnorm, SwiGLU feed-forward and residual; final rmsnorm, lm_head, argmax.
+ * Weights stay where they are in HBM (e.g. inside an uploaded MLF2 mirror,
+ * include/hako_gpu.h); activations, KV caches and token ids stay on the
+ * device between steps, so a greedy loop needs no host round trip per token.
+ *
+ * Numerics follow the reference's formulas; its matmuls are the library's
+ * kernels (Q4_K x q8 with exact integer sums, Q6_K / F16 / F32 x fp32), and
+ * the rope angles come from a table computed on the host with the reference's
+ * own expression (src/nn.c:31-41). Plain C, no HIP types; every function
+ * returns 0 or a negative HAKO_GPU_E* code with hako_gpu_last_error() set.
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#pragma GCC visibility push(default)
+
+/* One transformer block (reference src/model.h:5-10): device addresses and
+ * HAKO_TYPE_* of each matrix (rows of n_in elements, src/nn.h:18-21); norms
+ * and biases are F32 (biases may be NULL). */
+typedef struct {
+	const float *attn_norm, *ffn_norm;
+	const void *wq, *wk, *wv, *wo;
+	const float *bq, *bk, *bv;
+	const void *gate, *up, *down;
+	int t_q, t_k, t_v, t_o, t_gate, t_up, t_down;
+} hako_gpu_block;
+
+/* A Qwen2 model (reference src/model.h:12-26, mlf2_header fields). `blocks`
+ * is read at create time only. out_weight may equal tok_embd (tied). */
+typedef struct {
+	int n_layers, d_model, n_heads, n_kv_heads, head_dim, ffn_dim, vocab;
+	float rope_theta, rms_eps;
+	const void *tok_embd;
+	int t_embd;
+	const float *out_norm;
+	const void *out_weight;
+	int t_out;
+	const hako_gpu_block *blocks;
+} hako_gpu_model;
+
+typedef struct hako_gpu_decoder hako_gpu_decoder;
+
+/* A decoder for n_seq independent sequences of up to max_seq positions each
+ * (KV caches, activations and the rope table are allocated here, once).
+ * Requires head_dim 64 or 128, n_heads % n_kv_heads == 0, d_model and
+ * ffn_dim multiples of 256 and n_seq == 1 (one sequence per step). */
+int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec);
+int hako_gpu_decoder_destroy(hako_gpu_decoder *dec);
+
+/* Device addresses of the fp32 KV caches, laid out as the reference's
+ * (src/model.c:71-72, 117-118) once per sequence:
+ * [n_seq][n_layers][max_seq][n_kv_heads*head_dim]. A caller may fill
+ * positions below the next write position directly (a prefilled context). */
+int hako_gpu_decoder_kv(hako_gpu_decoder *dec, float **k_cache, float **v_cache);
+
+/* Set the next write position of every sequence (hakm_ctx.pos); pos[n_seq]. */
+int hako_gpu_decoder_set_pos(hako_gpu_decoder *dec, const int *pos);
+
+/* One step for every sequence: tokens[n_seq] in (host); if logits is not NULL
+ * the fp32 logits [n_seq][vocab] are copied to it (host), and next[n_seq]
+ * (host, may be NULL) receives the greedy ids. Advances every position by
+ * one. Synchronous. */
+int hako_gpu_decoder_step(hako_gpu_decoder *dec, const int *tokens, float *logits, int *next);
+
+/* n greedy steps from tokens[n_seq]: out[n][n_seq] (host) receives the ids
+ * chosen at each step, each fed back as the next step's input on the device.
+ * The step is captured once as a HIP graph and replayed n times; one
+ * synchronization at the end. Positions advance by n. */
+int hako_gpu_decoder_generate(hako_gpu_decoder *dec, const int *tokens, int n, int *out);
+
+/* Replays the captured step n times from the current device state (no host
+ * transfer, no synchronization): the timed loop of a benchmark. */
+int hako_gpu_decoder_replay(hako_gpu_decoder *dec, int n);
+
+#pragma GCC visibility pop
+
+#ifdef __cplusplus
+}
+#endif

@@ -10,6 +10,7 @@
  * resolves every symbol it used.
  */
 #pragma once
+#include "hako_decode.h"
 #include "hako_mlf2.h"
 
 #ifdef __cplusplus
@@ -43,6 +44,14 @@ int hako_model_upload(const hakm_model *m);
 /* Forget m's HBM mirror; call before unmapping a model whose address range
  * may be reused by another. */
 int hako_model_release(const hakm_model *m);
+
+/* A device decoder (hako_decode.h) for mapped model m: the tensors
+ * hakm_ctx_new resolves (reference src/model.c:30-57) at their mirror
+ * addresses, the lm_head tied to token_embd when the header says so. One
+ * hako_gpu_decoder_step / _generate call then replaces hakm_forward
+ * (src/model.c:93-165) plus the greedy pick for every step. Returns 0 or a
+ * negative hako_gpu error code. */
+int hako_decoder_from_model(const hakm_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec);
 
 #ifdef __cplusplus
 }
