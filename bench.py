@@ -34,6 +34,8 @@ from hako_amd import synth  # noqa: E402
 
 METRIC = "Q4_K×q8 GEMV GB/s (% HBM peak) + decode tok/s, 3B/7B shapes, batch 1"
 HBM_PEAK_GBPS = 8000.0            # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0           # MI355X dense int8 matrix cores
+FP16_PEAK_TFLOPS = 2500.0         # MI355X dense fp16 matrix cores
 ROTATION_BYTES = 512 << 20        # > 256 MB Infinity Cache
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "q4k_gemv_11008x2048_traffic.json")
 
@@ -147,6 +149,91 @@ def cpu_baseline(seconds: float, seed: int) -> dict:
                       f"copies), {threads} threads (HAKM_THREADS), median {med * 1e3:.3f} ms/call"}
 
 
+def bench_decode(g, steps: int, cpu_steps: int, seed: int = 30) -> dict:
+    """Greedy decode of a Qwen2.5-3B-shaped model (36 layers, Q4_K_M mix, tied
+    Q6_K embedding, random weights) with the KV cache prefilled to 1024
+    positions of seeded N(0,1) keys and values: `steps` graph-replayed device
+    steps; the reference's own hakm_forward on the same file and cache timed
+    for `cpu_steps` tokens on the host cores."""
+    import tempfile
+    from hako_amd import mlf2
+    from hako_amd.decoder import Decoder
+    cfg, pos = mlf2.QWEN2_3B, 1024
+    max_seq = pos + steps + 8
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    fd, path = tempfile.mkstemp(suffix=".mlf2")
+    os.close(fd)
+    try:
+        info = mlf2.write_qwen2(path, cfg, seed)
+        kv = np.random.default_rng(seed + 1).standard_normal((2, cfg.n_layers, pos, kvd)).astype(np.float32)
+        dec = Decoder(g, path, n_seq=1, max_seq=max_seq)
+        try:
+            k, v = dec.kv()
+            for l in range(cfg.n_layers):
+                g.h2d(k + dec.kv_offset(0, l, 0), kv[0, l])
+                g.h2d(v + dec.kv_offset(0, l, 0), kv[1, l])
+            dec.set_pos(pos)
+            dec.generate(9, 4)          # capture and warm
+            g.sync()
+            dec.set_pos(pos)
+            e0, e1 = g.event(), g.event()
+            g.record(e0)
+            dec.replay(steps)
+            g.record(e1)
+            ms = g.elapsed_ms(e0, e1)
+        finally:
+            dec.close()
+        weight_bytes = sum(e[4] for e in info.values())
+        kv_bytes = cfg.n_layers * 2 * kvd * 4 * (pos + 1 + steps // 2)
+        per_tok = weight_bytes + kv_bytes
+        us = ms * 1e3 / steps
+        res = {"workload": "Qwen2.5-3B-shaped greedy decode (36 layers, Q4_K attn/gate/up, Q6_K down and tied "
+                           "embedding), batch 1, KV cache from position 1024",
+               "steps": steps, "us_per_token": round(us, 2), "tok_per_s": round(1e6 / us, 1),
+               "bytes_per_token": per_tok, "gbps": round(per_tok / (us * 1e-6) / 1e9, 1),
+               "hbm_frac": round(per_tok / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+               "timing": "HIP graph of one step replayed K times between two HIP events"}
+        if cpu_steps > 0:
+            from oracle.hako_oracle import REF_LIB, RefLib, prefilled_greedy
+            threads = min(os.cpu_count() or 1, 16)
+            ref = RefLib(REF_LIB, threads=threads)
+            times = []
+            prefilled_greedy(ref.lib, path, kv, pos, 9, cpu_steps + 1, cfg.vocab, max_seq, times)
+            med = float(np.median(times[1:]))
+            res["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads,
+                                   "kind": "reference",
+                                   "sample": f"{cpu_steps} hakm_forward steps (after one warm-up) of the reference "
+                                             f"on the same model file and cache, {threads} threads, median "
+                                             f"{med * 1e3:.1f} ms/token"}
+        return res
+    finally:
+        os.unlink(path)
+
+
+def bench_prefill(g, launches: int) -> dict:
+    """The 7B prefill matmuls: Q4_K 18944x3584 x 512 tokens (q8_32 quantize +
+    int8-MFMA GEMM) and Q6_K 3584x18944 x 512 tokens (fp16-MFMA GEMM)."""
+    out = {}
+    for name, qt, m, n_out, n_in in (("q4k_7b_ffn_up_512x18944x3584", synth.TYPE_Q4_K, 512, 18944, 3584),
+                                     ("q6k_7b_ffn_down_512x3584x18944", synth.TYPE_Q6_K, 512, 3584, 18944)):
+        rng = np.random.default_rng(n_out)
+        w = synth.weight(rng, qt, n_out, n_in)
+        x = rng.standard_normal((m, n_in)).astype(np.float32)
+        dw, dx, dy = g.upload(w), g.upload(x), g.alloc(m * n_out * 4)
+        g.matmul_batch(dy, dx, qt, dw, None, m, n_out, n_in)   # sizes the workspace outside the capture
+        g.sync()
+        r = _time_launches(g, lambda k: g.matmul_batch(dy, dx, qt, dw, None, m, n_out, n_in), launches, 3, False)
+        for b in (dw, dx, dy):
+            b.free()
+        ops = 2.0 * m * n_out * n_in
+        tops = ops / (r["us_per_launch"] * 1e-6) / 1e12
+        peak = INT8_PEAK_TOPS if qt == synth.TYPE_Q4_K else FP16_PEAK_TFLOPS
+        out[name] = {"us_per_launch": round(r["us_per_launch"], 2), "tops": round(tops, 1),
+                     "peak": peak, "frac": round(tops / peak, 4),
+                     "unit": "TOPS (int8)" if qt == synth.TYPE_Q4_K else "TFLOP/s (fp16 matrix cores)"}
+    return out
+
+
 def read_traffic():
     try:
         with open(TRAFFIC_FILE) as f:
@@ -172,12 +259,16 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy"],
                     help="run one workload and print its timing only (profiling runs)")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
+    ap.add_argument("--decode-steps", type=int, default=100)
+    ap.add_argument("--cpu-decode-steps", type=int, default=3)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -212,6 +303,17 @@ def main():
             extra[name] = {"us_per_launch": round(r["us_per_launch"], 3), "gbps": round(r["gbps"], 1),
                            "hbm_frac": round(r["gbps"] / HBM_PEAK_GBPS, 4),
                            "single_launch_us": round(r["single_launch_us"], 3)}
+    decode = None
+    if not args.no_decode:
+        decode = bench_decode(g, args.decode_steps, 0 if args.no_cpu else args.cpu_decode_steps)
+        log(f"decode: {decode['us_per_token']:.1f} us/token, {decode['tok_per_s']:.1f} tok/s, "
+            f"{decode['gbps']:.0f} GB/s" + (f"; cpu {decode['cpu_baseline']['value']:.2f} tok/s"
+                                          if 'cpu_baseline' in decode else ""))
+    prefill = None
+    if not args.no_prefill:
+        prefill = bench_prefill(g, 30)
+        for k, v in prefill.items():
+            log(f"{k}: {v['us_per_launch']:.1f} us, {v['tops']:.1f} {v['unit']}")
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds, seed=2)
@@ -233,6 +335,8 @@ def main():
         "cpu_baseline": cpu,
         "single_launch_us": round(head["single_launch_us"], 3),
         "extra": extra,
+        "decode": decode,
+        "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
 

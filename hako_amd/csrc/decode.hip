@@ -456,7 +456,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	if (!last_s) return;
 	__threadfence();
 
-	// 6. merge the chunks: M, L per head (wave w: heads w, w+4), then the sums
+	// 6. merge the chunks: M, L and the weights e^(m_c - M)/L per head (wave w:
+	//    heads w, w+4; up to 64 chunks at a time in LDS, reusing s_s), then
+	//    the weighted sums with every chunk's load issued before any is used
 	const float *grp = part + ((size_t)(sq * KVH + kvh) * max_chunks) * kMaxG * REC;
 #pragma unroll
 	for (int h = 0; h < kMaxG / 4; h++) {
@@ -473,31 +475,44 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 			lsum = wave_sum(lsum);
 			if (lane == 0) {
 				ml_s[g][0] = mx;
-				ml_s[g][1] = lsum;
+				ml_s[g][1] = 1.0f / lsum;
 			}
 		}
 	}
 	__syncthreads();
-	for (int t = tid; t < G * HD; t += 256) {
-		const int g = t / HD, d = t - g * HD;
-		const float mx = ml_s[g][0];
-		float acc = 0.0f;
-		int cc = 0;
-		for (; cc + 4 <= nact; cc += 4) {
-			const float *r0 = grp + ((size_t)cc * kMaxG + g) * REC;
-			const float *r1 = r0 + kMaxG * REC, *r2 = r1 + kMaxG * REC, *r3 = r2 + kMaxG * REC;
-			const float o0 = r0[d], o1 = r1[d], o2 = r2[d], o3 = r3[d];
-			const float m0 = r0[HD], m1 = r1[HD], m2 = r2[HD], m3 = r3[HD];
-			acc = __builtin_fmaf(o0, expf(m0 - mx), acc);
-			acc = __builtin_fmaf(o1, expf(m1 - mx), acc);
-			acc = __builtin_fmaf(o2, expf(m2 - mx), acc);
-			acc = __builtin_fmaf(o3, expf(m3 - mx), acc);
+	constexpr int PER = kMaxG * HD / 256;   // (head, dim) outputs per thread
+	float acc[PER];
+#pragma unroll
+	for (int k = 0; k < PER; k++) acc[k] = 0.0f;
+	for (int c0 = 0; c0 < nact; c0 += kChunk) {
+		const int nc = min(kChunk, nact - c0);
+		__syncthreads();   // s_s of the previous batch is consumed
+		for (int t = tid; t < G * kChunk; t += 256) {
+			const int g = t / kChunk, cc = t - g * kChunk;
+			if (cc < nc) s_s[g][cc] = expf(grp[((size_t)(c0 + cc) * kMaxG + g) * REC + HD] - ml_s[g][0]) * ml_s[g][1];
 		}
-		for (; cc < nact; cc++) {
-			const float *r = grp + ((size_t)cc * kMaxG + g) * REC;
-			acc = __builtin_fmaf(r[d], expf(r[HD] - mx), acc);
+		__syncthreads();
+#pragma unroll
+		for (int k = 0; k < PER; k++) {
+			const int t = tid + 256 * k, g = t / HD, d = t - g * HD;
+			if (g < G) {
+				const float *r = grp + ((size_t)c0 * kMaxG + g) * REC + d;
+				int cc = 0;
+				for (; cc + 8 <= nc; cc += 8) {
+					float o[8];
+#pragma unroll
+					for (int j = 0; j < 8; j++) o[j] = r[(size_t)(cc + j) * kMaxG * REC];
+#pragma unroll
+					for (int j = 0; j < 8; j++) acc[k] = __builtin_fmaf(o[j], s_s[g][cc + j], acc[k]);
+				}
+				for (; cc < nc; cc++) acc[k] = __builtin_fmaf(r[(size_t)cc * kMaxG * REC], s_s[g][cc], acc[k]);
+			}
 		}
-		att[(size_t)sq * D + (size_t)(kvh * G + g) * HD + d] = acc / ml_s[g][1];
+	}
+#pragma unroll
+	for (int k = 0; k < PER; k++) {
+		const int t = tid + 256 * k, g = t / HD, d = t - g * HD;
+		if (g < G) att[(size_t)sq * D + (size_t)(kvh * G + g) * HD + d] = acc[k];
 	}
 	if (tid == 0) atomicExch(&cnt[sq * KVH + kvh], 0);   // ready for the next step
 }

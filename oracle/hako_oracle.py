@@ -13,6 +13,7 @@ CPU-baseline leg, never by product code.
 from __future__ import annotations
 
 import ctypes as C
+import time
 import os
 
 import numpy as np
@@ -194,3 +195,46 @@ class RefLib:
         self.lib.matmul(_p(out), _p(np.ascontiguousarray(x, np.float32)), C.byref(m), C.byref(t),
                         _p(bias), n_out, n_in)
         return out
+
+
+class HakmCtx(C.Structure):
+    """The reference's hakm_ctx (src/model.h:12-26), for tests that fill its
+    KV cache and position directly (a prefilled context)."""
+    _fields_ = [("model", C.c_uint8 * 168), ("layers", _vp), ("tok_embd", _vp), ("out_norm", _vp),
+                ("out_weight", _vp), ("d_model", _i), ("n_heads", _i), ("n_kv_heads", _i), ("head_dim", _i),
+                ("kv_dim", _i), ("ffn_dim", _i), ("n_layers", _i), ("vocab", _i), ("rope_theta", C.c_float),
+                ("rms_eps", C.c_float), ("max_seq", _i), ("pos", _i), ("k_cache", _vp), ("v_cache", _vp),
+                ("xb", _vp), ("xn", _vp), ("q", _vp), ("k", _vp), ("v", _vp), ("att_out", _vp),
+                ("gate_buf", _vp), ("up_buf", _vp), ("deq", _vp), ("logits", _vp)]
+
+
+assert C.sizeof(HakmCtx) == 344
+
+
+def prefilled_greedy(lib: C.CDLL, path: str, kv: np.ndarray, pos: int, start: int, steps: int, vocab: int,
+                     max_seq: int, times: list | None = None):
+    """Greedy decode through the reference's model.h API after writing the
+    caches directly: kv[0] / kv[1] are [n_layers][pos][kv_dim] keys / values
+    placed at positions 0..pos-1, and ctx.pos = pos. `times`, when given,
+    receives the wall time of each hakm_forward call (src/model.c:93)."""
+    ctx = lib.hakm_ctx_new(path.encode(), max_seq)
+    assert ctx, f"hakm_ctx_new({path}) failed"
+    toks, logits = [start], []
+    try:
+        c = HakmCtx.from_address(ctx)
+        n_layers, kvd = kv.shape[1], kv.shape[3]
+        for which, ptr in ((0, c.k_cache), (1, c.v_cache)):
+            cache = np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_float)), shape=(n_layers, max_seq, kvd))
+            cache[:, :pos, :] = kv[which]
+        c.pos = pos
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            p = lib.hakm_forward(ctx, toks[-1])
+            if times is not None:
+                times.append(time.perf_counter() - t0)
+            lg = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(vocab,)).copy()
+            logits.append(lg)
+            toks.append(int(np.argmax(lg)))
+    finally:
+        lib.hakm_ctx_free(ctx)
+    return toks[1:], np.stack(logits)
