@@ -262,7 +262,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy"],
+    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "decode", "prefill"],
                     help="run one workload and print its timing only (profiling runs)")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     ap.add_argument("--decode-steps", type=int, default=100)
@@ -280,6 +280,10 @@ def main():
     info = g.info()
     log(f"device {info.name.decode()} CUs={info.compute_units} HBM={info.hbm_bytes / 2**30:.0f} GiB")
 
+    if args.only in ("decode", "prefill"):
+        r = bench_decode(g, args.decode_steps, 0) if args.only == "decode" else bench_prefill(g, 30)
+        print(json.dumps(r), flush=True)
+        return
     if args.only:
         if args.only == "copy":
             r = bench_copy(g, 64 << 20, args.steps, args.warmup, args.eager)
