@@ -30,6 +30,7 @@
 #include "hako_dev.h"
 #include "hako_rt.h"
 #include "q4k_dev.h"
+#include "skinny.h"
 
 namespace hako {
 
@@ -111,6 +112,55 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ h, co
                                                        const float *__restrict__ u, int n) {
 	const int i = blockIdx.x * 256 + threadIdx.x;
 	if (i < n) h[i] = silu(g[i]) * u[i];
+}
+
+// Row r of x (n floats): rmsnorm with weight w (when w is not null), then
+// q8_32 into xq[r][n], xs[r][n/32] — the activation of the batched Q4_K
+// matmuls. One workgroup per row; n <= 4096 (4 quads per thread).
+constexpr int kNqPer = 4;
+__global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                         float eps, int8_t *__restrict__ xq, float *__restrict__ xs,
+                                                         int n) {
+	__shared__ float red[4];
+	const float *xr = x + (size_t)blockIdx.x * n;
+	float4 v[kNqPer], wv[kNqPer];
+#pragma unroll
+	for (int k = 0; k < kNqPer; k++) {
+		const int e = min((int)(threadIdx.x + 256 * k) * 4, n - 4);
+		v[k] = *(const float4 *)(xr + e);
+		wv[k] = w ? *(const float4 *)(w + e) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+	}
+	if (w) {
+		float ss = 0.0f;
+#pragma unroll
+		for (int k = 0; k < kNqPer; k++) {
+			if ((int)(threadIdx.x + 256 * k) * 4 < n) {
+				ss = __builtin_fmaf(v[k].x, v[k].x, ss);
+				ss = __builtin_fmaf(v[k].y, v[k].y, ss);
+				ss = __builtin_fmaf(v[k].z, v[k].z, ss);
+				ss = __builtin_fmaf(v[k].w, v[k].w, ss);
+			}
+		}
+		ss = block_sum256(ss, red);
+		const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+		for (int k = 0; k < kNqPer; k++) {
+			v[k].x = v[k].x * scale * wv[k].x;
+			v[k].y = v[k].y * scale * wv[k].y;
+			v[k].z = v[k].z * scale * wv[k].z;
+			v[k].w = v[k].w * scale * wv[k].w;
+		}
+	}
+#pragma unroll
+	for (int k = 0; k < kNqPer; k++) {
+		const int e = (threadIdx.x + 256 * k) * 4;
+		float sc;
+		const uint32_t packed = q8_quant4(v[k], sc);
+		if (e < n) {
+			*(uint32_t *)(xq + (size_t)blockIdx.x * n + e) = packed;
+			if ((threadIdx.x & 7) == 0) xs[(size_t)blockIdx.x * (n >> 5) + (e >> 5)] = sc;
+		}
+	}
 }
 
 // ── fused Q4_K GEMV of the decode step ──
@@ -618,6 +668,11 @@ struct hako_gpu_decoder {
 	      *tmp = nullptr, *logits = nullptr, *part = nullptr, *kc = nullptr, *vc = nullptr;
 	float2 *rope = nullptr, *apart = nullptr;
 	int *tok = nullptr, *pos = nullptr, *acnt = nullptr, *mcnt = nullptr, *ring = nullptr, *nout = nullptr;
+	// batched steps (n_seq > 1): q8 and fp16 hi/lo activations, split-K state
+	int8_t *xq = nullptr;
+	float *xs = nullptr, *esc = nullptr, *skpart = nullptr;
+	_Float16 *xh = nullptr, *xl = nullptr;
+	int *skcnt = nullptr;
 	std::vector<void *> allocs;
 	hipGraphExec_t exec = nullptr;
 	hipGraph_t graph = nullptr;
@@ -671,8 +726,97 @@ int add(float *x, const float *y, int n) {
 	return HAKO_GPU_OK;
 }
 
+int rmsnorm_q8(hako_gpu_decoder *d, const float *x, const float *w, int n) {
+	hipLaunchKernelGGL(rmsnorm_q8_kernel, dim3(d->n_seq), dim3(256), 0, stream(), x, w, d->m.rms_eps, d->xq, d->xs, n);
+	HK_LAUNCHED("rmsnorm_q8");
+	return HAKO_GPU_OK;
+}
+
+// The weight types the batched step runs (the Q4_K_M mix): Q4_K q/k/v/o/
+// gate/up, Q6_K down, Q4_K or Q6_K lm_head; d_model, ffn_dim <= 4096 /
+// any, kv_dim a multiple of 16.
+bool batched_ok(const hako_gpu_model &m, const std::vector<hako_gpu_block> &blocks, int kv_dim) {
+	if (m.d_model > kSkMaxQ4In || kv_dim % 16 || m.d_model % 16) return false;
+	if (m.t_out != HAKO_TYPE_Q4_K && m.t_out != HAKO_TYPE_Q6_K) return false;
+	for (const hako_gpu_block &B : blocks)
+		if (B.t_q != HAKO_TYPE_Q4_K || B.t_k != HAKO_TYPE_Q4_K || B.t_v != HAKO_TYPE_Q4_K || B.t_o != HAKO_TYPE_Q4_K ||
+		    B.t_gate != HAKO_TYPE_Q4_K || B.t_up != HAKO_TYPE_Q4_K || B.t_down != HAKO_TYPE_Q6_K)
+			return false;
+	return true;
+}
+
+// One step of n_seq > 1 sequences: every matmul a skinny MFMA GEMM that
+// streams the weights once for all sequences.
+int enqueue_batched_step(hako_gpu_decoder *d) {
+	const hako_gpu_model &m = d->m;
+	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, HD = m.head_dim, M = d->n_seq;
+	hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
+	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
+	HK_LAUNCHED("embed");
+	const float scale = 1.0f / sqrtf((float)HD);
+	const size_t kv_seq_stride = (size_t)m.n_layers * d->max_seq * KV;
+	for (int l = 0; l < m.n_layers; l++) {
+		const hako_gpu_block &B = d->blocks[l];
+		// 1. q, k, v for every sequence: rows [q | k | v] of qkv[t][D + 2KV]
+		if (int rc = rmsnorm_q8(d, d->x, B.attn_norm, D)) return rc;
+		SkSegs s{};
+		s.n = 3;
+		s.s[0] = {(const uint8_t *)B.wq, B.bq, d->qkv, 0, D, d->qkv_dim};
+		s.s[1] = {(const uint8_t *)B.wk, B.bk, d->qkv + D, D, KV, d->qkv_dim};
+		s.s[2] = {(const uint8_t *)B.wv, B.bv, d->qkv + D + KV, D + KV, KV, d->qkv_dim};
+		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, D + 2 * KV)) return rc;
+		// 2. attention, one grid over every sequence
+		float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
+		const dim3 ag(d->max_chunks, m.n_kv_heads, M);
+		if (HD == 128)
+			hipLaunchKernelGGL(attn_kernel<128>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride,
+			                   d->qkv_dim, scale);
+		else
+			hipLaunchKernelGGL(attn_kernel<64>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride,
+			                   d->qkv_dim, scale);
+		HK_LAUNCHED("attention");
+		// 3. output projection added into the residual stream
+		if (int rc = rmsnorm_q8(d, d->att, nullptr, D)) return rc;
+		s = SkSegs{};
+		s.n = 1;
+		s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D, D};
+		if (int rc = q4k_skinny(s, kSkAdd, d->xq, d->xs, M, D, D)) return rc;
+		// 4. gate, up, SwiGLU
+		if (int rc = rmsnorm_q8(d, d->x, B.ffn_norm, D)) return rc;
+		s = SkSegs{};
+		s.n = 2;
+		s.s[0] = {(const uint8_t *)B.gate, nullptr, d->h, 0, F, F};
+		s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, 0, F, F};
+		if (int rc = q4k_skinny(s, kSkSwiGLU, d->xq, d->xs, M, D, 2 * F)) return rc;
+		// 5. down projection added into the residual stream
+		if (int rc = f16_split(d->h, d->xh, d->xl, d->esc, M, F)) return rc;
+		s = SkSegs{};
+		s.n = 1;
+		s.s[0] = {(const uint8_t *)B.down, nullptr, d->x, 0, D, D};
+		if (int rc = q6k_skinny(s, kSkAdd, d->xh, d->xl, d->esc, M, F, D, d->skpart, d->skcnt)) return rc;
+	}
+	SkSegs s{};
+	s.n = 1;
+	s.s[0] = {(const uint8_t *)m.out_weight, nullptr, d->logits, 0, m.vocab, m.vocab};
+	if (m.t_out == HAKO_TYPE_Q4_K) {
+		if (int rc = rmsnorm_q8(d, d->x, m.out_norm, D)) return rc;
+		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, m.vocab)) return rc;
+	} else {
+		if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, M)) return rc;
+		if (int rc = f16_split(d->xn, d->xh, d->xl, d->esc, M, D)) return rc;
+		if (int rc = q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, D, m.vocab, d->skpart, d->skcnt)) return rc;
+	}
+	hipLaunchKernelGGL(argmax_kernel, dim3(kArgBlocks, M), dim3(256), 0, stream(), d->logits, m.vocab, d->tok, d->pos,
+	                   d->ring, d->max_seq, d->nout, d->apart, d->mcnt);
+	HK_LAUNCHED("argmax");
+	return HAKO_GPU_OK;
+}
+
 // One decode step on the library stream (n_seq == 1).
 int enqueue_step(hako_gpu_decoder *d) {
+	if (d->n_seq > 1) return enqueue_batched_step(d);
 	const hako_gpu_model &m = d->m;
 	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, HD = m.head_dim;
 	hipLaunchKernelGGL(embed_kernel, dim3(d->n_seq), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
@@ -795,7 +939,8 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	if (int rc = require_device()) return rc;
 	if (!m || !out || !m->blocks) return set_error(HAKO_GPU_EINVAL, "null model or output");
 	*out = nullptr;
-	if (n_seq != 1) return set_error(HAKO_GPU_EINVAL, "decoder supports one sequence per step (got %d)", n_seq);
+	if (n_seq < 1 || n_seq > kSkMaxTokens)
+		return set_error(HAKO_GPU_EINVAL, "decoder runs 1 to %d sequences per step (got %d)", kSkMaxTokens, n_seq);
 	if (m->n_layers <= 0 || m->n_heads <= 0 || m->n_kv_heads <= 0 || m->n_heads % m->n_kv_heads != 0 ||
 	    m->n_heads / m->n_kv_heads > kMaxG || (m->head_dim != 64 && m->head_dim != 128) ||
 	    m->d_model != m->n_heads * m->head_dim || m->d_model % kQK != 0 || m->ffn_dim % kQK != 0 || m->vocab <= 0 ||
@@ -818,6 +963,13 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	hako_gpu_decoder *d = new hako_gpu_decoder();
 	d->m = *m;
 	d->blocks.assign(m->blocks, m->blocks + m->n_layers);
+	if (n_seq > 1 && !batched_ok(d->m, d->blocks, m->n_kv_heads * m->head_dim)) {
+		delete d;
+		return set_error(HAKO_GPU_ETYPE,
+		                 "batched decode (n_seq > 1) runs the Q4_K_M mix (Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or "
+		                 "Q6_K output) with d_model <= %d",
+		                 kSkMaxQ4In);
+	}
 	d->m.blocks = nullptr;
 	d->n_seq = n_seq;
 	d->max_seq = max_seq;
@@ -849,6 +1001,19 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	HK_ALLOC(d->mcnt, sizeof(int) * n_seq);
 	HK_ALLOC(d->ring, sizeof(int) * n_seq * max_seq);
 	HK_ALLOC(d->nout, sizeof(int) * n_seq);
+	const int DF = F > D ? F : D;
+	size_t skpart = q6k_skinny_part_floats(F, D), sk2 = q6k_skinny_part_floats(D, m->vocab);
+	skpart = skpart > sk2 ? skpart : sk2;
+	const int sktiles = (m->vocab > D ? m->vocab : D) / 64 + 1;
+	if (n_seq > 1) {
+		HK_ALLOC(d->xq, (size_t)n_seq * D);
+		HK_ALLOC(d->xs, sizeof(float) * n_seq * (D / 32));
+		HK_ALLOC(d->xh, sizeof(_Float16) * n_seq * DF);
+		HK_ALLOC(d->xl, sizeof(_Float16) * n_seq * DF);
+		HK_ALLOC(d->esc, sizeof(float) * n_seq);
+		HK_ALLOC(d->skpart, sizeof(float) * (skpart ? skpart : 1));
+		HK_ALLOC(d->skcnt, sizeof(int) * sktiles);
+	}
 #undef HK_ALLOC
 	if (rc) {
 		hako_gpu_decoder_destroy(d);
@@ -869,6 +1034,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	if (e == hipSuccess) e = hipMemset(d->mcnt, 0, sizeof(int) * n_seq);
 	if (e == hipSuccess) e = hipMemset(d->pos, 0, sizeof(int) * n_seq);
 	if (e == hipSuccess) e = hipMemset(d->nout, 0, sizeof(int) * n_seq);
+	if (e == hipSuccess && d->skcnt) e = hipMemset(d->skcnt, 0, sizeof(int) * sktiles);
 	if (e == hipSuccess) e = hipDeviceSynchronize();
 	if (e != hipSuccess) {
 		hako_gpu_decoder_destroy(d);

@@ -36,6 +36,7 @@
 // activations then stay in that XCD's L2.
 #include "hako_dev.h"
 #include "hako_rt.h"
+#include "skinny.h"
 
 namespace hako {
 namespace {
@@ -209,19 +210,31 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const uint8_t *__restrict
 
 // Token row t of x (K floats): s = 2^-e with max|x_t| in [2^e, 2^(e+1)),
 // hi = fp16(x*s), lo = fp16(x*s - hi), esc[t] = 2^e. The scaling is exact,
-// and x*s - hi is exact in fp32.
-__global__ __launch_bounds__(kGT) void f16_split_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
-                                                        _Float16 *__restrict__ xl, float *__restrict__ esc,
-                                                        int K) {
-	__shared__ float red[kGT / kWave];
+// and x*s - hi is exact in fp32. 1024 threads per row; up to kSplitPer
+// float4 per thread are loaded once, all at the start, and kept in
+// registers for both passes (rows longer than that run the tail from memory).
+constexpr int kSplitT = 1024, kSplitPer = 8;
+__global__ __launch_bounds__(kSplitT) void f16_split_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
+                                                            _Float16 *__restrict__ xl, float *__restrict__ esc,
+                                                            int K) {
+	__shared__ float red[kSplitT / kWave];
 	const size_t base = (size_t)blockIdx.x * K;
 	const float *xr = x + base;
-	float a = 0.0f;
-	for (int i = threadIdx.x * 4; i < K; i += kGT * 4) {
-		const float4 v = *(const float4 *)(xr + i);
-		a = __builtin_fmaxf(a, __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
-		                                       __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
+	float4 v[kSplitPer];
+#pragma unroll
+	for (int u = 0; u < kSplitPer; u++) {
+		const int i = (threadIdx.x + kSplitT * u) * 4;
+		v[u] = *(const float4 *)(xr + min(i, K - 4));
 	}
+	auto amax4 = [](float4 q) {
+		return __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(q.x), __builtin_fabsf(q.y)),
+		                       __builtin_fmaxf(__builtin_fabsf(q.z), __builtin_fabsf(q.w)));
+	};
+	float a = 0.0f;
+#pragma unroll
+	for (int u = 0; u < kSplitPer; u++) a = __builtin_fmaxf(a, amax4(v[u]));   // clamped repeats are harmless
+	for (int i = (threadIdx.x + kSplitT * kSplitPer) * 4; i < K; i += kSplitT * 4)
+		a = __builtin_fmaxf(a, amax4(*(const float4 *)(xr + i)));
 	a = __builtin_fmaxf(a, dpp_f<kDppQuadSwap1>(a));
 	a = __builtin_fmaxf(a, dpp_f<kDppQuadSwap2>(a));
 	a = __builtin_fmaxf(a, dpp_f<kDppHalfMirror>(a));
@@ -230,7 +243,9 @@ __global__ __launch_bounds__(kGT) void f16_split_kernel(const float *__restrict_
 	a = __builtin_fmaxf(a, __shfl_xor(a, 32));
 	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
 	__syncthreads();
-	a = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+	a = 0.0f;
+#pragma unroll
+	for (int w = 0; w < kSplitT / kWave; w++) a = __builtin_fmaxf(a, red[w]);
 	int e = 0;
 	if (a > 0.0f && __builtin_isfinite(a)) {
 		// exponent of a normal a; subnormal rows clamp to -126, which keeps 2^-e
@@ -240,16 +255,24 @@ __global__ __launch_bounds__(kGT) void f16_split_kernel(const float *__restrict_
 	}
 	const float s = __builtin_ldexpf(1.0f, -e);
 	if (threadIdx.x == 0) esc[blockIdx.x] = __builtin_ldexpf(1.0f, e);
-	for (int i = threadIdx.x * 4; i < K; i += kGT * 4) {
-		const float4 v = *(const float4 *)(xr + i);
-		const float f[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
+	auto put = [&](int i, float4 q) {
+		const float f[4] = {q.x * s, q.y * s, q.z * s, q.w * s};
+		typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+		v4h_t h, l;
 #pragma unroll
-		for (int j = 0; j < 4; j++) {
-			const _Float16 h = (_Float16)f[j];
-			xh[base + i + j] = h;
-			xl[base + i + j] = (_Float16)(f[j] - (float)h);
+		for (int k = 0; k < 4; k++) {
+			h[k] = (_Float16)f[k];
+			l[k] = (_Float16)(f[k] - (float)h[k]);
 		}
+		*(v4h_t *)(xh + base + i) = h;
+		*(v4h_t *)(xl + base + i) = l;
+	};
+#pragma unroll
+	for (int u = 0; u < kSplitPer; u++) {
+		const int i = (threadIdx.x + kSplitT * u) * 4;
+		if (i < K) put(i, v[u]);
 	}
+	for (int i = (threadIdx.x + kSplitT * kSplitPer) * 4; i < K; i += kSplitT * 4) put(i, *(const float4 *)(xr + i));
 }
 
 // Two of the 6-bit values in `v` (bytes picked by the v_perm selector `sel`
@@ -384,6 +407,31 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 	}
 }
 
+// Split-K counters and partials of the skinny Q6_K kernel in library
+// workspace slot 5: counters first (one int per 64-row tile), zeroed when the
+// slot is (re)allocated or the counter region grows, and left zero by every
+// launch, so calls captured in a graph need no clearing.
+int skinny_split_workspace(int n_in, int n_out, float **part, int **cnt) {
+	*part = nullptr;
+	*cnt = nullptr;
+	const size_t pf = q6k_skinny_part_floats(n_in, n_out);
+	if (!pf) return HAKO_GPU_OK;
+	const size_t tiles = (size_t)(n_out + 63) / 64;
+	const size_t cnt_bytes = (tiles * 4 + 255) & ~(size_t)255;
+	static void *zero_base = nullptr;
+	static size_t zero_bytes = 0;
+	void *ws = nullptr;
+	if (int rc = workspace(5, cnt_bytes + pf * 4, &ws)) return rc;
+	if (ws != zero_base || zero_bytes < cnt_bytes) {
+		HK_HIP(hipMemsetAsync(ws, 0, cnt_bytes, stream()));
+		zero_base = ws;
+		zero_bytes = cnt_bytes;
+	}
+	*cnt = (int *)ws;
+	*part = (float *)((uint8_t *)ws + cnt_bytes);
+	return HAKO_GPU_OK;
+}
+
 int gemm_grid(int M, int N) {
 	const int tiles = ((M + kTM - 1) / kTM) * ((N + kTN - 1) / kTN);
 	return kXcds * ((tiles + kXcds - 1) / kXcds);
@@ -407,10 +455,23 @@ int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const f
 	if (int rc = check_gemm("Q4_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ4Bytes, w)) return rc;
 	if (((uintptr_t)w & 15) || ((uintptr_t)xq & 15) || ((uintptr_t)xs & 3))
 		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM needs w and xq 16-byte aligned");
+	if (m <= kSkMaxTokens && n_in <= kSkMaxQ4In) {   // a few tokens: the skinny kernel
+		SkSegs segs{};
+		segs.n = 1;
+		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
+		if (int rc = q4k_skinny(segs, kSkStore, xq, xs, m, n_in, n_out)) return rc;
+		return ok();
+	}
 	hipLaunchKernelGGL(q4k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
 	                   xq, xs, bias, y, m, n_out, n_in);
 	HK_LAUNCHED("q4k_gemm");
 	return ok();
+}
+
+int f16_split(const float *x, _Float16 *xh, _Float16 *xl, float *esc, int m, int n) {
+	hipLaunchKernelGGL(f16_split_kernel, dim3(m), dim3(kSplitT), 0, stream(), x, xh, xl, esc, n);
+	HK_LAUNCHED("f16_split");
+	return HAKO_GPU_OK;
 }
 
 int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, int n_out, int n_in) {
@@ -423,8 +484,17 @@ int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, 
 	_Float16 *xh = (_Float16 *)ws;
 	_Float16 *xl = (_Float16 *)((uint8_t *)ws + esc_off / 2);
 	float *esc = (float *)((uint8_t *)ws + esc_off);
-	hipLaunchKernelGGL(f16_split_kernel, dim3(m), dim3(kGT), 0, stream(), x, xh, xl, esc, n_in);
-	HK_LAUNCHED("f16_split");
+	if (int rc = f16_split(x, xh, xl, esc, m, n_in)) return rc;
+	if (m <= kSkMaxTokens) {   // a few tokens: the skinny kernel
+		SkSegs segs{};
+		segs.n = 1;
+		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
+		float *part = nullptr;
+		int *cnt = nullptr;
+		if (int rc = skinny_split_workspace(n_in, n_out, &part, &cnt)) return rc;
+		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part, cnt)) return rc;
+		return ok();
+	}
 	hipLaunchKernelGGL(q6k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
 	                   xh, xl, esc, bias, y, m, n_out, n_in);
 	HK_LAUNCHED("q6k_gemm");
@@ -451,8 +521,7 @@ extern "C" int hako_gpu_matmul_batch(float *y, const float *x, int type, const v
 	if (m == 1) return hako_gpu_matmul(y, x, type, w, bias, n_out, n_in);
 	switch (type) {
 	case HAKO_TYPE_Q4_K: {
-		if (n_in <= 0 || n_in % kQK != 0)
-			return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM needs n_in %% 256 == 0 (got %d)", n_in);
+		if (int rc = check_gemm("Q4_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ4Bytes, w)) return rc;
 		const size_t qbytes = ((size_t)m * n_in + 255) & ~(size_t)255;
 		void *ws = nullptr;
 		if (int rc = workspace(4, qbytes + (size_t)m * (n_in / 32) * 4, &ws)) return rc;

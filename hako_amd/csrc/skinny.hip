@@ -1,0 +1,456 @@
+// skinny.hip — matmuls of up to 16 tokens at once (batched decode) on the
+// gfx950 matrix cores, weights streamed from HBM once for all tokens.
+//
+// Y[t][r] for t < M <= 16: the M independent matmuls of M sequences stepping
+// together (the reference steps each sequence on its own, one matmul call per
+// token: src/nn.c:179-210). One wave owns 16 weight rows; one 16x16 MFMA tile
+// covers the 16 tokens (A operand, padded with zeros past M) against the 16
+// rows (B operand), so every lane owns one row (l % 16) and keeps that row's
+// scales to itself, and holds four tokens (4*(l/16) + v) of the output.
+//
+// Q4_K x q8 (src/quant.c:150-232 per token and row): one
+// v_mfma_i32_16x16x32_i8 per 32-wide sub-block gives the exact per-sub-block
+// sums iqx; they are folded as iqx*(xs*d*s) on the VALU, and the min term
+// Σ (dmin*m)*(−xs*Σxq) over the block's sub-blocks runs as two
+// v_mfma_f32_16x16x4_f32. The activations (q8_32 of each token row) are
+// staged in LDS once per workgroup.
+//
+// Q6_K x fp32 (src/nn.c:84-95): q−32 exact in fp16 against the activation as
+// fp16 hi + lo after an exact per-token power-of-two scaling (the prefill
+// GEMM's representation); two v_mfma_f32_16x16x16_f16 per 16-wide scale group
+// then the group sum times d*sc (exact fp32). Activations are staged through
+// LDS two super-blocks at a time, double-buffered.
+#include "hako_dev.h"
+#include "hako_rt.h"
+#include "skinny.h"
+
+namespace hako {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+constexpr int kT = 256;      // threads per workgroup: 4 waves
+constexpr int kRowsWave = 16;
+constexpr int kRowsWg = 4 * kRowsWave;
+constexpr int kAPadQ4 = 16;  // bytes of padding per staged token row
+
+__device__ __forceinline__ uint32_t ld_b32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+	return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+// segment of a wave (segment starts are multiples of 16 rows)
+struct SegView {
+	const uint8_t *w;
+	const float *bias;
+	float *out;
+	int row0, rows, ld;
+};
+
+// Fields picked with constant indices and masks: an indexed or selected
+// access to the by-value argument makes the compiler copy it to scratch.
+__device__ __forceinline__ SegView seg_of(const SkSegs s, int wrow0, bool swiglu) {
+	const int si = swiglu ? 0 : (s.n > 2 && wrow0 >= s.s[2].row0) ? 2 : (s.n > 1 && wrow0 >= s.s[1].row0) ? 1 : 0;
+	const uint64_t m0 = 0ull - (uint64_t)(si == 0), m1 = 0ull - (uint64_t)(si == 1), m2 = 0ull - (uint64_t)(si == 2);
+	auto pick = [&](uint64_t a, uint64_t b, uint64_t c) { return (a & m0) | (b & m1) | (c & m2); };
+	auto pp = [](const void *p) { return (uint64_t)(uintptr_t)p; };
+	SegView v;
+	v.w = (const uint8_t *)(uintptr_t)pick(pp(s.s[0].w), pp(s.s[1].w), pp(s.s[2].w));
+	v.bias = (const float *)(uintptr_t)pick(pp(s.s[0].bias), pp(s.s[1].bias), pp(s.s[2].bias));
+	v.out = (float *)(uintptr_t)pick(pp(s.s[0].out), pp(s.s[1].out), pp(s.s[2].out));
+	v.row0 = (int)pick((uint32_t)s.s[0].row0, (uint32_t)s.s[1].row0, (uint32_t)s.s[2].row0);
+	v.rows = (int)pick((uint32_t)s.s[0].rows, (uint32_t)s.s[1].rows, (uint32_t)s.s[2].rows);
+	v.ld = (int)pick((uint32_t)s.s[0].ld, (uint32_t)s.s[1].ld, (uint32_t)s.s[2].ld);
+	return v;
+}
+
+// Epilogue: lane holds tokens 4*(l/16) + v of row r (its lane's row).
+// Store: out[t][r] = y + bias[r]; Add: out[t][r] += y.
+__device__ __forceinline__ void skinny_epilogue(int epi, const SegView &S, int vrow, bool ok,
+                                                const float y[4], int M, int lane) {
+	const int t0 = 4 * (lane >> 4);
+	if (!ok) return;
+	const int r = vrow - S.row0;
+	const float b = (epi == kSkStore && S.bias) ? S.bias[r] : 0.0f;
+#pragma unroll
+	for (int v = 0; v < 4; v++) {
+		if (t0 + v < M) {
+			float *o = S.out + (size_t)(t0 + v) * S.ld + r;
+			*o = epi == kSkAdd ? *o + y[v] : y[v] + b;
+		}
+	}
+}
+
+// ── Q4_K x q8 ──
+
+struct Q4SkBuf {
+	uint4 h;        // block header of the lane's row
+	uint2 q[4];     // qs bytes 32g + 8(l/16) .. +8 of each 64-weight group g
+};
+
+// Rows of a workgroup: Store / Add — wave w takes 16 consecutive rows of the
+// launch's row space; SwiGLU — the workgroup takes 32 rows r0.., wave w the
+// gate (w even) or up (w odd) rows r0 + 16*(w/2) .., so that each wave
+// streams one matrix through one (uniform) buffer descriptor; the up sums
+// reach the gate waves through LDS.
+template <int EPI, int DEPTH>
+__global__ __launch_bounds__(kT) void q4k_skinny_kernel(SkSegs segs, const int8_t *__restrict__ xq,
+                                                        const float *__restrict__ xs, int M, int K, int vrows) {
+	extern __shared__ __align__(16) uint8_t smem[];
+	const int KP = K + kAPadQ4, NB = K >> 8, NS = K >> 5;
+	int8_t *a_s = (int8_t *)smem;                           // [16][KP] xq
+	float *xs_s = (float *)(smem + 16 * KP);                // [NS][16] xs
+	float *nu_s = xs_s + NS * 16;                           // [NS][16] -xs*Σxq
+	float *ex_s = nu_s + NS * 16;                           // [4 waves][16 rows][8] d*s per sub-block
+	float *up_s = ex_s + 4 * 16 * 8;                        // [2][16 rows][16 tokens] up sums (SwiGLU)
+	int4 *trash_s = (int4 *)(up_s + 2 * 16 * 16);           // target of the stores with no item
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment and descriptors in SGPRs
+	const int j = lane & 15, kq = lane >> 4;
+	const bool swiglu = EPI == kSkSwiGLU;
+	const int wrow0 = swiglu ? blockIdx.x * 32 + (wave >> 1) * 16 : (blockIdx.x * 4 + wave) * kRowsWave;
+	const SegView S = seg_of(segs, swiglu ? 0 : wrow0, swiglu);
+	const uint8_t *wbase = swiglu ? ((wave & 1) ? segs.s[1].w : segs.s[0].w) : S.w;
+	const int srows = swiglu ? segs.s[0].rows : S.rows;
+	const int wr = swiglu ? wrow0 + j : wrow0 + j - S.row0;   // this lane's row of its matrix
+	const bool ok = wr < srows && (swiglu || wrow0 + j < vrows);
+	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
+	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(wbase, (uint32_t)srows * rb);
+	const uint32_t row_off = ok ? (uint32_t)wr * rb : kBufNone;
+
+	// 1. the first DEPTH super-blocks' weight loads (every one of the row when
+	//    n_in <= 256*DEPTH), before the activation staging
+	constexpr int kQ4Depth = DEPTH;
+	Q4SkBuf buf[kQ4Depth];
+	auto issue = [&](Q4SkBuf &b, int kb) {
+		const uint32_t o = kb < NB ? row_off + (uint32_t)kb * kQ4Bytes : kBufNone;
+		b.h = ld_b128(wrs, o);
+#pragma unroll
+		for (int g = 0; g < 4; g++) b.q[g] = ld_b64(wrs, o + 16 + 32 * g + 8 * kq);
+	};
+#pragma unroll
+	for (int d = 0; d < kQ4Depth; d++) issue(buf[d], d);
+	__builtin_amdgcn_sched_barrier(0);
+
+	// 2. activations: xq rows (zeros past M), xs, and -xs*Σxq per sub-block.
+	//    Buffer loads answer items past the data with zeros, and items past
+	//    the work store into a trash slot, so no load sits behind a branch and
+	//    the staging costs one L2 round trip.
+	constexpr int kXqPer = 16 * kSkMaxQ4In / 16 / kT;   // int4 of xq per thread at most
+	constexpr int kXsPer = 16 * kSkMaxQ4In / 32 / kT;   // xs per thread at most
+	const int nq = 16 * (K >> 4), nsv = 16 * NS;
+	const __amdgpu_buffer_rsrc_t qrs = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
+	const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
+	uint4 qv[kXqPer];
+	float sv[kXsPer];
+#pragma unroll
+	for (int u = 0; u < kXqPer; u++) {
+		const int c = tid + kT * u, t = c / (K >> 4), p = c - t * (K >> 4);
+		qv[u] = ld_b128(qrs, c < nq ? (uint32_t)t * K + 16u * p : kBufNone);
+	}
+#pragma unroll
+	for (int u = 0; u < kXsPer; u++) {
+		const int c = tid + kT * u, t = c / NS, sb = c - t * NS;
+		sv[u] = __builtin_bit_cast(float, ld_b32(srs, c < nsv ? 4u * ((uint32_t)t * NS + sb) : kBufNone));
+	}
+#pragma unroll
+	for (int u = 0; u < kXqPer; u++) {
+		const int c = tid + kT * u, t = c / (K >> 4), p = c - t * (K >> 4);
+		*(c < nq ? (uint4 *)(a_s + t * KP + 16 * p) : (uint4 *)(trash_s + tid)) = qv[u];
+	}
+	__syncthreads();
+#pragma unroll
+	for (int u = 0; u < kXsPer; u++) {
+		const int c = min(tid + kT * u, nsv - 1), t = c / NS, sb = c - t * NS;
+		const int4 *p = (const int4 *)(a_s + t * KP + 32 * sb);
+		const int4 p0 = p[0], p1 = p[1];
+		int ix = 0;
+		ix = sdot4(p0.x, 0x01010101, ix); ix = sdot4(p0.y, 0x01010101, ix);
+		ix = sdot4(p0.z, 0x01010101, ix); ix = sdot4(p0.w, 0x01010101, ix);
+		ix = sdot4(p1.x, 0x01010101, ix); ix = sdot4(p1.y, 0x01010101, ix);
+		ix = sdot4(p1.z, 0x01010101, ix); ix = sdot4(p1.w, 0x01010101, ix);
+		if (tid + kT * u < nsv) {
+			xs_s[sb * 16 + t] = sv[u];
+			nu_s[sb * 16 + t] = -sv[u] * (float)ix;
+		}
+	}
+	__syncthreads();
+
+	v4f acc = {0.0f, 0.0f, 0.0f, 0.0f}, accm = {0.0f, 0.0f, 0.0f, 0.0f};
+	const v4i zero = {0, 0, 0, 0};
+	float *ex = ex_s + (wave * 16 + j) * 8;
+	const int8_t *arow = a_s + j * KP + 8 * kq;   // A operand: token j, K-slice 8kq
+	for (int kb0 = 0; kb0 < NB; kb0 += kQ4Depth) {
+#pragma unroll
+		for (int d = 0; d < kQ4Depth; d++) {
+			const int kb = kb0 + d;
+			if (kb < NB) {
+				const Q4SkBuf &b = buf[d];
+				// (s, m) of sub-blocks kq and kq + 4 of this lane's row: d*s shared
+				// with the row's other lanes through LDS, dmin*m kept for the MFMA
+				uint32_t s0, m0, s1, m1;
+				scale_min_k4((uint32_t)kq, b.h.y, b.h.z, b.h.w, s0, m0);
+				scale_min_k4((uint32_t)kq + 4u, b.h.y, b.h.z, b.h.w, s1, m1);
+				const float dd = f16_to_f32(b.h.x & 0xFFFFu), dmin = f16_to_f32(b.h.x >> 16);
+				ex[kq] = dd * (float)s0;
+				ex[kq + 4] = dd * (float)s1;
+				const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
+				// min term: K = sub-block (4 per MFMA), lanes kq supply sub-blocks kq, kq+4
+				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kb + kq) * 16 + j], dm0, accm, 0, 0, 0);
+				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kb + kq + 4) * 16 + j], dm1, accm, 0, 0, 0);
+				__builtin_amdgcn_wave_barrier();
+				const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
+				const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
+#pragma unroll
+				for (int g = 0; g < 4; g++) {
+					const uint2 q = b.q[g];
+#pragma unroll
+					for (int h = 0; h < 2; h++) {
+						const int sb = 2 * g + h;
+						const uint32_t w0 = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+						const uint32_t w1 = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+						const long wv = (long)(((uint64_t)w1 << 32) | w0);
+						const long av = *(const long *)(arow + 256 * kb + 32 * sb);
+						const v4i di = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zero, 0, 0, 0);
+						const float4 x4 = *(const float4 *)(xs_s + (8 * kb + sb) * 16 + 4 * kq);
+						acc[0] = __builtin_fmaf((float)di[0], x4.x * ds[sb], acc[0]);
+						acc[1] = __builtin_fmaf((float)di[1], x4.y * ds[sb], acc[1]);
+						acc[2] = __builtin_fmaf((float)di[2], x4.z * ds[sb], acc[2]);
+						acc[3] = __builtin_fmaf((float)di[3], x4.w * ds[sb], acc[3]);
+					}
+				}
+				__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next block
+			}
+			issue(buf[d], kb + kQ4Depth);
+		}
+	}
+	float y[4] = {acc[0] + accm[0], acc[1] + accm[1], acc[2] + accm[2], acc[3] + accm[3]};
+	if (swiglu) {
+		// up waves hand their sums to the gate waves of the same rows
+		float *up = up_s + ((wave >> 1) * 16 + j) * 16 + 4 * kq;
+		if (wave & 1) *(float4 *)up = make_float4(y[0], y[1], y[2], y[3]);
+		__syncthreads();
+		if ((wave & 1) || !ok) return;
+		const float4 u4 = *(const float4 *)up;
+		const float uv[4] = {u4.x, u4.y, u4.z, u4.w};
+		float *out = segs.s[0].out;
+		const int ld = segs.s[0].ld;
+#pragma unroll
+		for (int v = 0; v < 4; v++)
+			if (4 * kq + v < M) out[(size_t)(4 * kq + v) * ld + wr] = y[v] / (1.0f + expf(-y[v])) * uv[v];
+		return;
+	}
+	skinny_epilogue(EPI, S, wrow0 + j, ok, y, M, lane);
+}
+
+// ── Q6_K x fp32 (fp16 hi/lo) ──
+
+constexpr int kQ6SkStage = 512;             // K per activation stage (two super-blocks)
+constexpr int kHPadSk = kQ6SkStage + 8;     // fp16 per staged token row
+
+struct Q6SkBuf {
+	uint32_t ql[2][4];   // per half n: ql bytes 64n + 16q + 4kq .. +4, q = 0..3
+	uint32_t qh[2][2];   // per half n: qh bytes 32n + 16p + 4kq .. +4, p = 0..1
+	uint4 sc;            // the 16 scales
+	uint32_t d;
+};
+
+// Workgroup (row tile, K split): the tile's 64 rows over super-blocks
+// [kb_beg, kb_end). With nsplit > 1 the splits' results go to `part`
+// ([nsplit][16][vrows]) and the last split of a tile to finish (counter in
+// cnt[tile], reset by that workgroup) sums them in split order and applies
+// the epilogue.
+template <int EPI>
+__global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Float16 *__restrict__ xh,
+                                                        const _Float16 *__restrict__ xl,
+                                                        const float *__restrict__ esc, int M, int K, int vrows,
+                                                        int nsplit, float *part, int *cnt) {
+	__shared__ __align__(16) _Float16 ah_s[2][16 * kHPadSk];
+	__shared__ __align__(16) _Float16 al_s[2][16 * kHPadSk];
+	__shared__ int last_s;
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment and descriptors in SGPRs
+	const int j = lane & 15, kq = lane >> 4;
+	const int NB = K >> 8;
+	const int tile = blockIdx.x / nsplit, split = blockIdx.x - tile * nsplit;
+	const int kb_beg = (int)((int64_t)split * NB / nsplit), kb_end = (int)((int64_t)(split + 1) * NB / nsplit);
+	const int NSt = (kb_end - kb_beg + 1) / 2;
+	const int wrow0 = (tile * 4 + wave) * kRowsWave;
+	const SegView S = seg_of(segs, wrow0, false);
+	const int vrow = wrow0 + j, wr = vrow - S.row0;
+	const bool ok = vrow < vrows && wr < S.rows;
+	const uint32_t rb = (uint32_t)NB * kQ6Bytes;
+	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, (uint32_t)S.rows * rb);   // the wave's segment
+	const uint32_t row_off = ok ? (uint32_t)wr * rb : kBufNone;
+	const __amdgpu_buffer_rsrc_t hrs = stream_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
+	const __amdgpu_buffer_rsrc_t lrs = stream_rsrc(xl, (uint32_t)M * (uint32_t)K * 2u);
+
+	auto issue = [&](Q6SkBuf &b, int kb) {
+		const uint32_t o = kb < kb_end ? row_off + (uint32_t)kb * kQ6Bytes : kBufNone;
+#pragma unroll
+		for (int n = 0; n < 2; n++) {
+#pragma unroll
+			for (int q = 0; q < 4; q++) b.ql[n][q] = ld_b32(wrs, o + 64 * n + 16 * q + 4 * kq);
+#pragma unroll
+			for (int p = 0; p < 2; p++) b.qh[n][p] = ld_b32(wrs, o + 128 + 32 * n + 16 * p + 4 * kq);
+		}
+		b.sc = ld_b128(wrs, o + 192);
+		b.d = ld_b16(wrs, o + 208);
+	};
+	// activation stage st: 16 tokens x 512 K of hi and lo (zeros past M or K)
+	uint4 hreg[4], lreg[4];
+	auto load_stage = [&](int st) {
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			const int c = tid + kT * u, t = c >> 6, p = c & 63;   // 16 tokens x 64 pieces of 8 fp16
+			const int k = 256 * kb_beg + kQ6SkStage * st + 8 * p;
+			const uint32_t off = (t < M && k < 256 * kb_end) ? 2u * ((uint32_t)t * K + k) : kBufNone;
+			hreg[u] = ld_b128(hrs, off);
+			lreg[u] = ld_b128(lrs, off);
+		}
+	};
+	auto store_stage = [&](int slot) {
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			const int c = tid + kT * u, t = c >> 6, p = c & 63;
+			*(uint4 *)(ah_s[slot] + t * kHPadSk + 8 * p) = hreg[u];
+			*(uint4 *)(al_s[slot] + t * kHPadSk + 8 * p) = lreg[u];
+		}
+	};
+
+	Q6SkBuf b0, b1;
+	issue(b0, kb_beg);
+	issue(b1, kb_beg + 1);
+	load_stage(0);
+	store_stage(0);
+	__syncthreads();
+	v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+	const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+	for (int st = 0; st < NSt; st++) {
+		const int slot = st & 1;
+		if (st + 1 < NSt) load_stage(st + 1);
+		const _Float16 *ah = ah_s[slot] + j * kHPadSk + 4 * kq;
+		const _Float16 *al = al_s[slot] + j * kHPadSk + 4 * kq;
+#pragma unroll
+		for (int half_st = 0; half_st < 2; half_st++) {
+			const int kb = kb_beg + 2 * st + half_st;
+			Q6SkBuf &b = half_st ? b1 : b0;
+			if (kb < kb_end) {
+				const float dd = f16_to_f32(b.d);
+				const uint32_t scw[4] = {b.sc.x, b.sc.y, b.sc.z, b.sc.w};
+#pragma unroll
+				for (int gg = 0; gg < 16; gg++) {
+					// K = 16gg + 4kq + e: half n = gg/8, k = (gg/2)%4, l = 16(gg%2) + 4kq + e
+					const int n = gg >> 3, k = (gg >> 1) & 3, p = gg & 1;
+					const uint32_t qlw = b.ql[n][2 * (k & 1) + p], qhw = b.qh[n][p];
+					const uint32_t nib = (k >> 1) ? (qlw >> 4) & 0x0F0F0F0Fu : qlw & 0x0F0F0F0Fu;
+					const uint32_t q6 = nib | (((qhw >> (2 * k)) & 0x03030303u) << 4);
+					const uint32_t lo2 = (__builtin_amdgcn_perm(q6, q6, 0x0C010C00u) | 0x64006400u);
+					const uint32_t hi2 = (__builtin_amdgcn_perm(q6, q6, 0x0C030C02u) | 0x64006400u);
+					const v2h bias2 = {(_Float16)1056.0f, (_Float16)1056.0f};
+					const v2h w01 = __builtin_bit_cast(v2h, lo2) - bias2, w23 = __builtin_bit_cast(v2h, hi2) - bias2;
+					const v4h wv = {w01[0], w01[1], w23[0], w23[1]};
+					const int ko = 256 * half_st + 16 * gg;
+					v4f pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(ah + ko), wv, zero, 0, 0, 0);
+					pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(al + ko), wv, pr, 0, 0, 0);
+					const float s = dd * (float)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 0xFFu);
+					acc[0] = __builtin_fmaf(pr[0], s, acc[0]);
+					acc[1] = __builtin_fmaf(pr[1], s, acc[1]);
+					acc[2] = __builtin_fmaf(pr[2], s, acc[2]);
+					acc[3] = __builtin_fmaf(pr[3], s, acc[3]);
+				}
+			}
+			issue(b, kb + 2);
+		}
+		if (st + 1 < NSt) {
+			store_stage(slot ^ 1);
+			__syncthreads();
+		}
+	}
+	const int t0 = 4 * kq;
+	float y[4];
+#pragma unroll
+	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? acc[v] * esc[t0 + v] : 0.0f;
+	if (nsplit > 1) {
+		if (ok)
+#pragma unroll
+			for (int v = 0; v < 4; v++) part[((size_t)split * 16 + t0 + v) * vrows + vrow] = y[v];
+		__threadfence();
+		__syncthreads();
+		if (tid == 0) last_s = atomicAdd(&cnt[tile], 1) == nsplit - 1;
+		__syncthreads();
+		if (!last_s) return;
+		__threadfence();
+#pragma unroll
+		for (int v = 0; v < 4; v++) y[v] = 0.0f;
+		if (ok)
+			for (int sp = 0; sp < nsplit; sp++)
+#pragma unroll
+				for (int v = 0; v < 4; v++) y[v] += part[((size_t)sp * 16 + t0 + v) * vrows + vrow];
+		if (tid == 0) atomicExch(&cnt[tile], 0);   // ready for the next launch
+	}
+	skinny_epilogue(EPI, S, vrow, ok, y, M, lane);
+}
+
+}  // namespace
+
+int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows) {
+	const size_t lds = q4k_skinny_lds(n_in);
+	// SwiGLU: 32 rows (gate and up) per workgroup, row space 2*rows
+	const int wgs = epi == kSkSwiGLU ? (segs.s[0].rows + 31) / 32 : (vrows + kRowsWg - 1) / kRowsWg;
+	const int nb = n_in / kQK;
+#define HK_Q4SK(E, D) \
+	hipLaunchKernelGGL((q4k_skinny_kernel<E, D>), dim3(wgs), dim3(kT), lds, stream(), segs, xq, xs, m, n_in, vrows)
+#define HK_Q4SK_D(E)                       \
+	do {                                   \
+		if (nb <= 8) HK_Q4SK(E, 8);        \
+		else HK_Q4SK(E, 16);               \
+	} while (0)
+	if (epi == kSkStore)
+		HK_Q4SK_D(kSkStore);
+	else if (epi == kSkAdd)
+		HK_Q4SK_D(kSkAdd);
+	else
+		HK_Q4SK_D(kSkSwiGLU);
+#undef HK_Q4SK_D
+#undef HK_Q4SK
+	HK_LAUNCHED("q4k_skinny");
+	return HAKO_GPU_OK;
+}
+
+int q6k_skinny_splits(int n_in, int vrows) {
+	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
+	int ns = (kSkTargetWgs + tiles - 1) / tiles;       // enough workgroups to fill the chip
+	ns = ns > nb / 4 ? nb / 4 : ns;                    // at least two stages of K per split
+	return ns < 1 ? 1 : ns;
+}
+
+size_t q6k_skinny_part_floats(int n_in, int vrows) {
+	const int ns = q6k_skinny_splits(n_in, vrows);
+	return ns > 1 ? (size_t)ns * 16 * vrows : 0;
+}
+
+int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
+               int n_in, int vrows, float *part, int *cnt) {
+	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
+	const int ns = q6k_skinny_splits(n_in, vrows);
+	if (ns > 1 && (!part || !cnt)) return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace");
+	const dim3 grid(tiles * ns);
+	if (epi == kSkStore)
+		hipLaunchKernelGGL(q6k_skinny_kernel<kSkStore>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
+		                   vrows, ns, part, cnt);
+	else
+		hipLaunchKernelGGL(q6k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
+		                   vrows, ns, part, cnt);
+	HK_LAUNCHED("q6k_skinny");
+	return HAKO_GPU_OK;
+}
+
+size_t q4k_skinny_lds(int n_in) {
+	return (size_t)16 * (n_in + kAPadQ4) + (size_t)2 * 16 * (n_in / 32) * 4 + 4 * 16 * 8 * 4 + 2 * 16 * 16 * 4 +
+	       kT * 16;
+}
+
+}  // namespace hako

@@ -82,7 +82,11 @@ class Decoder:
             m.out_weight, m.t_out = dev("output.weight")
         m.blocks = blocks
         d = _vp()
-        gpu.check(self.lib.hako_gpu_decoder_create(C.byref(m), n_seq, max_seq, C.byref(d)), "decoder_create")
+        try:
+            gpu.check(self.lib.hako_gpu_decoder_create(C.byref(m), n_seq, max_seq, C.byref(d)), "decoder_create")
+        except Exception:
+            gpu.mirror_release(self.data)
+            raise
         self.d = d.value
 
     def close(self):

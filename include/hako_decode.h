@@ -54,8 +54,12 @@ typedef struct hako_gpu_decoder hako_gpu_decoder;
 
 /* A decoder for n_seq independent sequences of up to max_seq positions each
  * (KV caches, activations and the rope table are allocated here, once).
- * Requires head_dim 64 or 128, n_heads % n_kv_heads == 0, d_model and
- * ffn_dim multiples of 256 and n_seq == 1 (one sequence per step). */
+ * Requires head_dim 64 or 128, n_heads % n_kv_heads == 0 with at most 8
+ * query heads per KV head, d_model and ffn_dim multiples of 256, and
+ * 1 <= n_seq <= 16. With n_seq > 1 every step advances all sequences
+ * together, each matmul streaming its weights once for all of them (the
+ * Q4_K_M mix: Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or Q6_K lm_head, and
+ * d_model <= 4096); n_seq == 1 takes any F32/F16/Q4_K/Q6_K mix. */
 int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec);
 int hako_gpu_decoder_destroy(hako_gpu_decoder *dec);
 

@@ -1,0 +1,147 @@
+"""The batched decode step (include/hako_decode.h, n_seq > 1): up to 16
+independent sequences advance together, each matmul a skinny matrix-core GEMM
+that streams the weights once for all of them.
+
+Each sequence is checked against the reference's own forward
+(src/model.c:93-165, compiled from its sources) run on that sequence alone
+with the same prefilled KV cache and start position: identical greedy tokens,
+logits within 2e-2 of their range (q8 re-quantization of activations that
+differ in the last bit flips single int8 values).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from hako_amd import mlf2, synth
+from helpers import maxabs_rel
+
+pytestmark = pytest.mark.gpu
+
+TINY = mlf2.Qwen2Config(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512,
+                        vocab=1024, ctx=256)
+SMALL_128 = mlf2.Qwen2Config(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=2816,
+                             vocab=4096, ctx=512)
+# untied Q4_K output (the Q4_K lm_head branch), 7 query heads per KV head
+UNTIED_Q4_OUT = mlf2.Qwen2Config(n_layers=2, d_model=1792, n_heads=14, n_kv_heads=2, head_dim=128, ffn_dim=1536,
+                                 vocab=2000, ctx=256, tied=False, embd_type=synth.TYPE_Q4_K,
+                                 out_type=synth.TYPE_Q4_K)
+
+
+@pytest.fixture(scope="module")
+def ref():
+    from dropin import bind_ctx
+    from oracle.hako_oracle import REF_LIB
+    return bind_ctx(C.CDLL(REF_LIB))
+
+
+def fill_kv(gpu, dec, kv_per_seq, n_layers):
+    k, v = dec.kv()
+    for s, kv in enumerate(kv_per_seq):
+        for l in range(n_layers):
+            if kv.shape[2]:
+                gpu.h2d(k + dec.kv_offset(s, l, 0), np.ascontiguousarray(kv[0, l]))
+                gpu.h2d(v + dec.kv_offset(s, l, 0), np.ascontiguousarray(kv[1, l]))
+
+
+def seq_setup(cfg, n_seq, seed, max_pos):
+    rng = np.random.default_rng(seed)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    pos = rng.integers(0, max_pos + 1, n_seq)
+    pos[0] = 0
+    starts = rng.integers(0, cfg.vocab, n_seq)
+    kvs = [rng.standard_normal((2, cfg.n_layers, int(p), kvd)).astype(np.float32) for p in pos]
+    return pos.astype(np.int32), starts.astype(np.int32), kvs
+
+
+@pytest.mark.parametrize("cfg,n_seq,seed", [(TINY, 4, 1), (TINY, 16, 2), (SMALL_128, 16, 3),
+                                            (UNTIED_Q4_OUT, 5, 4)])
+def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, n_seq, seed):
+    from dropin import prefilled_greedy
+    from hako_amd.decoder import Decoder
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, seed)
+    max_seq, steps = 256, 8
+    pos, starts, kvs = seq_setup(cfg, n_seq, seed, 200)
+    dec = Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
+    try:
+        fill_kv(gpu, dec, kvs, cfg.n_layers)
+        dec.set_pos(pos)
+        toks, got, logits = starts.copy(), [], []
+        for _ in range(steps):
+            toks, lg = dec.step(toks, logits=True)
+            assert np.array_equal(toks, np.argmax(lg, axis=1))
+            got.append(toks.copy())
+            logits.append(lg)
+    finally:
+        dec.close()
+    got, logits = np.stack(got), np.stack(logits)
+    for s in range(n_seq):
+        want, want_logits = prefilled_greedy(ref, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=steps,
+                                             vocab=cfg.vocab, max_seq=max_seq)
+        assert np.all(np.isfinite(want_logits))
+        assert got[:, s].tolist() == want, f"sequence {s} (position {pos[s]})"
+        assert maxabs_rel(logits[:, s], want_logits) < 2e-2, f"sequence {s}"
+
+
+def test_batched_graph_replays_equal_eager_steps(gpu, tmp_path):
+    """generate() with n_seq = 16 replays one captured step; the replays equal
+    the eager steps, across two generate calls (the split-K counters return
+    to zero after every launch)."""
+    from hako_amd.decoder import Decoder
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, SMALL_128, 6)
+    n_seq = 16
+    starts = np.arange(100, 100 + n_seq, dtype=np.int32) * 7
+    dec = Decoder(gpu, path, n_seq=n_seq, max_seq=128)
+    try:
+        dec.set_pos(0)
+        eager, toks = [], starts
+        for _ in range(12):
+            toks = dec.step(toks)
+            eager.append(toks.copy())
+        dec.set_pos(0)
+        first = dec.generate(starts, 6)
+        second = dec.generate(first[-1], 6)
+    finally:
+        dec.close()
+    assert np.array_equal(np.concatenate([first, second]), np.stack(eager))
+
+
+def test_batched_sequences_are_independent(gpu, tmp_path):
+    """A sequence's tokens do not depend on what the other sequences hold:
+    sequence 3 alone (n_seq = 1 decoder) equals sequence 3 of a batch of 8."""
+    from hako_amd.decoder import Decoder
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, TINY, 12)
+    n_seq, steps = 8, 10
+    pos, starts, kvs = seq_setup(TINY, n_seq, 12, 150)
+    dec = Decoder(gpu, path, n_seq=n_seq, max_seq=256)
+    try:
+        fill_kv(gpu, dec, kvs, TINY.n_layers)
+        dec.set_pos(pos)
+        batch = dec.generate(starts, steps)
+    finally:
+        dec.close()
+    one = Decoder(gpu, path, n_seq=1, max_seq=256)
+    try:
+        fill_kv(gpu, one, [kvs[3]], TINY.n_layers)
+        one.set_pos(pos[3])
+        alone = one.generate(starts[3], steps)[:, 0]
+    finally:
+        one.close()
+    assert batch[:, 3].tolist() == alone.tolist()
+
+
+def test_batched_rejects_other_weight_mixes(gpu, tmp_path):
+    from hako_amd.decoder import Decoder
+    from hako_amd.gpu import HakoGpuError
+    path = str(tmp_path / "m.mlf2")
+    cfg = mlf2.Qwen2Config(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512,
+                           vocab=512, ctx=64, down_type=synth.TYPE_Q4_K)
+    mlf2.write_qwen2(path, cfg, 13)
+    with pytest.raises(HakoGpuError, match="Q4_K_M"):
+        Decoder(gpu, path, n_seq=4, max_seq=64)
+    with pytest.raises(HakoGpuError, match="sequences"):
+        Decoder(gpu, path, n_seq=17, max_seq=64)
+    Decoder(gpu, path, n_seq=1, max_seq=64).close()   # one sequence takes any mix

@@ -39,8 +39,10 @@ def run_q4k_gemm(gpu, w, xq, xs, n_out, n_in):
     return y
 
 
-GEMM_SHAPES = [(64, 64, 256), (130, 200, 2048), (7, 100, 3584), (64, 512, 3584), (200, 37, 1280),
-               (96, 300, 11008)]
+GEMM_SHAPES = [(64, 64, 256), (130, 200, 2048), (17, 100, 3584), (64, 512, 3584), (200, 37, 1280),
+               (96, 300, 11008),
+               # up to 16 tokens: the skinny kernels (batched decode)
+               (2, 64, 256), (5, 100, 2048), (16, 512, 3584), (16, 1000, 1280), (1 + 15, 37, 2048), (3, 18944, 3584)]
 
 
 @pytest.mark.parametrize("m,n_out,n_in", GEMM_SHAPES)
@@ -54,7 +56,7 @@ def test_q4k_batch_vs_oracle(gpu, oracle, m, n_out, n_in):
     assert maxabs_rel(got, want) < TOL
 
 
-@pytest.mark.parametrize("m,n_out,n_in", GEMM_SHAPES + [(70, 100, 18944)])
+@pytest.mark.parametrize("m,n_out,n_in", GEMM_SHAPES + [(70, 100, 18944), (16, 100, 18944), (7, 3584, 11008)])
 def test_q6k_batch_vs_oracle(gpu, oracle, m, n_out, n_in):
     rng = np.random.default_rng(m * 1001 + n_out + n_in)
     w = synth.q6k_weight(rng, n_out, n_in)
@@ -98,14 +100,15 @@ def _one_hot_scales(n_blocks, sb, which):
     return np.tile(sc, (n_blocks, 1))
 
 
+@pytest.mark.parametrize("m", [80, 16, 5])
 @pytest.mark.parametrize("sb", [0, 3, 4, 7])
 @pytest.mark.parametrize("which", ["s", "m"])
-def test_q4k_gemm_integer_sums_exact(gpu, oracle, sb, which):
+def test_q4k_gemm_integer_sums_exact(gpu, oracle, m, sb, which):
     """d = 1, dmin = 1, one (s, m) = (1, 0) or (0, 1) per block and xs = 1:
     each output is Σ over blocks of the sub-block's iqx (or −ix), an integer
     the fp32 fold represents exactly — bit-exact against the oracle's sums."""
-    rng = np.random.default_rng(sb * 3 + (which == "m"))
-    m, n_out, n_in = 80, 96, 3584
+    rng = np.random.default_rng(sb * 3 + (which == "m") + m)
+    n_out, n_in = 96, 3584
     nb = n_in // 256
     w = synth.q4k_weight(rng, n_out, n_in).reshape(n_out * nb, 144).copy()
     w[:, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
@@ -123,12 +126,13 @@ def test_q4k_gemm_integer_sums_exact(gpu, oracle, sb, which):
     assert np.array_equal(got, want.astype(np.float32))
 
 
-def test_q6k_gemm_exact_integers(gpu, oracle):
+@pytest.mark.parametrize("m", [70, 16, 3])
+def test_q6k_gemm_exact_integers(gpu, oracle, m):
     """Small-integer activations (exact in fp16, lo = 0) and d = 1: outputs are
     integers the fp32 accumulation holds exactly — bit-exact against the
     oracle's double-precision result."""
-    rng = np.random.default_rng(9)
-    m, n_out, n_in = 70, 90, 2048
+    rng = np.random.default_rng(9 + m)
+    n_out, n_in = 90, 2048
     nb = n_in // 256
     w = synth.q6k_weight(rng, n_out, n_in).reshape(n_out * nb, 210).copy()
     w[:, 208:210] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
