@@ -210,6 +210,76 @@ def bench_decode(g, steps: int, cpu_steps: int, seed: int = 30) -> dict:
         os.unlink(path)
 
 
+def bench_decode_batched(g, steps: int, cpu_steps: int, seed: int = 40, n_seq: int = 16) -> dict:
+    """Greedy decode of 16 sequences of a Qwen2-7B-shaped model (28 layers,
+    Q4_K attn/gate/up and embedding, Q6_K down and untied output, random
+    weights), every sequence's KV cache prefilled with 4095 positions of seeded
+    N(0,1) keys and values, so that the first step writes position 4096:
+    `steps` graph-replayed steps, each advancing all 16 sequences. The
+    reference steps one hakm_ctx per sequence; its hakm_forward on the same
+    file and a cache of the same length is timed for `cpu_steps` tokens."""
+    import tempfile
+    from hako_amd import mlf2
+    from hako_amd.decoder import Decoder
+    cfg, pos = mlf2.QWEN2_7B, 4095
+    max_seq = pos + steps + 8
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    fd, path = tempfile.mkstemp(suffix=".mlf2")
+    os.close(fd)
+    try:
+        info = mlf2.write_qwen2(path, cfg, seed)
+        # one seeded N(0,1) cache, copied to every sequence's own (distinct) slots
+        kv = np.random.default_rng(seed + 1).standard_normal((2, cfg.n_layers, pos, kvd)).astype(np.float32)
+        starts = (np.arange(n_seq, dtype=np.int32) * 9973 + 11) % cfg.vocab
+        dec = Decoder(g, path, n_seq=n_seq, max_seq=max_seq)
+        try:
+            k, v = dec.kv()
+            for s in range(n_seq):
+                for l in range(cfg.n_layers):
+                    g.h2d(k + dec.kv_offset(s, l, 0), kv[0, l])
+                    g.h2d(v + dec.kv_offset(s, l, 0), kv[1, l])
+            dec.set_pos(pos)
+            dec.generate(starts, 4)     # capture and warm
+            g.sync()
+            dec.set_pos(pos)
+            e0, e1 = g.event(), g.event()
+            g.record(e0)
+            dec.replay(steps)
+            g.record(e1)
+            ms = g.elapsed_ms(e0, e1)
+        finally:
+            dec.close()
+        # the untied embedding contributes one row per sequence, not its matrix
+        weight_bytes = sum(e[4] for name, e in info.items() if name != "token_embd.weight")
+        kv_bytes = n_seq * cfg.n_layers * 2 * kvd * 4 * (pos + 1 + (steps - 1) / 2)
+        per_step = weight_bytes + kv_bytes
+        us = ms * 1e3 / steps
+        res = {"workload": "Qwen2-7B-shaped greedy decode (28 layers, Q4_K attn/gate/up, Q6_K down and untied "
+                           "output), 16 sequences per step, each KV cache from position 4095",
+               "n_seq": n_seq, "steps": steps, "us_per_step": round(us, 2),
+               "tok_per_s": round(n_seq * 1e6 / us, 1), "bytes_per_step": int(per_step),
+               "gbps": round(per_step / (us * 1e-6) / 1e9, 1),
+               "hbm_frac": round(per_step / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+               "timing": "HIP graph of one 16-sequence step replayed K times between two HIP events"}
+        if cpu_steps > 0:
+            from oracle.hako_oracle import REF_LIB, RefLib, prefilled_greedy
+            threads = min(os.cpu_count() or 1, 16)
+            ref = RefLib(REF_LIB, threads=threads)
+            times = []
+            prefilled_greedy(ref.lib, path, kv, pos, int(starts[0]), cpu_steps + 1, cfg.vocab, pos + cpu_steps + 2,
+                             times)
+            med = float(np.median(times[1:]))
+            res["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads,
+                                   "kind": "reference",
+                                   "sample": f"{cpu_steps} hakm_forward steps (after one warm-up) of the reference "
+                                             f"on the same model file, one sequence with its cache at position "
+                                             f"4095, {threads} threads, median {med * 1e3:.1f} ms/token (the "
+                                             f"reference steps its 16 contexts one after another)"}
+        return res
+    finally:
+        os.unlink(path)
+
+
 def bench_prefill(g, launches: int) -> dict:
     """The 7B prefill matmuls: Q4_K 18944x3584 x 512 tokens (q8_32 quantize +
     int8-MFMA GEMM) and Q6_K 3584x18944 x 512 tokens (fp16-MFMA GEMM)."""
@@ -262,11 +332,13 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "decode", "prefill"],
+    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "decode", "decode16", "prefill"],
                     help="run one workload and print its timing only (profiling runs)")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     ap.add_argument("--decode-steps", type=int, default=100)
     ap.add_argument("--cpu-decode-steps", type=int, default=3)
+    ap.add_argument("--batched-steps", type=int, default=30)
+    ap.add_argument("--cpu-batched-steps", type=int, default=2)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
@@ -280,8 +352,13 @@ def main():
     info = g.info()
     log(f"device {info.name.decode()} CUs={info.compute_units} HBM={info.hbm_bytes / 2**30:.0f} GiB")
 
-    if args.only in ("decode", "prefill"):
-        r = bench_decode(g, args.decode_steps, 0) if args.only == "decode" else bench_prefill(g, 30)
+    if args.only in ("decode", "decode16", "prefill"):
+        if args.only == "decode":
+            r = bench_decode(g, args.decode_steps, 0)
+        elif args.only == "decode16":
+            r = bench_decode_batched(g, args.batched_steps, 0)
+        else:
+            r = bench_prefill(g, 30)
         print(json.dumps(r), flush=True)
         return
     if args.only:
@@ -313,6 +390,12 @@ def main():
         log(f"decode: {decode['us_per_token']:.1f} us/token, {decode['tok_per_s']:.1f} tok/s, "
             f"{decode['gbps']:.0f} GB/s" + (f"; cpu {decode['cpu_baseline']['value']:.2f} tok/s"
                                           if 'cpu_baseline' in decode else ""))
+    batched = None
+    if not args.no_decode:
+        batched = bench_decode_batched(g, args.batched_steps, 0 if args.no_cpu else args.cpu_batched_steps)
+        log(f"decode x16: {batched['us_per_step']:.1f} us/step, {batched['tok_per_s']:.1f} tok/s, "
+            f"{batched['gbps']:.0f} GB/s" + (f"; cpu {batched['cpu_baseline']['value']:.3f} tok/s"
+                                           if 'cpu_baseline' in batched else ""))
     prefill = None
     if not args.no_prefill:
         prefill = bench_prefill(g, 30)
@@ -340,6 +423,7 @@ def main():
         "single_launch_us": round(head["single_launch_us"], 3),
         "extra": extra,
         "decode": decode,
+        "decode_batched": batched,
         "prefill": prefill,
     }
     print(json.dumps(out), flush=True)

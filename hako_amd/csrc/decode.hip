@@ -334,12 +334,11 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 // cos/sin of pos*theta^(-2i/hd)); the workgroup whose chunk holds pos also
 // rotates the new key, appends it and the new value to the caches and uses
 // them from LDS. Scores, chunk-local softmax (max m, sum l) and the weighted
-// value sum o go to `part`; the last workgroup of the (sq, kvh) group to
-// finish merges the chunks: out = Σ o_c e^(m_c-M) / Σ l_c e^(m_c-M).
+// value sum o go to `part` for attn_merge_kernel.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv, const float2 *__restrict__ rope,
                                                    float *kc, float *vc, const int *__restrict__ posv,
-                                                   float *part, int *cnt, float *__restrict__ att, int H, int KVH,
+                                                   float *part, int H, int KVH,
                                                    int max_seq, int max_chunks, size_t kv_seq_stride,
                                                    int qkv_stride, float scale) {
 	constexpr int HALF = HD / 2;
@@ -352,7 +351,6 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	__shared__ float ml_s[kMaxG][2];
 	__shared__ float o_s[4][kMaxG][HD];         // value sums per position group
 	__shared__ float kn_s[HD], vn_s[HD];
-	__shared__ int last_s;
 	const int c = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int G = H / KVH, KV = KVH * HD, D = H * HD;
@@ -499,72 +497,63 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 		rec0[(size_t)tid * REC + HD] = ml_s[tid][0];
 		rec0[(size_t)tid * REC + HD + 1] = ml_s[tid][1];
 	}
-	__threadfence();
-	__syncthreads();
-	if (tid == 0) last_s = atomicAdd(&cnt[sq * KVH + kvh], 1) == nact - 1;
-	__syncthreads();
-	if (!last_s) return;
-	__threadfence();
+}
 
-	// 6. merge the chunks: M, L and the weights e^(m_c - M)/L per head (wave w:
-	//    heads w, w+4; up to 64 chunks at a time in LDS, reusing s_s), then
-	//    the weighted sums with every chunk's load issued before any is used
-	const float *grp = part + ((size_t)(sq * KVH + kvh) * max_chunks) * kMaxG * REC;
-#pragma unroll
-	for (int h = 0; h < kMaxG / 4; h++) {
-		const int g = wave + 4 * h;
-		if (g < G) {
-			float mx = -INFINITY;
-			for (int cc = lane; cc < nact; cc += 64) mx = __builtin_fmaxf(mx, grp[((size_t)cc * kMaxG + g) * REC + HD]);
-			mx = wave_max(mx);
-			float lsum = 0.0f;
-			for (int cc = lane; cc < nact; cc += 64) {
-				const float *r = grp + ((size_t)cc * kMaxG + g) * REC;
-				lsum += r[HD + 1] * expf(r[HD] - mx);
-			}
-			lsum = wave_sum(lsum);
-			if (lane == 0) {
-				ml_s[g][0] = mx;
-				ml_s[g][1] = 1.0f / lsum;
-			}
-		}
-	}
+// Grid (G, n_kv_heads, n_seq), HD threads: query head kvh*G + g of sequence
+// sq from its chunks' records — M = max m_c, weights e^(m_c - M) / L with
+// L = sum l_c e^(m_c - M), output sum over chunks of weight * o_c, in chunk
+// order. A launch of its own: the records of every chunk's workgroup are
+// visible at the kernel boundary, with no fence per workgroup.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict__ part, const int *__restrict__ posv,
+                                                        float *__restrict__ att, int H, int KVH, int max_seq,
+                                                        int max_chunks) {
+	constexpr int REC = HD + 2, NW = HD / 64;
+	constexpr size_t CS = (size_t)kMaxG * REC;   // floats between two chunks' records of one head
+	__shared__ float w_s[HD];
+	__shared__ float r_s[2][NW];
+	const int g = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z, tid = threadIdx.x, lane = tid & 63,
+	          wave = tid >> 6;
+	const int G = H / KVH;
+	const int pos = posv[sq];
+	if (pos < 0 || pos >= max_seq) return;
+	const int nact = pos / kChunk + 1;
+	const float *grp = part + ((size_t)(sq * KVH + kvh) * max_chunks * kMaxG + g) * REC;
+	float mx = -INFINITY;
+	for (int cc = tid; cc < nact; cc += HD) mx = __builtin_fmaxf(mx, grp[cc * CS + HD]);
+	mx = wave_max(mx);
+	if (lane == 0) r_s[0][wave] = mx;
 	__syncthreads();
-	constexpr int PER = kMaxG * HD / 256;   // (head, dim) outputs per thread
-	float acc[PER];
+	mx = r_s[0][0];
 #pragma unroll
-	for (int k = 0; k < PER; k++) acc[k] = 0.0f;
-	for (int c0 = 0; c0 < nact; c0 += kChunk) {
-		const int nc = min(kChunk, nact - c0);
-		__syncthreads();   // s_s of the previous batch is consumed
-		for (int t = tid; t < G * kChunk; t += 256) {
-			const int g = t / kChunk, cc = t - g * kChunk;
-			if (cc < nc) s_s[g][cc] = expf(grp[((size_t)(c0 + cc) * kMaxG + g) * REC + HD] - ml_s[g][0]) * ml_s[g][1];
-		}
+	for (int w = 1; w < NW; w++) mx = __builtin_fmaxf(mx, r_s[0][w]);
+	float lsum = 0.0f;
+	for (int cc = tid; cc < nact; cc += HD) lsum += grp[cc * CS + HD + 1] * expf(grp[cc * CS + HD] - mx);
+	lsum = wave_sum(lsum);
+	if (lane == 0) r_s[1][wave] = lsum;
+	__syncthreads();
+	lsum = r_s[1][0];
+#pragma unroll
+	for (int w = 1; w < NW; w++) lsum += r_s[1][w];
+	const float inv = 1.0f / lsum;
+	float acc = 0.0f;
+	for (int c0 = 0; c0 < nact; c0 += HD) {
+		const int nc = min(HD, nact - c0);
+		__syncthreads();   // w_s of the previous batch is consumed
+		if (tid < nc) w_s[tid] = expf(grp[(c0 + tid) * CS + HD] - mx) * inv;
 		__syncthreads();
+		const float *r = grp + c0 * CS + tid;
+		int cc = 0;
+		for (; cc + 8 <= nc; cc += 8) {
+			float o[8];
 #pragma unroll
-		for (int k = 0; k < PER; k++) {
-			const int t = tid + 256 * k, g = t / HD, d = t - g * HD;
-			if (g < G) {
-				const float *r = grp + ((size_t)c0 * kMaxG + g) * REC + d;
-				int cc = 0;
-				for (; cc + 8 <= nc; cc += 8) {
-					float o[8];
+			for (int j = 0; j < 8; j++) o[j] = r[(cc + j) * CS];
 #pragma unroll
-					for (int j = 0; j < 8; j++) o[j] = r[(size_t)(cc + j) * kMaxG * REC];
-#pragma unroll
-					for (int j = 0; j < 8; j++) acc[k] = __builtin_fmaf(o[j], s_s[g][cc + j], acc[k]);
-				}
-				for (; cc < nc; cc++) acc[k] = __builtin_fmaf(r[(size_t)cc * kMaxG * REC], s_s[g][cc], acc[k]);
-			}
+			for (int j = 0; j < 8; j++) acc = __builtin_fmaf(o[j], w_s[cc + j], acc);
 		}
+		for (; cc < nc; cc++) acc = __builtin_fmaf(r[cc * CS], w_s[cc], acc);
 	}
-#pragma unroll
-	for (int k = 0; k < PER; k++) {
-		const int t = tid + 256 * k, g = t / HD, d = t - g * HD;
-		if (g < G) att[(size_t)sq * D + (size_t)(kvh * G + g) * HD + d] = acc[k];
-	}
-	if (tid == 0) atomicExch(&cnt[sq * KVH + kvh], 0);   // ready for the next step
+	att[(size_t)sq * H * HD + (size_t)(kvh * G + g) * HD + tid] = acc;
 }
 
 // ── greedy pick (reference src/sample.c:28-32) ──
@@ -589,13 +578,11 @@ __device__ __forceinline__ void argmax_wave(float &v, int &i) {
 	}
 }
 
-// Grid (kArgBlocks, n_seq). The last block of a sequence writes the token,
-// appends it to the ring and advances the position.
-__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int V, int *tok, int *posv,
-                                                     int *ring, int ring_len, int *nout, float2 *part, int *cnt) {
+// Grid (kArgBlocks, n_seq): each block's best (value, index) of its slice.
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float *__restrict__ logits, int V,
+                                                          float2 *__restrict__ part) {
 	__shared__ float bv_s[4];
 	__shared__ int bi_s[4];
-	__shared__ int last_s;
 	const int b = blockIdx.x, sq = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 	const float *lg = logits + (size_t)sq * V;
 	const int i0 = (int)((int64_t)b * V / kArgBlocks), i1 = (int)((int64_t)(b + 1) * V / kArgBlocks);
@@ -619,12 +606,14 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ l
 				bi = bi_s[w];
 			}
 		part[sq * kArgBlocks + b] = make_float2(bv, __builtin_bit_cast(float, bi));
-		__threadfence();
-		last_s = atomicAdd(&cnt[sq], 1) == kArgBlocks - 1;
 	}
-	__syncthreads();
-	if (!last_s || wave != 0) return;
-	__threadfence();
+}
+
+// Grid (n_seq), one wave: the token of the blocks' best, appended to the ring;
+// the position advances.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float2 *__restrict__ part, int *tok, int *posv,
+                                                          int *ring, int ring_len, int *nout) {
+	const int sq = blockIdx.x, lane = threadIdx.x;
 	const float2 p = part[sq * kArgBlocks + lane];
 	float v = p.x;
 	int i = __builtin_bit_cast(int, p.y);
@@ -636,7 +625,6 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ l
 		if (n < ring_len) ring[(size_t)sq * ring_len + n] = t;
 		nout[sq] = n + 1;
 		posv[sq] += 1;
-		atomicExch(&cnt[sq], 0);
 	}
 }
 
@@ -667,12 +655,11 @@ struct hako_gpu_decoder {
 	float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *g = nullptr, *u = nullptr,
 	      *tmp = nullptr, *logits = nullptr, *part = nullptr, *kc = nullptr, *vc = nullptr;
 	float2 *rope = nullptr, *apart = nullptr;
-	int *tok = nullptr, *pos = nullptr, *acnt = nullptr, *mcnt = nullptr, *ring = nullptr, *nout = nullptr;
+	int *tok = nullptr, *pos = nullptr, *ring = nullptr, *nout = nullptr;
 	// batched steps (n_seq > 1): q8 and fp16 hi/lo activations, split-K state
 	int8_t *xq = nullptr;
 	float *xs = nullptr, *esc = nullptr, *skpart = nullptr;
 	_Float16 *xh = nullptr, *xl = nullptr;
-	int *skcnt = nullptr;
 	std::vector<void *> allocs;
 	hipGraphExec_t exec = nullptr;
 	hipGraph_t graph = nullptr;
@@ -726,6 +713,41 @@ int add(float *x, const float *y, int n) {
 	return HAKO_GPU_OK;
 }
 
+// Attention of layer l for every sequence: chunk records, then their merge.
+int attention(hako_gpu_decoder *d, int l) {
+	const hako_gpu_model &m = d->m;
+	const int KV = d->kv_dim, HD = m.head_dim, G = m.n_heads / m.n_kv_heads;
+	const float scale = 1.0f / sqrtf((float)HD);
+	const size_t kv_seq_stride = (size_t)m.n_layers * d->max_seq * KV;
+	float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
+	const dim3 ag(d->max_chunks, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
+	if (HD == 128) {
+		hipLaunchKernelGGL(attn_kernel<128>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
+		HK_LAUNCHED("attention");
+		hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->part, d->pos, d->att, m.n_heads,
+		                   m.n_kv_heads, d->max_seq, d->max_chunks);
+	} else {
+		hipLaunchKernelGGL(attn_kernel<64>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
+		HK_LAUNCHED("attention");
+		hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->part, d->pos, d->att, m.n_heads,
+		                   m.n_kv_heads, d->max_seq, d->max_chunks);
+	}
+	HK_LAUNCHED("attention merge");
+	return HAKO_GPU_OK;
+}
+
+int argmax(hako_gpu_decoder *d) {
+	hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgBlocks, d->n_seq), dim3(256), 0, stream(), d->logits, d->m.vocab,
+	                   d->apart);
+	HK_LAUNCHED("argmax");
+	hipLaunchKernelGGL(argmax_final_kernel, dim3(d->n_seq), dim3(64), 0, stream(), d->apart, d->tok, d->pos, d->ring,
+	                   d->max_seq, d->nout);
+	HK_LAUNCHED("argmax final");
+	return HAKO_GPU_OK;
+}
+
 int rmsnorm_q8(hako_gpu_decoder *d, const float *x, const float *w, int n) {
 	hipLaunchKernelGGL(rmsnorm_q8_kernel, dim3(d->n_seq), dim3(256), 0, stream(), x, w, d->m.rms_eps, d->xq, d->xs, n);
 	HK_LAUNCHED("rmsnorm_q8");
@@ -749,12 +771,10 @@ bool batched_ok(const hako_gpu_model &m, const std::vector<hako_gpu_block> &bloc
 // streams the weights once for all sequences.
 int enqueue_batched_step(hako_gpu_decoder *d) {
 	const hako_gpu_model &m = d->m;
-	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, HD = m.head_dim, M = d->n_seq;
+	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, M = d->n_seq;
 	hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
 	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
 	HK_LAUNCHED("embed");
-	const float scale = 1.0f / sqrtf((float)HD);
-	const size_t kv_seq_stride = (size_t)m.n_layers * d->max_seq * KV;
 	for (int l = 0; l < m.n_layers; l++) {
 		const hako_gpu_block &B = d->blocks[l];
 		// 1. q, k, v for every sequence: rows [q | k | v] of qkv[t][D + 2KV]
@@ -766,17 +786,7 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 		s.s[2] = {(const uint8_t *)B.wv, B.bv, d->qkv + D + KV, D + KV, KV, d->qkv_dim};
 		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, D + 2 * KV)) return rc;
 		// 2. attention, one grid over every sequence
-		float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
-		const dim3 ag(d->max_chunks, m.n_kv_heads, M);
-		if (HD == 128)
-			hipLaunchKernelGGL(attn_kernel<128>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
-			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride,
-			                   d->qkv_dim, scale);
-		else
-			hipLaunchKernelGGL(attn_kernel<64>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
-			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride,
-			                   d->qkv_dim, scale);
-		HK_LAUNCHED("attention");
+		if (int rc = attention(d, l)) return rc;
 		// 3. output projection added into the residual stream
 		if (int rc = rmsnorm_q8(d, d->att, nullptr, D)) return rc;
 		s = SkSegs{};
@@ -795,7 +805,7 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 		s = SkSegs{};
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.down, nullptr, d->x, 0, D, D};
-		if (int rc = q6k_skinny(s, kSkAdd, d->xh, d->xl, d->esc, M, F, D, d->skpart, d->skcnt)) return rc;
+		if (int rc = q6k_skinny(s, kSkAdd, d->xh, d->xl, d->esc, M, F, D, d->skpart)) return rc;
 	}
 	SkSegs s{};
 	s.n = 1;
@@ -806,11 +816,9 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 	} else {
 		if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, M)) return rc;
 		if (int rc = f16_split(d->xn, d->xh, d->xl, d->esc, M, D)) return rc;
-		if (int rc = q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, D, m.vocab, d->skpart, d->skcnt)) return rc;
+		if (int rc = q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, D, m.vocab, d->skpart)) return rc;
 	}
-	hipLaunchKernelGGL(argmax_kernel, dim3(kArgBlocks, M), dim3(256), 0, stream(), d->logits, m.vocab, d->tok, d->pos,
-	                   d->ring, d->max_seq, d->nout, d->apart, d->mcnt);
-	HK_LAUNCHED("argmax");
+	if (int rc = argmax(d)) return rc;
 	return HAKO_GPU_OK;
 }
 
@@ -818,12 +826,10 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 int enqueue_step(hako_gpu_decoder *d) {
 	if (d->n_seq > 1) return enqueue_batched_step(d);
 	const hako_gpu_model &m = d->m;
-	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, HD = m.head_dim;
+	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim;
 	hipLaunchKernelGGL(embed_kernel, dim3(d->n_seq), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
 	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
 	HK_LAUNCHED("embed");
-	const float scale = 1.0f / sqrtf((float)HD);
-	const size_t kv_seq_stride = (size_t)m.n_layers * d->max_seq * KV;
 	for (int l = 0; l < m.n_layers; l++) {
 		const hako_gpu_block &B = d->blocks[l];
 		float *q = d->qkv, *k = d->qkv + D, *v = d->qkv + D + KV;
@@ -844,17 +850,7 @@ int enqueue_step(hako_gpu_decoder *d) {
 			if (int rc = hako_gpu_matmul(v, d->xn, B.t_v, B.wv, B.bv, KV, D)) return rc;
 		}
 		// 2. rope, cache append, attention
-		float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
-		const dim3 ag(d->max_chunks, m.n_kv_heads, d->n_seq);
-		if (HD == 128)
-			hipLaunchKernelGGL(attn_kernel<128>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
-			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim,
-			                   scale);
-		else
-			hipLaunchKernelGGL(attn_kernel<64>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
-			                   d->acnt, d->att, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim,
-			                   scale);
-		HK_LAUNCHED("attention");
+		if (int rc = attention(d, l)) return rc;
 		// 3. output projection + residual
 		if (B.t_o == HAKO_TYPE_Q4_K && fusable_q4(D) && D % rpw == 0) {
 			DecSegs s{};
@@ -889,9 +885,7 @@ int enqueue_step(hako_gpu_decoder *d) {
 	}
 	if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, 1)) return rc;
 	if (int rc = hako_gpu_matmul(d->logits, d->xn, m.t_out, m.out_weight, nullptr, m.vocab, D)) return rc;
-	hipLaunchKernelGGL(argmax_kernel, dim3(kArgBlocks, d->n_seq), dim3(256), 0, stream(), d->logits, m.vocab, d->tok,
-	                   d->pos, d->ring, d->max_seq, d->nout, d->apart, d->mcnt);
-	HK_LAUNCHED("argmax");
+	if (int rc = argmax(d)) return rc;
 	return HAKO_GPU_OK;
 }
 
@@ -997,14 +991,11 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	HK_ALLOC(d->apart, sizeof(float2) * n_seq * kArgBlocks);
 	HK_ALLOC(d->tok, sizeof(int) * n_seq);
 	HK_ALLOC(d->pos, sizeof(int) * n_seq);
-	HK_ALLOC(d->acnt, sizeof(int) * n_seq * m->n_kv_heads);
-	HK_ALLOC(d->mcnt, sizeof(int) * n_seq);
 	HK_ALLOC(d->ring, sizeof(int) * n_seq * max_seq);
 	HK_ALLOC(d->nout, sizeof(int) * n_seq);
 	const int DF = F > D ? F : D;
 	size_t skpart = q6k_skinny_part_floats(F, D), sk2 = q6k_skinny_part_floats(D, m->vocab);
 	skpart = skpart > sk2 ? skpart : sk2;
-	const int sktiles = (m->vocab > D ? m->vocab : D) / 64 + 1;
 	if (n_seq > 1) {
 		HK_ALLOC(d->xq, (size_t)n_seq * D);
 		HK_ALLOC(d->xs, sizeof(float) * n_seq * (D / 32));
@@ -1012,7 +1003,6 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 		HK_ALLOC(d->xl, sizeof(_Float16) * n_seq * DF);
 		HK_ALLOC(d->esc, sizeof(float) * n_seq);
 		HK_ALLOC(d->skpart, sizeof(float) * (skpart ? skpart : 1));
-		HK_ALLOC(d->skcnt, sizeof(int) * sktiles);
 	}
 #undef HK_ALLOC
 	if (rc) {
@@ -1030,11 +1020,8 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	hipError_t e = hipMemcpy(d->rope, rope.data(), sizeof(float2) * rope.size(), hipMemcpyHostToDevice);
 	if (e == hipSuccess) e = hipMemset(d->kc, 0, sizeof(float) * kvn);
 	if (e == hipSuccess) e = hipMemset(d->vc, 0, sizeof(float) * kvn);
-	if (e == hipSuccess) e = hipMemset(d->acnt, 0, sizeof(int) * n_seq * m->n_kv_heads);
-	if (e == hipSuccess) e = hipMemset(d->mcnt, 0, sizeof(int) * n_seq);
 	if (e == hipSuccess) e = hipMemset(d->pos, 0, sizeof(int) * n_seq);
 	if (e == hipSuccess) e = hipMemset(d->nout, 0, sizeof(int) * n_seq);
-	if (e == hipSuccess && d->skcnt) e = hipMemset(d->skcnt, 0, sizeof(int) * sktiles);
 	if (e == hipSuccess) e = hipDeviceSynchronize();
 	if (e != hipSuccess) {
 		hako_gpu_decoder_destroy(d);

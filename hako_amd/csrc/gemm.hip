@@ -407,28 +407,14 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 	}
 }
 
-// Split-K counters and partials of the skinny Q6_K kernel in library
-// workspace slot 5: counters first (one int per 64-row tile), zeroed when the
-// slot is (re)allocated or the counter region grows, and left zero by every
-// launch, so calls captured in a graph need no clearing.
-int skinny_split_workspace(int n_in, int n_out, float **part, int **cnt) {
+// Split-K partials of the skinny Q6_K matmul (workspace slot 5).
+int skinny_split_workspace(int n_in, int n_out, float **part) {
 	*part = nullptr;
-	*cnt = nullptr;
 	const size_t pf = q6k_skinny_part_floats(n_in, n_out);
 	if (!pf) return HAKO_GPU_OK;
-	const size_t tiles = (size_t)(n_out + 63) / 64;
-	const size_t cnt_bytes = (tiles * 4 + 255) & ~(size_t)255;
-	static void *zero_base = nullptr;
-	static size_t zero_bytes = 0;
 	void *ws = nullptr;
-	if (int rc = workspace(5, cnt_bytes + pf * 4, &ws)) return rc;
-	if (ws != zero_base || zero_bytes < cnt_bytes) {
-		HK_HIP(hipMemsetAsync(ws, 0, cnt_bytes, stream()));
-		zero_base = ws;
-		zero_bytes = cnt_bytes;
-	}
-	*cnt = (int *)ws;
-	*part = (float *)((uint8_t *)ws + cnt_bytes);
+	if (int rc = workspace(5, pf * 4, &ws)) return rc;
+	*part = (float *)ws;
 	return HAKO_GPU_OK;
 }
 
@@ -490,9 +476,8 @@ int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, 
 		segs.n = 1;
 		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
 		float *part = nullptr;
-		int *cnt = nullptr;
-		if (int rc = skinny_split_workspace(n_in, n_out, &part, &cnt)) return rc;
-		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part, cnt)) return rc;
+		if (int rc = skinny_split_workspace(n_in, n_out, &part)) return rc;
+		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part)) return rc;
 		return ok();
 	}
 	hipLaunchKernelGGL(q6k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,

@@ -36,14 +36,13 @@ int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, i
 size_t q4k_skinny_lds(int n_in);
 // Q6_K x fp32 as fp16 hi/lo rows [m][n_in] with per-row powers of two esc[m];
 // Store or Add epilogue. Long rows are split along K over several
-// workgroups: `part` (q6k_skinny_part_floats floats) holds their results and
-// `cnt` (one int per 64-row tile, zero before the first launch, left zero
-// by every launch) counts them in.
+// workgroups: `part` (q6k_skinny_part_floats floats) holds their results,
+// summed by a second launch that applies the epilogue.
 constexpr int kSkTargetWgs = 512;
 int q6k_skinny_splits(int n_in, int vrows);
 size_t q6k_skinny_part_floats(int n_in, int vrows);
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
-               int n_in, int vrows, float *part, int *cnt);
+               int n_in, int vrows, float *part);
 // The fp16 hi/lo split of m fp32 rows of n floats (gemm.hip).
 int f16_split(const float *x, _Float16 *xh, _Float16 *xl, float *esc, int m, int n);
 

@@ -259,17 +259,16 @@ struct Q6SkBuf {
 
 // Workgroup (row tile, K split): the tile's 64 rows over super-blocks
 // [kb_beg, kb_end). With nsplit > 1 the splits' results go to `part`
-// ([nsplit][16][vrows]) and the last split of a tile to finish (counter in
-// cnt[tile], reset by that workgroup) sums them in split order and applies
-// the epilogue.
+// ([nsplit][16][vrows]) and skinny_reduce_kernel, launched next, sums them in
+// split order and applies the epilogue (a kernel boundary instead of a
+// device-scope fence in every workgroup).
 template <int EPI>
 __global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Float16 *__restrict__ xh,
                                                         const _Float16 *__restrict__ xl,
                                                         const float *__restrict__ esc, int M, int K, int vrows,
-                                                        int nsplit, float *part, int *cnt) {
+                                                        int nsplit, float *__restrict__ part) {
 	__shared__ __align__(16) _Float16 ah_s[2][16 * kHPadSk];
 	__shared__ __align__(16) _Float16 al_s[2][16 * kHPadSk];
-	__shared__ int last_s;
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment and descriptors in SGPRs
 	const int j = lane & 15, kq = lane >> 4;
@@ -374,24 +373,31 @@ __global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Floa
 #pragma unroll
 	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? acc[v] * esc[t0 + v] : 0.0f;
 	if (nsplit > 1) {
+		// tokens past M hold zeros; skinny_reduce_kernel sums the splits
 		if (ok)
 #pragma unroll
 			for (int v = 0; v < 4; v++) part[((size_t)split * 16 + t0 + v) * vrows + vrow] = y[v];
-		__threadfence();
-		__syncthreads();
-		if (tid == 0) last_s = atomicAdd(&cnt[tile], 1) == nsplit - 1;
-		__syncthreads();
-		if (!last_s) return;
-		__threadfence();
-#pragma unroll
-		for (int v = 0; v < 4; v++) y[v] = 0.0f;
-		if (ok)
-			for (int sp = 0; sp < nsplit; sp++)
-#pragma unroll
-				for (int v = 0; v < 4; v++) y[v] += part[((size_t)sp * 16 + t0 + v) * vrows + vrow];
-		if (tid == 0) atomicExch(&cnt[tile], 0);   // ready for the next launch
+		return;
 	}
 	skinny_epilogue(EPI, S, vrow, ok, y, M, lane);
+}
+
+// Grid (ceil(vrows/256), M): out[t][row] = sum over splits, in split order,
+// then the epilogue of the row's segment.
+template <int EPI>
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(SkSegs segs, const float *__restrict__ part, int nsplit,
+                                                            int vrows) {
+	const int vrow = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+	if (vrow >= vrows) return;
+	float y = 0.0f;
+	for (int sp = 0; sp < nsplit; sp++) y += part[((size_t)sp * 16 + t) * vrows + vrow];
+	const SegView S = seg_of(segs, vrow, false);
+	const int r = vrow - S.row0;
+	float *o = S.out + (size_t)t * S.ld + r;
+	if (EPI == kSkAdd)
+		*o += y;
+	else
+		*o = y + (S.bias ? S.bias[r] : 0.0f);
 }
 
 }  // namespace
@@ -433,18 +439,26 @@ size_t q6k_skinny_part_floats(int n_in, int vrows) {
 }
 
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
-               int n_in, int vrows, float *part, int *cnt) {
+               int n_in, int vrows, float *part) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
 	const int ns = q6k_skinny_splits(n_in, vrows);
-	if (ns > 1 && (!part || !cnt)) return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace");
+	if (ns > 1 && !part) return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace");
 	const dim3 grid(tiles * ns);
 	if (epi == kSkStore)
 		hipLaunchKernelGGL(q6k_skinny_kernel<kSkStore>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
-		                   vrows, ns, part, cnt);
+		                   vrows, ns, part);
 	else
 		hipLaunchKernelGGL(q6k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
-		                   vrows, ns, part, cnt);
+		                   vrows, ns, part);
 	HK_LAUNCHED("q6k_skinny");
+	if (ns > 1) {
+		const dim3 rg((vrows + 255) / 256, m);
+		if (epi == kSkStore)
+			hipLaunchKernelGGL(skinny_reduce_kernel<kSkStore>, rg, dim3(256), 0, stream(), segs, part, ns, vrows);
+		else
+			hipLaunchKernelGGL(skinny_reduce_kernel<kSkAdd>, rg, dim3(256), 0, stream(), segs, part, ns, vrows);
+		HK_LAUNCHED("skinny_reduce");
+	}
 	return HAKO_GPU_OK;
 }
 

@@ -145,3 +145,32 @@ def test_batched_rejects_other_weight_mixes(gpu, tmp_path):
     with pytest.raises(HakoGpuError, match="sequences"):
         Decoder(gpu, path, n_seq=17, max_seq=64)
     Decoder(gpu, path, n_seq=1, max_seq=64).close()   # one sequence takes any mix
+
+
+def test_qwen2_7b_sixteen_sequences(gpu, ref, tmp_path):
+    """The full Qwen2-7B shape (28 layers, d_model 3584, 28/4 heads, ffn
+    18944, untied Q6_K output 152064 x 3584) with 16 sequences at their own
+    prefilled positions: every sequence's greedy tokens equal the reference's
+    run of that sequence alone, and its logits are within 2e-3."""
+    from dropin import prefilled_greedy
+    from hako_amd.decoder import Decoder
+    cfg = mlf2.QWEN2_7B
+    path = str(tmp_path / "qwen2_7b.mlf2")
+    mlf2.write_qwen2(path, cfg, 41)
+    n_seq, max_seq, steps = 16, 160, 3
+    pos, starts, kvs = seq_setup(cfg, n_seq, 41, 120)
+    dec = Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
+    try:
+        fill_kv(gpu, dec, kvs, cfg.n_layers)
+        dec.set_pos(pos)
+        first, lg = dec.step(starts, logits=True)
+        rest = dec.generate(first, steps - 1)
+    finally:
+        dec.close()
+    got = np.concatenate([first[None], rest])
+    for s in range(n_seq):
+        want, want_logits = prefilled_greedy(ref, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=steps,
+                                             vocab=cfg.vocab, max_seq=max_seq)
+        assert np.all(np.isfinite(want_logits))
+        assert got[:, s].tolist() == want, f"sequence {s} (position {pos[s]})"
+        assert maxabs_rel(lg[s], want_logits[0]) < 2e-3, f"sequence {s}"
