@@ -758,7 +758,7 @@ int rmsnorm_q8(hako_gpu_decoder *d, const float *x, const float *w, int n) {
 // gate/up, Q6_K down, Q4_K or Q6_K lm_head; d_model, ffn_dim <= 4096 /
 // any, kv_dim a multiple of 16.
 bool batched_ok(const hako_gpu_model &m, const std::vector<hako_gpu_block> &blocks, int kv_dim) {
-	if (m.d_model > kSkMaxQ4In || kv_dim % 16 || m.d_model % 16) return false;
+	if (kv_dim % 16 || m.d_model % 16) return false;
 	if (m.t_out != HAKO_TYPE_Q4_K && m.t_out != HAKO_TYPE_Q6_K) return false;
 	for (const hako_gpu_block &B : blocks)
 		if (B.t_q != HAKO_TYPE_Q4_K || B.t_k != HAKO_TYPE_Q4_K || B.t_v != HAKO_TYPE_Q4_K || B.t_o != HAKO_TYPE_Q4_K ||
@@ -784,7 +784,7 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 		s.s[0] = {(const uint8_t *)B.wq, B.bq, d->qkv, 0, D, d->qkv_dim};
 		s.s[1] = {(const uint8_t *)B.wk, B.bk, d->qkv + D, D, KV, d->qkv_dim};
 		s.s[2] = {(const uint8_t *)B.wv, B.bv, d->qkv + D + KV, D + KV, KV, d->qkv_dim};
-		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, D + 2 * KV)) return rc;
+		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, D + 2 * KV, d->skpart)) return rc;
 		// 2. attention, one grid over every sequence
 		if (int rc = attention(d, l)) return rc;
 		// 3. output projection added into the residual stream
@@ -792,14 +792,14 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 		s = SkSegs{};
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D, D};
-		if (int rc = q4k_skinny(s, kSkAdd, d->xq, d->xs, M, D, D)) return rc;
+		if (int rc = q4k_skinny(s, kSkAdd, d->xq, d->xs, M, D, D, d->skpart)) return rc;
 		// 4. gate, up, SwiGLU
 		if (int rc = rmsnorm_q8(d, d->x, B.ffn_norm, D)) return rc;
 		s = SkSegs{};
 		s.n = 2;
 		s.s[0] = {(const uint8_t *)B.gate, nullptr, d->h, 0, F, F};
-		s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, 0, F, F};
-		if (int rc = q4k_skinny(s, kSkSwiGLU, d->xq, d->xs, M, D, 2 * F)) return rc;
+		s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, F, F, F};
+		if (int rc = q4k_skinny(s, kSkSwiGLU, d->xq, d->xs, M, D, 2 * F, d->skpart)) return rc;
 		// 5. down projection added into the residual stream
 		if (int rc = f16_split(d->h, d->xh, d->xl, d->esc, M, F)) return rc;
 		s = SkSegs{};
@@ -812,7 +812,7 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 	s.s[0] = {(const uint8_t *)m.out_weight, nullptr, d->logits, 0, m.vocab, m.vocab};
 	if (m.t_out == HAKO_TYPE_Q4_K) {
 		if (int rc = rmsnorm_q8(d, d->x, m.out_norm, D)) return rc;
-		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, m.vocab)) return rc;
+		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, m.vocab, d->skpart)) return rc;
 	} else {
 		if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, M)) return rc;
 		if (int rc = f16_split(d->xn, d->xh, d->xl, d->esc, M, D)) return rc;
@@ -961,8 +961,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 		delete d;
 		return set_error(HAKO_GPU_ETYPE,
 		                 "batched decode (n_seq > 1) runs the Q4_K_M mix (Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or "
-		                 "Q6_K output) with d_model <= %d",
-		                 kSkMaxQ4In);
+		                 "Q6_K output) with d_model and n_kv_heads*head_dim multiples of 16");
 	}
 	d->m.blocks = nullptr;
 	d->n_seq = n_seq;
@@ -994,8 +993,14 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	HK_ALLOC(d->ring, sizeof(int) * n_seq * max_seq);
 	HK_ALLOC(d->nout, sizeof(int) * n_seq);
 	const int DF = F > D ? F : D;
-	size_t skpart = q6k_skinny_part_floats(F, D), sk2 = q6k_skinny_part_floats(D, m->vocab);
-	skpart = skpart > sk2 ? skpart : sk2;
+	// split-K partials of the largest skinny matmul of a step
+	size_t skpart = 0;
+	const int qkv_rows = D + 2 * d->kv_dim;
+	const size_t needs[6] = {q4k_skinny_part_floats(D, qkv_rows, kSkStore), q4k_skinny_part_floats(D, D, kSkAdd),
+	                         q4k_skinny_part_floats(D, 2 * F, kSkSwiGLU), q6k_skinny_part_floats(F, D),
+	                         m->t_out == HAKO_TYPE_Q4_K ? q4k_skinny_part_floats(D, m->vocab, kSkStore) : 0,
+	                         m->t_out == HAKO_TYPE_Q6_K ? q6k_skinny_part_floats(D, m->vocab) : 0};
+	for (size_t nf : needs) skpart = nf > skpart ? nf : skpart;
 	if (n_seq > 1) {
 		HK_ALLOC(d->xq, (size_t)n_seq * D);
 		HK_ALLOC(d->xs, sizeof(float) * n_seq * (D / 32));

@@ -407,13 +407,12 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 	}
 }
 
-// Split-K partials of the skinny Q6_K matmul (workspace slot 5).
-int skinny_split_workspace(int n_in, int n_out, float **part) {
+// Split-K partials of the skinny matmuls (workspace slot 5).
+int skinny_split_workspace(size_t floats, float **part) {
 	*part = nullptr;
-	const size_t pf = q6k_skinny_part_floats(n_in, n_out);
-	if (!pf) return HAKO_GPU_OK;
+	if (!floats) return HAKO_GPU_OK;
 	void *ws = nullptr;
-	if (int rc = workspace(5, pf * 4, &ws)) return rc;
+	if (int rc = workspace(5, floats * 4, &ws)) return rc;
 	*part = (float *)ws;
 	return HAKO_GPU_OK;
 }
@@ -441,11 +440,13 @@ int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const f
 	if (int rc = check_gemm("Q4_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ4Bytes, w)) return rc;
 	if (((uintptr_t)w & 15) || ((uintptr_t)xq & 15) || ((uintptr_t)xs & 3))
 		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM needs w and xq 16-byte aligned");
-	if (m <= kSkMaxTokens && n_in <= kSkMaxQ4In) {   // a few tokens: the skinny kernel
+	if (m <= kSkMaxTokens) {   // a few tokens: the skinny kernel
 		SkSegs segs{};
 		segs.n = 1;
 		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
-		if (int rc = q4k_skinny(segs, kSkStore, xq, xs, m, n_in, n_out)) return rc;
+		float *part = nullptr;
+		if (int rc = skinny_split_workspace(q4k_skinny_part_floats(n_in, n_out, kSkStore), &part)) return rc;
+		if (int rc = q4k_skinny(segs, kSkStore, xq, xs, m, n_in, n_out, part)) return rc;
 		return ok();
 	}
 	hipLaunchKernelGGL(q4k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
@@ -476,7 +477,7 @@ int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, 
 		segs.n = 1;
 		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
 		float *part = nullptr;
-		if (int rc = skinny_split_workspace(n_in, n_out, &part)) return rc;
+		if (int rc = skinny_split_workspace(q6k_skinny_part_floats(n_in, n_out), &part)) return rc;
 		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part)) return rc;
 		return ok();
 	}

@@ -8,18 +8,25 @@
 // rows (B operand), so every lane owns one row (l % 16) and keeps that row's
 // scales to itself, and holds four tokens (4*(l/16) + v) of the output.
 //
+// A workgroup (4 waves, 64 rows) takes a range of at most a few
+// super-blocks of K: its activations fit a small LDS stage and its weight
+// loads a few registers per lane, so several workgroups share a CU and keep
+// enough bytes in flight. When K is split over several workgroups their
+// partial results go to a buffer that skinny_reduce_kernel sums in split
+// order, applying the epilogue (a kernel boundary, not a device-scope fence
+// per workgroup, makes the partials visible).
+//
 // Q4_K x q8 (src/quant.c:150-232 per token and row): one
 // v_mfma_i32_16x16x32_i8 per 32-wide sub-block gives the exact per-sub-block
 // sums iqx; they are folded as iqx*(xs*d*s) on the VALU, and the min term
-// Σ (dmin*m)*(−xs*Σxq) over the block's sub-blocks runs as two
-// v_mfma_f32_16x16x4_f32. The activations (q8_32 of each token row) are
-// staged in LDS once per workgroup.
+// sum over the block's sub-blocks of (dmin*m)*(-xs*sum xq) runs as two
+// v_mfma_f32_16x16x4_f32.
 //
-// Q6_K x fp32 (src/nn.c:84-95): q−32 exact in fp16 against the activation as
+// Q6_K x fp32 (src/nn.c:84-95): q-32 exact in fp16 against the activation as
 // fp16 hi + lo after an exact per-token power-of-two scaling (the prefill
 // GEMM's representation); two v_mfma_f32_16x16x16_f16 per 16-wide scale group
 // then the group sum times d*sc (exact fp32). Activations are staged through
-// LDS two super-blocks at a time, double-buffered.
+// LDS one super-block at a time, double-buffered.
 #include "hako_dev.h"
 #include "hako_rt.h"
 #include "skinny.h"
@@ -85,170 +92,147 @@ __device__ __forceinline__ void skinny_epilogue(int epi, const SegView &S, int v
 
 // ── Q4_K x q8 ──
 
+constexpr int kQ4SkBlocks = 4;                       // super-blocks of K per workgroup at most
+constexpr int kQ4SkRow = kQ4SkBlocks * kQK + kAPadQ4; // bytes per staged token row
+
 struct Q4SkBuf {
 	uint4 h;        // block header of the lane's row
 	uint2 q[4];     // qs bytes 32g + 8(l/16) .. +8 of each 64-weight group g
 };
 
-// Rows of a workgroup: Store / Add — wave w takes 16 consecutive rows of the
-// launch's row space; SwiGLU — the workgroup takes 32 rows r0.., wave w the
-// gate (w even) or up (w odd) rows r0 + 16*(w/2) .., so that each wave
-// streams one matrix through one (uniform) buffer descriptor; the up sums
-// reach the gate waves through LDS.
-template <int EPI, int DEPTH>
+// Workgroup (64-row tile, K split): wave w takes rows 16w.. of the tile over
+// super-blocks [kb_beg, kb_end) (at most kQ4SkBlocks). EPI kSkStore / kSkAdd
+// apply the epilogue directly (one split); kSkPart writes the partial sums
+// to part[split][t][vrow].
+constexpr int kSkPart = 3;
+template <int EPI>
 __global__ __launch_bounds__(kT) void q4k_skinny_kernel(SkSegs segs, const int8_t *__restrict__ xq,
-                                                        const float *__restrict__ xs, int M, int K, int vrows) {
-	extern __shared__ __align__(16) uint8_t smem[];
-	const int KP = K + kAPadQ4, NB = K >> 8, NS = K >> 5;
-	int8_t *a_s = (int8_t *)smem;                           // [16][KP] xq
-	float *xs_s = (float *)(smem + 16 * KP);                // [NS][16] xs
-	float *nu_s = xs_s + NS * 16;                           // [NS][16] -xs*Σxq
-	float *ex_s = nu_s + NS * 16;                           // [4 waves][16 rows][8] d*s per sub-block
-	float *up_s = ex_s + 4 * 16 * 8;                        // [2][16 rows][16 tokens] up sums (SwiGLU)
-	int4 *trash_s = (int4 *)(up_s + 2 * 16 * 16);           // target of the stores with no item
+                                                        const float *__restrict__ xs, int M, int K, int vrows,
+                                                        int nsplit, float *__restrict__ part) {
+	__shared__ __align__(16) int8_t a_s[16 * kQ4SkRow];          // xq of the range, token rows
+	__shared__ __align__(16) float xs_s[kQ4SkBlocks * 8][16];    // xs per (sub-block, token)
+	__shared__ __align__(16) float nu_s[kQ4SkBlocks * 8][16];    // -xs * sum xq
+	__shared__ __align__(16) float ex_s[4][16][8];               // d*s per (wave, row, sub-block)
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment and descriptors in SGPRs
 	const int j = lane & 15, kq = lane >> 4;
-	const bool swiglu = EPI == kSkSwiGLU;
-	const int wrow0 = swiglu ? blockIdx.x * 32 + (wave >> 1) * 16 : (blockIdx.x * 4 + wave) * kRowsWave;
-	const SegView S = seg_of(segs, swiglu ? 0 : wrow0, swiglu);
-	const uint8_t *wbase = swiglu ? ((wave & 1) ? segs.s[1].w : segs.s[0].w) : S.w;
-	const int srows = swiglu ? segs.s[0].rows : S.rows;
-	const int wr = swiglu ? wrow0 + j : wrow0 + j - S.row0;   // this lane's row of its matrix
-	const bool ok = wr < srows && (swiglu || wrow0 + j < vrows);
+	const int NB = K >> 8, NS = K >> 5;
+	const int tile = blockIdx.x / nsplit, split = blockIdx.x - tile * nsplit;
+	const int kb_beg = (int)((int64_t)split * NB / nsplit), kb_end = (int)((int64_t)(split + 1) * NB / nsplit);
+	const int nbk = kb_end - kb_beg;
+	const int wrow0 = (tile * 4 + wave) * kRowsWave;
+	const SegView S = seg_of(segs, wrow0, false);
+	const int vrow = wrow0 + j, wr = vrow - S.row0;
+	const bool ok = vrow < vrows && wr < S.rows;
 	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
-	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(wbase, (uint32_t)srows * rb);
+	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, (uint32_t)S.rows * rb);
 	const uint32_t row_off = ok ? (uint32_t)wr * rb : kBufNone;
 
-	// 1. the first DEPTH super-blocks' weight loads (every one of the row when
-	//    n_in <= 256*DEPTH), before the activation staging
-	constexpr int kQ4Depth = DEPTH;
-	Q4SkBuf buf[kQ4Depth];
-	auto issue = [&](Q4SkBuf &b, int kb) {
-		const uint32_t o = kb < NB ? row_off + (uint32_t)kb * kQ4Bytes : kBufNone;
-		b.h = ld_b128(wrs, o);
+	// 1. every weight load of the range, then the activation staging
+	Q4SkBuf buf[kQ4SkBlocks];
 #pragma unroll
-		for (int g = 0; g < 4; g++) b.q[g] = ld_b64(wrs, o + 16 + 32 * g + 8 * kq);
-	};
+	for (int d = 0; d < kQ4SkBlocks; d++) {
+		const uint32_t o = d < nbk ? row_off + (uint32_t)(kb_beg + d) * kQ4Bytes : kBufNone;
+		buf[d].h = ld_b128(wrs, o);
 #pragma unroll
-	for (int d = 0; d < kQ4Depth; d++) issue(buf[d], d);
+		for (int g = 0; g < 4; g++) buf[d].q[g] = ld_b64(wrs, o + 16 + 32 * g + 8 * kq);
+	}
 	__builtin_amdgcn_sched_barrier(0);
-
-	// 2. activations: xq rows (zeros past M), xs, and -xs*Σxq per sub-block.
-	//    Buffer loads answer items past the data with zeros, and items past
-	//    the work store into a trash slot, so no load sits behind a branch and
-	//    the staging costs one L2 round trip.
-	constexpr int kXqPer = 16 * kSkMaxQ4In / 16 / kT;   // int4 of xq per thread at most
-	constexpr int kXsPer = 16 * kSkMaxQ4In / 32 / kT;   // xs per thread at most
-	const int nq = 16 * (K >> 4), nsv = 16 * NS;
+	// 16 tokens x 64 pieces of 16 bytes (4 blocks), zeros past M or the range
 	const __amdgpu_buffer_rsrc_t qrs = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
 	const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
-	uint4 qv[kXqPer];
-	float sv[kXsPer];
+	uint4 qv[4];
+	float sv[2];
 #pragma unroll
-	for (int u = 0; u < kXqPer; u++) {
-		const int c = tid + kT * u, t = c / (K >> 4), p = c - t * (K >> 4);
-		qv[u] = ld_b128(qrs, c < nq ? (uint32_t)t * K + 16u * p : kBufNone);
+	for (int u = 0; u < 4; u++) {
+		const int c = tid + kT * u, t = c >> 6, p = c & 63;
+		qv[u] = ld_b128(qrs, (p < 16 * nbk && t < M) ? (uint32_t)t * K + 256u * kb_beg + 16u * p : kBufNone);
 	}
 #pragma unroll
-	for (int u = 0; u < kXsPer; u++) {
-		const int c = tid + kT * u, t = c / NS, sb = c - t * NS;
-		sv[u] = __builtin_bit_cast(float, ld_b32(srs, c < nsv ? 4u * ((uint32_t)t * NS + sb) : kBufNone));
+	for (int u = 0; u < 2; u++) {
+		const int c = tid + kT * u, t = c >> 5, sb = c & 31;
+		sv[u] = __builtin_bit_cast(float, ld_b32(srs, (sb < 8 * nbk && t < M)
+		                                                  ? 4u * ((uint32_t)t * NS + 8u * kb_beg + sb)
+		                                                  : kBufNone));
 	}
 #pragma unroll
-	for (int u = 0; u < kXqPer; u++) {
-		const int c = tid + kT * u, t = c / (K >> 4), p = c - t * (K >> 4);
-		*(c < nq ? (uint4 *)(a_s + t * KP + 16 * p) : (uint4 *)(trash_s + tid)) = qv[u];
+	for (int u = 0; u < 4; u++) {
+		const int c = tid + kT * u, t = c >> 6, p = c & 63;
+		*(uint4 *)(a_s + t * kQ4SkRow + 16 * p) = qv[u];
 	}
 	__syncthreads();
 #pragma unroll
-	for (int u = 0; u < kXsPer; u++) {
-		const int c = min(tid + kT * u, nsv - 1), t = c / NS, sb = c - t * NS;
-		const int4 *p = (const int4 *)(a_s + t * KP + 32 * sb);
+	for (int u = 0; u < 2; u++) {
+		const int c = tid + kT * u, t = c >> 5, sb = c & 31;
+		const int4 *p = (const int4 *)(a_s + t * kQ4SkRow + 32 * sb);
 		const int4 p0 = p[0], p1 = p[1];
 		int ix = 0;
 		ix = sdot4(p0.x, 0x01010101, ix); ix = sdot4(p0.y, 0x01010101, ix);
 		ix = sdot4(p0.z, 0x01010101, ix); ix = sdot4(p0.w, 0x01010101, ix);
 		ix = sdot4(p1.x, 0x01010101, ix); ix = sdot4(p1.y, 0x01010101, ix);
 		ix = sdot4(p1.z, 0x01010101, ix); ix = sdot4(p1.w, 0x01010101, ix);
-		if (tid + kT * u < nsv) {
-			xs_s[sb * 16 + t] = sv[u];
-			nu_s[sb * 16 + t] = -sv[u] * (float)ix;
-		}
+		xs_s[sb][t] = sv[u];
+		nu_s[sb][t] = -sv[u] * (float)ix;
 	}
 	__syncthreads();
 
+	// 2. per block: (s, m) of sub-blocks kq, kq+4 of the lane's row; d*s to
+	//    the row's other lanes through LDS, dmin*m into the min-term MFMA
 	v4f acc = {0.0f, 0.0f, 0.0f, 0.0f}, accm = {0.0f, 0.0f, 0.0f, 0.0f};
 	const v4i zero = {0, 0, 0, 0};
-	float *ex = ex_s + (wave * 16 + j) * 8;
-	const int8_t *arow = a_s + j * KP + 8 * kq;   // A operand: token j, K-slice 8kq
-	for (int kb0 = 0; kb0 < NB; kb0 += kQ4Depth) {
+	float *ex = &ex_s[wave][j][0];
+	const int8_t *arow = a_s + j * kQ4SkRow + 8 * kq;   // A operand: token j, K-slice 8kq
 #pragma unroll
-		for (int d = 0; d < kQ4Depth; d++) {
-			const int kb = kb0 + d;
-			if (kb < NB) {
-				const Q4SkBuf &b = buf[d];
-				// (s, m) of sub-blocks kq and kq + 4 of this lane's row: d*s shared
-				// with the row's other lanes through LDS, dmin*m kept for the MFMA
-				uint32_t s0, m0, s1, m1;
-				scale_min_k4((uint32_t)kq, b.h.y, b.h.z, b.h.w, s0, m0);
-				scale_min_k4((uint32_t)kq + 4u, b.h.y, b.h.z, b.h.w, s1, m1);
-				const float dd = f16_to_f32(b.h.x & 0xFFFFu), dmin = f16_to_f32(b.h.x >> 16);
-				ex[kq] = dd * (float)s0;
-				ex[kq + 4] = dd * (float)s1;
-				const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
-				// min term: K = sub-block (4 per MFMA), lanes kq supply sub-blocks kq, kq+4
-				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kb + kq) * 16 + j], dm0, accm, 0, 0, 0);
-				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kb + kq + 4) * 16 + j], dm1, accm, 0, 0, 0);
-				__builtin_amdgcn_wave_barrier();
-				const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
-				const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
+	for (int d = 0; d < kQ4SkBlocks; d++) {
+		if (d < nbk) {
+			const Q4SkBuf &b = buf[d];
+			uint32_t s0, m0, s1, m1;
+			scale_min_k4((uint32_t)kq, b.h.y, b.h.z, b.h.w, s0, m0);
+			scale_min_k4((uint32_t)kq + 4u, b.h.y, b.h.z, b.h.w, s1, m1);
+			const float dd = f16_to_f32(b.h.x & 0xFFFFu), dmin = f16_to_f32(b.h.x >> 16);
+			ex[kq] = dd * (float)s0;
+			ex[kq + 4] = dd * (float)s1;
+			const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
+			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[8 * d + kq][j], dm0, accm, 0, 0, 0);
+			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[8 * d + kq + 4][j], dm1, accm, 0, 0, 0);
+			__builtin_amdgcn_wave_barrier();
+			const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
+			const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
 #pragma unroll
-				for (int g = 0; g < 4; g++) {
-					const uint2 q = b.q[g];
+			for (int g = 0; g < 4; g++) {
+				const uint2 q = b.q[g];
 #pragma unroll
-					for (int h = 0; h < 2; h++) {
-						const int sb = 2 * g + h;
-						const uint32_t w0 = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
-						const uint32_t w1 = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
-						const long wv = (long)(((uint64_t)w1 << 32) | w0);
-						const long av = *(const long *)(arow + 256 * kb + 32 * sb);
-						const v4i di = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zero, 0, 0, 0);
-						const float4 x4 = *(const float4 *)(xs_s + (8 * kb + sb) * 16 + 4 * kq);
-						acc[0] = __builtin_fmaf((float)di[0], x4.x * ds[sb], acc[0]);
-						acc[1] = __builtin_fmaf((float)di[1], x4.y * ds[sb], acc[1]);
-						acc[2] = __builtin_fmaf((float)di[2], x4.z * ds[sb], acc[2]);
-						acc[3] = __builtin_fmaf((float)di[3], x4.w * ds[sb], acc[3]);
-					}
+				for (int h = 0; h < 2; h++) {
+					const int sb = 2 * g + h;
+					const uint32_t w0 = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+					const uint32_t w1 = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+					const long wv = (long)(((uint64_t)w1 << 32) | w0);
+					const long av = *(const long *)(arow + 256 * d + 32 * sb);
+					const v4i di = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zero, 0, 0, 0);
+					const float4 x4 = *(const float4 *)&xs_s[8 * d + sb][4 * kq];
+					acc[0] = __builtin_fmaf((float)di[0], x4.x * ds[sb], acc[0]);
+					acc[1] = __builtin_fmaf((float)di[1], x4.y * ds[sb], acc[1]);
+					acc[2] = __builtin_fmaf((float)di[2], x4.z * ds[sb], acc[2]);
+					acc[3] = __builtin_fmaf((float)di[3], x4.w * ds[sb], acc[3]);
 				}
-				__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next block
 			}
-			issue(buf[d], kb + kQ4Depth);
+			__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next block
 		}
 	}
-	float y[4] = {acc[0] + accm[0], acc[1] + accm[1], acc[2] + accm[2], acc[3] + accm[3]};
-	if (swiglu) {
-		// up waves hand their sums to the gate waves of the same rows
-		float *up = up_s + ((wave >> 1) * 16 + j) * 16 + 4 * kq;
-		if (wave & 1) *(float4 *)up = make_float4(y[0], y[1], y[2], y[3]);
-		__syncthreads();
-		if ((wave & 1) || !ok) return;
-		const float4 u4 = *(const float4 *)up;
-		const float uv[4] = {u4.x, u4.y, u4.z, u4.w};
-		float *out = segs.s[0].out;
-		const int ld = segs.s[0].ld;
+	const float y[4] = {acc[0] + accm[0], acc[1] + accm[1], acc[2] + accm[2], acc[3] + accm[3]};
+	if (EPI == kSkPart) {
+		// tokens past M hold zeros (zero activations)
+		if (ok)
 #pragma unroll
-		for (int v = 0; v < 4; v++)
-			if (4 * kq + v < M) out[(size_t)(4 * kq + v) * ld + wr] = y[v] / (1.0f + expf(-y[v])) * uv[v];
+			for (int v = 0; v < 4; v++) part[((size_t)split * 16 + 4 * kq + v) * vrows + vrow] = y[v];
 		return;
 	}
-	skinny_epilogue(EPI, S, wrow0 + j, ok, y, M, lane);
+	skinny_epilogue(EPI, S, vrow, ok, y, M, lane);
 }
 
 // ── Q6_K x fp32 (fp16 hi/lo) ──
 
-constexpr int kQ6SkStage = 512;             // K per activation stage (two super-blocks)
-constexpr int kHPadSk = kQ6SkStage + 8;     // fp16 per staged token row
+constexpr int kHPadSk = kQK + 8;     // fp16 per staged token row
 
 struct Q6SkBuf {
 	uint32_t ql[2][4];   // per half n: ql bytes 64n + 16q + 4kq .. +4, q = 0..3
@@ -257,13 +241,11 @@ struct Q6SkBuf {
 	uint32_t d;
 };
 
-// Workgroup (row tile, K split): the tile's 64 rows over super-blocks
-// [kb_beg, kb_end). With nsplit > 1 the splits' results go to `part`
-// ([nsplit][16][vrows]) and skinny_reduce_kernel, launched next, sums them in
-// split order and applies the epilogue (a kernel boundary instead of a
-// device-scope fence in every workgroup).
+// Workgroup (64-row tile, K split): the tile's rows over super-blocks
+// [kb_beg, kb_end). EPI kSkStore / kSkAdd apply the epilogue directly (one
+// split); kSkPart writes the partial sums to part[split][t][vrow].
 template <int EPI>
-__global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Float16 *__restrict__ xh,
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6k_skinny_kernel(SkSegs segs, const _Float16 *__restrict__ xh,
                                                         const _Float16 *__restrict__ xl,
                                                         const float *__restrict__ esc, int M, int K, int vrows,
                                                         int nsplit, float *__restrict__ part) {
@@ -275,7 +257,6 @@ __global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Floa
 	const int NB = K >> 8;
 	const int tile = blockIdx.x / nsplit, split = blockIdx.x - tile * nsplit;
 	const int kb_beg = (int)((int64_t)split * NB / nsplit), kb_end = (int)((int64_t)(split + 1) * NB / nsplit);
-	const int NSt = (kb_end - kb_beg + 1) / 2;
 	const int wrow0 = (tile * 4 + wave) * kRowsWave;
 	const SegView S = seg_of(segs, wrow0, false);
 	const int vrow = wrow0 + j, wr = vrow - S.row0;
@@ -298,22 +279,21 @@ __global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Floa
 		b.sc = ld_b128(wrs, o + 192);
 		b.d = ld_b16(wrs, o + 208);
 	};
-	// activation stage st: 16 tokens x 512 K of hi and lo (zeros past M or K)
-	uint4 hreg[4], lreg[4];
-	auto load_stage = [&](int st) {
+	// activation stage of block kb: 16 tokens x 256 K of hi and lo (zeros past M)
+	uint4 hreg[2], lreg[2];
+	auto load_stage = [&](int kb) {
 #pragma unroll
-		for (int u = 0; u < 4; u++) {
-			const int c = tid + kT * u, t = c >> 6, p = c & 63;   // 16 tokens x 64 pieces of 8 fp16
-			const int k = 256 * kb_beg + kQ6SkStage * st + 8 * p;
-			const uint32_t off = (t < M && k < 256 * kb_end) ? 2u * ((uint32_t)t * K + k) : kBufNone;
+		for (int u = 0; u < 2; u++) {
+			const int c = tid + kT * u, t = c >> 5, p = c & 31;   // 16 tokens x 32 pieces of 8 fp16
+			const uint32_t off = t < M ? 2u * ((uint32_t)t * K + kQK * kb + 8 * p) : kBufNone;
 			hreg[u] = ld_b128(hrs, off);
 			lreg[u] = ld_b128(lrs, off);
 		}
 	};
 	auto store_stage = [&](int slot) {
 #pragma unroll
-		for (int u = 0; u < 4; u++) {
-			const int c = tid + kT * u, t = c >> 6, p = c & 63;
+		for (int u = 0; u < 2; u++) {
+			const int c = tid + kT * u, t = c >> 5, p = c & 31;
 			*(uint4 *)(ah_s[slot] + t * kHPadSk + 8 * p) = hreg[u];
 			*(uint4 *)(al_s[slot] + t * kHPadSk + 8 * p) = lreg[u];
 		}
@@ -322,21 +302,21 @@ __global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Floa
 	Q6SkBuf b0, b1;
 	issue(b0, kb_beg);
 	issue(b1, kb_beg + 1);
-	load_stage(0);
+	load_stage(kb_beg);
 	store_stage(0);
 	__syncthreads();
 	v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 	const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-	for (int st = 0; st < NSt; st++) {
-		const int slot = st & 1;
-		if (st + 1 < NSt) load_stage(st + 1);
-		const _Float16 *ah = ah_s[slot] + j * kHPadSk + 4 * kq;
-		const _Float16 *al = al_s[slot] + j * kHPadSk + 4 * kq;
+	for (int kb0 = kb_beg; kb0 < kb_end; kb0 += 2) {
 #pragma unroll
-		for (int half_st = 0; half_st < 2; half_st++) {
-			const int kb = kb_beg + 2 * st + half_st;
-			Q6SkBuf &b = half_st ? b1 : b0;
+		for (int half = 0; half < 2; half++) {
+			const int kb = kb0 + half;
 			if (kb < kb_end) {
+				const bool more = kb + 1 < kb_end;
+				if (more) load_stage(kb + 1);
+				Q6SkBuf &b = half ? b1 : b0;
+				const _Float16 *ah = ah_s[half] + j * kHPadSk + 4 * kq;
+				const _Float16 *al = al_s[half] + j * kHPadSk + 4 * kq;
 				const float dd = f16_to_f32(b.d);
 				const uint32_t scw[4] = {b.sc.x, b.sc.y, b.sc.z, b.sc.w};
 #pragma unroll
@@ -351,29 +331,27 @@ __global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Floa
 					const v2h bias2 = {(_Float16)1056.0f, (_Float16)1056.0f};
 					const v2h w01 = __builtin_bit_cast(v2h, lo2) - bias2, w23 = __builtin_bit_cast(v2h, hi2) - bias2;
 					const v4h wv = {w01[0], w01[1], w23[0], w23[1]};
-					const int ko = 256 * half_st + 16 * gg;
-					v4f pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(ah + ko), wv, zero, 0, 0, 0);
-					pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(al + ko), wv, pr, 0, 0, 0);
+					v4f pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(ah + 16 * gg), wv, zero, 0, 0, 0);
+					pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(al + 16 * gg), wv, pr, 0, 0, 0);
 					const float s = dd * (float)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 0xFFu);
 					acc[0] = __builtin_fmaf(pr[0], s, acc[0]);
 					acc[1] = __builtin_fmaf(pr[1], s, acc[1]);
 					acc[2] = __builtin_fmaf(pr[2], s, acc[2]);
 					acc[3] = __builtin_fmaf(pr[3], s, acc[3]);
 				}
+				issue(b, kb + 2);
+				if (more) {
+					store_stage(half ^ 1);
+					__syncthreads();
+				}
 			}
-			issue(b, kb + 2);
-		}
-		if (st + 1 < NSt) {
-			store_stage(slot ^ 1);
-			__syncthreads();
 		}
 	}
 	const int t0 = 4 * kq;
 	float y[4];
 #pragma unroll
 	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? acc[v] * esc[t0 + v] : 0.0f;
-	if (nsplit > 1) {
-		// tokens past M hold zeros; skinny_reduce_kernel sums the splits
+	if (EPI == kSkPart) {
 		if (ok)
 #pragma unroll
 			for (int v = 0; v < 4; v++) part[((size_t)split * 16 + t0 + v) * vrows + vrow] = y[v];
@@ -382,12 +360,24 @@ __global__ __launch_bounds__(kT) void q6k_skinny_kernel(SkSegs segs, const _Floa
 	skinny_epilogue(EPI, S, vrow, ok, y, M, lane);
 }
 
-// Grid (ceil(vrows/256), M): out[t][row] = sum over splits, in split order,
-// then the epilogue of the row's segment.
+// Grid (ceil(rows/256), M): the splits' sums, in split order, through the
+// epilogue. Store / Add: row = vrow of the launch's row space; SwiGLU: row r
+// of segment 0 combines gate row r and up row rows + r.
 template <int EPI>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkSegs segs, const float *__restrict__ part, int nsplit,
                                                             int vrows) {
 	const int vrow = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+	if (EPI == kSkSwiGLU) {
+		const int F = segs.s[0].rows;
+		if (vrow >= F) return;
+		float g = 0.0f, u = 0.0f;
+		for (int sp = 0; sp < nsplit; sp++) {
+			g += part[((size_t)sp * 16 + t) * vrows + vrow];
+			u += part[((size_t)sp * 16 + t) * vrows + F + vrow];
+		}
+		segs.s[0].out[(size_t)t * segs.s[0].ld + vrow] = g / (1.0f + expf(-g)) * u;
+		return;
+	}
 	if (vrow >= vrows) return;
 	float y = 0.0f;
 	for (int sp = 0; sp < nsplit; sp++) y += part[((size_t)sp * 16 + t) * vrows + vrow];
@@ -400,36 +390,58 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkSegs segs, const f
 		*o = y + (S.bias ? S.bias[r] : 0.0f);
 }
 
+int reduce(const SkSegs &segs, int epi, const float *part, int nsplit, int m, int vrows) {
+	const int rows = epi == kSkSwiGLU ? segs.s[0].rows : vrows;
+	const dim3 rg((rows + 255) / 256, m);
+	if (epi == kSkStore)
+		hipLaunchKernelGGL(skinny_reduce_kernel<kSkStore>, rg, dim3(256), 0, stream(), segs, part, nsplit, vrows);
+	else if (epi == kSkAdd)
+		hipLaunchKernelGGL(skinny_reduce_kernel<kSkAdd>, rg, dim3(256), 0, stream(), segs, part, nsplit, vrows);
+	else
+		hipLaunchKernelGGL(skinny_reduce_kernel<kSkSwiGLU>, rg, dim3(256), 0, stream(), segs, part, nsplit, vrows);
+	HK_LAUNCHED("skinny_reduce");
+	return HAKO_GPU_OK;
+}
+
 }  // namespace
 
-int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows) {
-	const size_t lds = q4k_skinny_lds(n_in);
-	// SwiGLU: 32 rows (gate and up) per workgroup, row space 2*rows
-	const int wgs = epi == kSkSwiGLU ? (segs.s[0].rows + 31) / 32 : (vrows + kRowsWg - 1) / kRowsWg;
-	const int nb = n_in / kQK;
-#define HK_Q4SK(E, D) \
-	hipLaunchKernelGGL((q4k_skinny_kernel<E, D>), dim3(wgs), dim3(kT), lds, stream(), segs, xq, xs, m, n_in, vrows)
-#define HK_Q4SK_D(E)                       \
-	do {                                   \
-		if (nb <= 8) HK_Q4SK(E, 8);        \
-		else HK_Q4SK(E, 16);               \
-	} while (0)
-	if (epi == kSkStore)
-		HK_Q4SK_D(kSkStore);
-	else if (epi == kSkAdd)
-		HK_Q4SK_D(kSkAdd);
+int q4k_skinny_splits(int n_in, int vrows) {
+	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
+	int ns = (kSkTargetWgs + tiles - 1) / tiles;           // enough workgroups to fill the chip
+	const int need = (nb + kQ4SkBlocks - 1) / kQ4SkBlocks;  // at most kQ4SkBlocks per workgroup
+	ns = ns < need ? need : ns;
+	return ns > nb ? nb : ns;
+}
+
+size_t q4k_skinny_part_floats(int n_in, int vrows, int epi) {
+	const int ns = q4k_skinny_splits(n_in, vrows);
+	return (ns > 1 || epi == kSkSwiGLU) ? (size_t)ns * 16 * vrows : 0;
+}
+
+int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
+               float *part) {
+	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
+	const int ns = q4k_skinny_splits(n_in, vrows);
+	const bool direct = ns == 1 && epi != kSkSwiGLU;
+	if (!direct && !part) return set_error(HAKO_GPU_EINVAL, "Q4_K skinny split needs a workspace");
+	const dim3 grid(tiles * ns);
+	if (!direct)
+		hipLaunchKernelGGL(q4k_skinny_kernel<kSkPart>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, ns,
+		                   part);
+	else if (epi == kSkStore)
+		hipLaunchKernelGGL(q4k_skinny_kernel<kSkStore>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, 1,
+		                   part);
 	else
-		HK_Q4SK_D(kSkSwiGLU);
-#undef HK_Q4SK_D
-#undef HK_Q4SK
+		hipLaunchKernelGGL(q4k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, 1,
+		                   part);
 	HK_LAUNCHED("q4k_skinny");
-	return HAKO_GPU_OK;
+	return direct ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
 }
 
 int q6k_skinny_splits(int n_in, int vrows) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
 	int ns = (kSkTargetWgs + tiles - 1) / tiles;       // enough workgroups to fill the chip
-	ns = ns > nb / 4 ? nb / 4 : ns;                    // at least two stages of K per split
+	ns = ns > nb / 4 ? nb / 4 : ns;                    // at least four super-blocks per split
 	return ns < 1 ? 1 : ns;
 }
 
@@ -444,27 +456,17 @@ int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *
 	const int ns = q6k_skinny_splits(n_in, vrows);
 	if (ns > 1 && !part) return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace");
 	const dim3 grid(tiles * ns);
-	if (epi == kSkStore)
-		hipLaunchKernelGGL(q6k_skinny_kernel<kSkStore>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
+	if (ns > 1)
+		hipLaunchKernelGGL(q6k_skinny_kernel<kSkPart>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
 		                   vrows, ns, part);
+	else if (epi == kSkStore)
+		hipLaunchKernelGGL(q6k_skinny_kernel<kSkStore>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
+		                   vrows, 1, part);
 	else
 		hipLaunchKernelGGL(q6k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
-		                   vrows, ns, part);
+		                   vrows, 1, part);
 	HK_LAUNCHED("q6k_skinny");
-	if (ns > 1) {
-		const dim3 rg((vrows + 255) / 256, m);
-		if (epi == kSkStore)
-			hipLaunchKernelGGL(skinny_reduce_kernel<kSkStore>, rg, dim3(256), 0, stream(), segs, part, ns, vrows);
-		else
-			hipLaunchKernelGGL(skinny_reduce_kernel<kSkAdd>, rg, dim3(256), 0, stream(), segs, part, ns, vrows);
-		HK_LAUNCHED("skinny_reduce");
-	}
-	return HAKO_GPU_OK;
-}
-
-size_t q4k_skinny_lds(int n_in) {
-	return (size_t)16 * (n_in + kAPadQ4) + (size_t)2 * 16 * (n_in / 32) * 4 + 4 * 16 * 8 * 4 + 2 * 16 * 16 * 4 +
-	       kT * 16;
+	return ns > 1 ? reduce(segs, epi, part, ns, m, vrows) : HAKO_GPU_OK;
 }
 
 }  // namespace hako
