@@ -38,6 +38,9 @@ class Decoder:
 
     def __init__(self, gpu: Gpu, path: str, n_seq: int = 1, max_seq: int = 2048):
         self.gpu, self.lib = gpu, gpu.lib
+        why = mlf2.check(path)
+        if why:
+            raise ValueError(f"{path}: {why}")
         self.f = mlf2.Mlf2File(path)
         h = self.f.header
         start = h["data_off"]

@@ -41,6 +41,11 @@ static const void *dev_tensor(const hakm_model *m, const char *name, int require
 int hako_decoder_from_model(const hakm_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec) {
 	if (!m || !dec || !m->map) return HAKO_GPU_EINVAL;
 	*dec = NULL;
+	char why[256];
+	if (hako_mlf2_check(m->map, m->map_size, why, sizeof why)) {
+		fprintf(stderr, "hako: %s\n", why);
+		return HAKO_GPU_EINVAL;
+	}
 	int rc = hako_model_upload(m);
 	if (rc) return rc;
 	const mlf2_header *h = &m->h;

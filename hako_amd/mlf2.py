@@ -158,3 +158,23 @@ class Mlf2File:
         t = self.tensors[name]
         start = self.header["data_off"] + t["data_off"]
         return self.buf[start:start + t["nbytes"]]
+
+
+def check_bytes(buf) -> str:
+    """The library's structural check (hako_mlf2_check, include/hako_mlf2.h)
+    of an MLF2 image held in `buf` (bytes, bytearray or a uint8 array): ''
+    when it passes, else the reason."""
+    import ctypes as C
+    from hako_amd.gpu import HOST_LIB
+    lib = C.CDLL(HOST_LIB)
+    lib.hako_mlf2_check.restype = C.c_int
+    lib.hako_mlf2_check.argtypes = [C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]
+    arr = np.frombuffer(buf, dtype=np.uint8) if not isinstance(buf, np.ndarray) else buf
+    msg = C.create_string_buffer(256)
+    rc = lib.hako_mlf2_check(arr.ctypes.data if arr.size else None, arr.size, msg, len(msg))
+    return "" if rc == 0 else (msg.value.decode() or "rejected")
+
+
+def check(path: str) -> str:
+    """hako_mlf2_check of the file at `path` (memory-mapped)."""
+    return check_bytes(np.memmap(path, dtype=np.uint8, mode="r"))

@@ -79,6 +79,23 @@ typedef struct {
 } hakm_model;
 #endif
 
+/* ── addition (no reference counterpart) ── */
+
+/* Structural check of a whole MLF2 image (`map`, `size` bytes: the mapped
+ * file): the reference loader's own checks (src/loader.c:26-43: size, magic,
+ * version, section offsets) plus the converter's layout rules
+ * (tools/gguf2mlf.py:138-190: 32-byte aligned data section and tensor
+ * offsets, dims padded with zeros), every tensor's type known, nbytes equal
+ * to what its type and dims give, its bytes inside the data section, names
+ * terminated and unique, the tokenizer records inside their section, and the
+ * Qwen2 tensors hakm_ctx_new resolves (src/model.c:30-57) present with the
+ * header's dims (norms and biases F32; biases required when the header's
+ * QKV_BIAS flag is set). Returns 0, or -1 with a description in msg
+ * (msg_len bytes, may be 0). Reads only the image; no device needed. */
+#pragma GCC visibility push(default)
+int hako_mlf2_check(const void *map, size_t size, char *msg, size_t msg_len);
+#pragma GCC visibility pop
+
 #ifdef __cplusplus
 }
 #endif
