@@ -114,6 +114,29 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ h, co
 	if (i < n) h[i] = silu(g[i]) * u[i];
 }
 
+// Prompt prefill, token i of a chunk at position posv[i]: its key heads
+// rotated (NeoX, the rope table) and written with its value row into the
+// caches, as the reference's steps 2c-2d (src/model.c:113-121) per token.
+__global__ __launch_bounds__(256) void rope_append_kernel(const float *__restrict__ k, const float *__restrict__ v,
+                                                          const float2 *__restrict__ rope,
+                                                          const int *__restrict__ posv, float *kc, float *vc,
+                                                          int KVH, int HD, int max_seq) {
+	const int i = blockIdx.x, KV = KVH * HD, half = HD / 2;
+	const int pos = posv[i];
+	if (pos < 0 || pos >= max_seq) return;   // the host checks the room first
+	const float2 *rp = rope + (size_t)pos * half;
+	const float *kr = k + (size_t)i * KV;
+	float *kd = kc + (size_t)pos * KV, *vd = vc + (size_t)pos * KV;
+	for (int t = threadIdx.x; t < KVH * half; t += 256) {
+		const int h = t / half, j = t - h * half;
+		const float2 cs = rp[j];
+		const float a = kr[h * HD + j], b = kr[h * HD + j + half];
+		kd[h * HD + j] = a * cs.x - b * cs.y;
+		kd[h * HD + j + half] = a * cs.y + b * cs.x;
+	}
+	for (int t = threadIdx.x; t < KV; t += 256) vd[t] = v[(size_t)i * KV + t];
+}
+
 // Row r of x (n floats): rmsnorm with weight w (when w is not null), then
 // q8_32 into xq[r][n], xs[r][n/32] — the activation of the batched Q4_K
 // matmuls. One workgroup per row; n <= 4096 (4 quads per thread).
@@ -334,8 +357,10 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 // cos/sin of pos*theta^(-2i/hd)); the workgroup whose chunk holds pos also
 // rotates the new key, appends it and the new value to the caches and uses
 // them from LDS. Scores, chunk-local softmax (max m, sum l) and the weighted
-// value sum o go to `part` for attn_merge_kernel.
-template <int HD>
+// value sum o go to `part` for attn_merge_kernel. Without APPEND (prompt
+// prefill) the rotated key and the value at pos are already in the caches
+// and are read like every other position.
+template <int HD, bool APPEND>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv, const float2 *__restrict__ rope,
                                                    float *kc, float *vc, const int *__restrict__ posv,
                                                    float *part, int H, int KVH,
@@ -358,7 +383,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	if (pos < 0 || pos >= max_seq) return;   // no room left: the host refuses such steps
 	const int nact = pos / kChunk + 1;
 	if (c >= nact) return;
-	const bool has_pos = c == nact - 1;
+	const bool has_pos = APPEND && c == nact - 1;
 	const float *q = qkv + (size_t)sq * qkv_stride;
 	float *kcs = kc + (size_t)sq * kv_seq_stride + kvh * HD;
 	float *vcs = vc + (size_t)sq * kv_seq_stride + kvh * HD;
@@ -419,7 +444,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	__syncthreads();
 
 	// 3. scores: 4 threads per position, a quarter of the dims each
-	if (ks == pos) {
+	if (APPEND && ks == pos) {
 #pragma unroll
 		for (int j = 0; j < KQ; j++) kr[j] = *(const float4 *)(kn_s + kq * (HD / 4) + 4 * j);
 	}
@@ -660,6 +685,10 @@ struct hako_gpu_decoder {
 	int8_t *xq = nullptr;
 	float *xs = nullptr, *esc = nullptr, *skpart = nullptr;
 	_Float16 *xh = nullptr, *xl = nullptr;
+	// prompt prefill (allocated on first use): chunk activations and records
+	float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr,
+	      *pf_tmp = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_part = nullptr;
+	int *pf_tok = nullptr, *pf_pos = nullptr;
 	std::vector<void *> allocs;
 	hipGraphExec_t exec = nullptr;
 	hipGraph_t graph = nullptr;
@@ -722,13 +751,13 @@ int attention(hako_gpu_decoder *d, int l) {
 	float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
 	const dim3 ag(d->max_chunks, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
 	if (HD == 128) {
-		hipLaunchKernelGGL(attn_kernel<128>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+		hipLaunchKernelGGL((attn_kernel<128, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
 		HK_LAUNCHED("attention");
 		hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->part, d->pos, d->att, m.n_heads,
 		                   m.n_kv_heads, d->max_seq, d->max_chunks);
 	} else {
-		hipLaunchKernelGGL(attn_kernel<64>, ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
+		hipLaunchKernelGGL((attn_kernel<64, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
 		HK_LAUNCHED("attention");
 		hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->part, d->pos, d->att, m.n_heads,
@@ -755,8 +784,8 @@ int rmsnorm_q8(hako_gpu_decoder *d, const float *x, const float *w, int n) {
 }
 
 // The weight types the batched step runs (the Q4_K_M mix): Q4_K q/k/v/o/
-// gate/up, Q6_K down, Q4_K or Q6_K lm_head; d_model, ffn_dim <= 4096 /
-// any, kv_dim a multiple of 16.
+// gate/up, Q6_K down, Q4_K or Q6_K lm_head; d_model and kv_dim multiples of
+// 16 (skinny row segments start on 16-row boundaries).
 bool batched_ok(const hako_gpu_model &m, const std::vector<hako_gpu_block> &blocks, int kv_dim) {
 	if (kv_dim % 16 || m.d_model % 16) return false;
 	if (m.t_out != HAKO_TYPE_Q4_K && m.t_out != HAKO_TYPE_Q6_K) return false;
@@ -925,6 +954,94 @@ int check_room(hako_gpu_decoder *d, int n) {
 	return HAKO_GPU_OK;
 }
 
+// ── prompt prefill: the reference's feed (src/hakm_api.c:105-111), one
+// hakm_forward per prompt token, as chunks of up to kPrefillChunk tokens
+// through the multi-token matmuls ──
+
+constexpr int kPrefillChunk = 128;
+
+int prefill_alloc(hako_gpu_decoder *d) {
+	if (d->pf_x) return HAKO_GPU_OK;
+	const hako_gpu_model &m = d->m;
+	const size_t C = kPrefillChunk, D = m.d_model, F = m.ffn_dim, KV = d->kv_dim;
+	int rc = 0;
+#define HK_ALLOC(ptr, bytes) \
+	if (!rc) rc = dalloc(d, (bytes), (void **)&(ptr))
+	HK_ALLOC(d->pf_x, 4 * C * D);
+	HK_ALLOC(d->pf_xn, 4 * C * D);
+	HK_ALLOC(d->pf_q, 4 * C * D);
+	HK_ALLOC(d->pf_k, 4 * C * KV);
+	HK_ALLOC(d->pf_v, 4 * C * KV);
+	HK_ALLOC(d->pf_att, 4 * C * D);
+	HK_ALLOC(d->pf_tmp, 4 * C * D);
+	HK_ALLOC(d->pf_g, 4 * C * F);
+	HK_ALLOC(d->pf_u, 4 * C * F);
+	HK_ALLOC(d->pf_part, 4 * C * m.n_kv_heads * d->max_chunks * kMaxG * (m.head_dim + 2));
+	HK_ALLOC(d->pf_tok, 4 * C);
+	HK_ALLOC(d->pf_pos, 4 * C);
+#undef HK_ALLOC
+	if (rc) d->pf_x = nullptr;   // retried on the next call; the others stay tracked for destroy
+	return rc;
+}
+
+// Tokens [0, n) of sequence seq at positions pos0.. (n <= kPrefillChunk):
+// every layer for all of them, each matmul one multi-token launch, causal
+// attention over the cache (the chunk's keys and values appended first).
+int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int pos0) {
+	const hako_gpu_model &m = d->m;
+	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, HD = m.head_dim, KVH = m.n_kv_heads;
+	const int G = m.n_heads / KVH;
+	int posv[kPrefillChunk];
+	for (int i = 0; i < n; i++) posv[i] = pos0 + i;
+	HK_HIP(hipMemcpyAsync(d->pf_tok, tokens, sizeof(int) * n, hipMemcpyHostToDevice, stream()));
+	HK_HIP(hipMemcpyAsync(d->pf_pos, posv, sizeof(int) * n, hipMemcpyHostToDevice, stream()));
+	HK_HIP(hipStreamSynchronize(stream()));   // posv is this frame's
+	hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
+	                   row_bytes(m.t_embd, D), d->pf_tok, d->pf_x, D, m.vocab);
+	HK_LAUNCHED("embed");
+	const float scale = 1.0f / sqrtf((float)HD);
+	const size_t seq_off = (size_t)seq * m.n_layers * d->max_seq * KV;
+	for (int l = 0; l < m.n_layers; l++) {
+		const hako_gpu_block &B = d->blocks[l];
+		float *kcl = d->kc + seq_off + (size_t)l * d->max_seq * KV;
+		float *vcl = d->vc + seq_off + (size_t)l * d->max_seq * KV;
+		if (int rc = rmsnorm(d->pf_x, B.attn_norm, d->pf_xn, D, m.rms_eps, n)) return rc;
+		if (int rc = hako_gpu_matmul_batch(d->pf_q, d->pf_xn, B.t_q, B.wq, B.bq, n, D, D)) return rc;
+		if (int rc = hako_gpu_matmul_batch(d->pf_k, d->pf_xn, B.t_k, B.wk, B.bk, n, KV, D)) return rc;
+		if (int rc = hako_gpu_matmul_batch(d->pf_v, d->pf_xn, B.t_v, B.wv, B.bv, n, KV, D)) return rc;
+		hipLaunchKernelGGL(rope_append_kernel, dim3(n), dim3(256), 0, stream(), d->pf_k, d->pf_v, d->rope, d->pf_pos,
+		                   kcl, vcl, KVH, HD, d->max_seq);
+		HK_LAUNCHED("rope_append");
+		// token i attends over positions [0, pos0 + i] of the sequence's cache
+		const dim3 ag(d->max_chunks, KVH, n), mg(G, KVH, n);
+		if (HD == 128) {
+			hipLaunchKernelGGL((attn_kernel<128, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
+			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale);
+			HK_LAUNCHED("attention");
+			hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
+			                   m.n_heads, KVH, d->max_seq, d->max_chunks);
+		} else {
+			hipLaunchKernelGGL((attn_kernel<64, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
+			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale);
+			HK_LAUNCHED("attention");
+			hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
+			                   m.n_heads, KVH, d->max_seq, d->max_chunks);
+		}
+		HK_LAUNCHED("attention merge");
+		if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_att, B.t_o, B.wo, nullptr, n, D, D)) return rc;
+		if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
+		if (int rc = rmsnorm(d->pf_x, B.ffn_norm, d->pf_xn, D, m.rms_eps, n)) return rc;
+		if (int rc = hako_gpu_matmul_batch(d->pf_g, d->pf_xn, B.t_gate, B.gate, nullptr, n, F, D)) return rc;
+		if (int rc = hako_gpu_matmul_batch(d->pf_u, d->pf_xn, B.t_up, B.up, nullptr, n, F, D)) return rc;
+		hipLaunchKernelGGL(silu_mul_kernel, dim3((n * F + 255) / 256), dim3(256), 0, stream(), d->pf_g, d->pf_g,
+		                   d->pf_u, n * F);
+		HK_LAUNCHED("silu_mul");
+		if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_g, B.t_down, B.down, nullptr, n, D, F)) return rc;
+		if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
+	}
+	return HAKO_GPU_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1088,6 +1205,51 @@ int hako_gpu_decoder_generate(hako_gpu_decoder *d, const int *tokens, int n, int
 	HK_HIP(hipStreamSynchronize(stream()));
 	for (int i = 0; i < n; i++)
 		for (int s = 0; s < d->n_seq; s++) out[(size_t)i * d->n_seq + s] = ring[(size_t)s * d->max_seq + i];
+	return ok();
+}
+
+int hako_gpu_decoder_prefill(hako_gpu_decoder *d, int seq, const int *tokens, int n, float *logits, int *next) {
+	if (!d || !tokens || n <= 0) return set_error(HAKO_GPU_EINVAL, "null decoder or tokens, or n <= 0");
+	if (seq < 0 || seq >= d->n_seq) return set_error(HAKO_GPU_EINVAL, "sequence %d of %d", seq, d->n_seq);
+	const hako_gpu_model &m = d->m;
+	for (int i = 0; i < n; i++)
+		if (tokens[i] < 0 || tokens[i] >= m.vocab)
+			return set_error(HAKO_GPU_EINVAL, "prompt token %d (%d) outside the vocabulary", i, tokens[i]);
+	int pos0 = 0;
+	HK_HIP(hipMemcpyAsync(&pos0, d->pos + seq, sizeof(int), hipMemcpyDeviceToHost, stream()));
+	HK_HIP(hipStreamSynchronize(stream()));
+	if (pos0 < 0 || pos0 + n > d->max_seq)
+		return set_error(HAKO_GPU_EINVAL, "sequence %d at position %d has no room for %d prompt tokens (max_seq %d)",
+		                 seq, pos0, n, d->max_seq);
+	if (int rc = prefill_alloc(d)) return rc;
+	const int D = m.d_model;
+	int last = 0;
+	for (int c0 = 0; c0 < n; c0 += kPrefillChunk) {
+		last = n - c0 < kPrefillChunk ? n - c0 : kPrefillChunk;
+		if (int rc = prefill_chunk(d, seq, tokens + c0, last, pos0 + c0)) return rc;
+	}
+	// logits of the last prompt token (what feed returns), into the
+	// sequence's row of the step's logits
+	float *lg = d->logits + (size_t)seq * m.vocab;
+	if (int rc = rmsnorm(d->pf_x + (size_t)(last - 1) * D, m.out_norm, d->pf_xn, D, m.rms_eps, 1)) return rc;
+	if (int rc = hako_gpu_matmul(lg, d->pf_xn, m.t_out, m.out_weight, nullptr, m.vocab, D)) return rc;
+	const int pos1 = pos0 + n;
+	HK_HIP(hipMemcpyAsync(d->pos + seq, &pos1, sizeof(int), hipMemcpyHostToDevice, stream()));
+	std::vector<float> host;
+	float *dst = logits;
+	if (!dst && next) {
+		host.resize(m.vocab);
+		dst = host.data();
+	}
+	if (dst) HK_HIP(hipMemcpyAsync(dst, lg, sizeof(float) * m.vocab, hipMemcpyDeviceToHost, stream()));
+	HK_HIP(hipStreamSynchronize(stream()));
+	if (next) {
+		// greedy pick as the device argmax: NaN never wins, ties take the lowest index
+		int best = -1;
+		for (int i = 0; i < m.vocab; i++)
+			if (dst[i] == dst[i] && (best < 0 || dst[i] > dst[best])) best = i;
+		*next = best < 0 ? 0 : best;
+	}
 	return ok();
 }
 

@@ -127,5 +127,16 @@ class Decoder:
                        "decoder_generate")
         return out
 
+    def prefill(self, tokens, seq: int = 0, logits: bool = False):
+        """Feed a prompt to sequence `seq` from its position; returns the
+        greedy id after it (and the last prompt token's logits)."""
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32).reshape(-1))
+        nxt = np.zeros(1, np.int32)
+        lg = np.empty(self.cfg["vocab"], np.float32) if logits else None
+        self.gpu.check(self.lib.hako_gpu_decoder_prefill(self.d, seq, t.ctypes.data, t.size,
+                                                         None if lg is None else lg.ctypes.data, nxt.ctypes.data),
+                       "decoder_prefill")
+        return (int(nxt[0]), lg) if logits else int(nxt[0])
+
     def replay(self, n: int):
         self.gpu.check(self.lib.hako_gpu_decoder_replay(self.d, n), "decoder_replay")

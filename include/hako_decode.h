@@ -84,6 +84,16 @@ int hako_gpu_decoder_step(hako_gpu_decoder *dec, const int *tokens, float *logit
  * synchronization at the end. Positions advance by n. */
 int hako_gpu_decoder_generate(hako_gpu_decoder *dec, const int *tokens, int n, int *out);
 
+/* Feeds n prompt tokens (host) to sequence seq from its current position,
+ * as the reference's feed (src/hakm_api.c:105-111, one hakm_forward per
+ * token) but through the multi-token matmuls, up to 128 tokens per pass,
+ * with causal attention over the sequence's cache: the keys and values of
+ * every prompt position are written, the position advances by n, and the
+ * logits of the last prompt token go to logits[vocab] (host, may be NULL)
+ * with their greedy id in *next (may be NULL). Synchronous. The other
+ * sequences are untouched. */
+int hako_gpu_decoder_prefill(hako_gpu_decoder *dec, int seq, const int *tokens, int n, float *logits, int *next);
+
 /* Replays the captured step n times from the current device state (no host
  * transfer, no synchronization): the timed loop of a benchmark. */
 int hako_gpu_decoder_replay(hako_gpu_decoder *dec, int n);

@@ -1,0 +1,217 @@
+"""Prompt prefill through the model (hako_gpu_decoder_prefill) against the
+reference's feed (src/hakm_api.c:105-111: one hakm_forward per prompt token,
+src/model.c:93-165, compiled from its sources) followed by greedy decoding.
+
+Bars: the KV cache rows the prompt writes, and the last prompt token's
+logits, within 2e-2 of their range (q8 re-quantization of activations that
+differ in the last bit flips single int8 values); the greedy tokens after
+the prompt identical.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from hako_amd import mlf2, synth
+from helpers import maxabs_rel
+
+pytestmark = pytest.mark.gpu
+
+TINY = mlf2.Qwen2Config(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512,
+                        vocab=1024, ctx=512)
+TINY_UNTIED = mlf2.Qwen2Config(n_layers=2, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=768,
+                               vocab=768, ctx=256, tied=False, embd_type=synth.TYPE_Q4_K)
+SMALL_128 = mlf2.Qwen2Config(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=2816,
+                             vocab=4096, ctx=512)
+# dense weight types: the generic multi-token matmuls
+DENSE = mlf2.Qwen2Config(n_layers=1, d_model=256, n_heads=2, n_kv_heads=1, head_dim=128, ffn_dim=512, vocab=640,
+                         ctx=256, attn_type=synth.TYPE_F16, gate_up_type=synth.TYPE_F32, down_type=synth.TYPE_Q4_K,
+                         embd_type=synth.TYPE_F16)
+
+
+@pytest.fixture(scope="module")
+def ref():
+    from dropin import bind_ctx
+    from oracle.hako_oracle import REF_LIB
+    return bind_ctx(C.CDLL(REF_LIB))
+
+
+class RefSeq:
+    """One reference context fed token by token."""
+
+    def __init__(self, lib, path, max_seq, cfg):
+        from oracle.hako_oracle import HakmCtx
+        self.lib, self.cfg, self.max_seq = lib, cfg, max_seq
+        self.ctx = lib.hakm_ctx_new(path.encode(), max_seq)
+        assert self.ctx
+        self.c = HakmCtx.from_address(self.ctx)
+
+    def forward(self, tok):
+        p = self.lib.hakm_forward(self.ctx, int(tok))
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(self.cfg.vocab,)).copy()
+
+    def feed(self, toks):
+        lg = None
+        for t in toks:
+            lg = self.forward(t)
+        return lg
+
+    def greedy(self, lg, steps):
+        out = []
+        for _ in range(steps):
+            out.append(int(np.argmax(lg)))
+            lg = self.forward(out[-1])
+        return out
+
+    def kv(self, upto):
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        shape = (self.cfg.n_layers, self.max_seq, kvd)
+        k = np.ctypeslib.as_array(C.cast(self.c.k_cache, C.POINTER(C.c_float)), shape=shape)[:, :upto].copy()
+        v = np.ctypeslib.as_array(C.cast(self.c.v_cache, C.POINTER(C.c_float)), shape=shape)[:, :upto].copy()
+        return k, v
+
+    def close(self):
+        self.lib.hakm_ctx_free(self.ctx)
+
+
+def device_kv(gpu, dec, seq, upto):
+    k, v = dec.kv()
+    kvd = dec.kv_dim
+    out = []
+    for base in (k, v):
+        out.append(np.stack([gpu.download(base + dec.kv_offset(seq, l, 0), np.float32, (upto, kvd))
+                             for l in range(dec.cfg["n_layers"])]))
+    return out
+
+
+def make(gpu, path, n_seq, max_seq):
+    from hako_amd.decoder import Decoder
+    return Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
+
+
+@pytest.mark.parametrize("cfg,seed,n_prompt", [(TINY, 1, 37), (TINY_UNTIED, 2, 50), (SMALL_128, 3, 140),
+                                               (DENSE, 4, 21), (TINY, 5, 300)])
+def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt):
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, seed)
+    max_seq, steps = 384, 8
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    r = RefSeq(ref, path, max_seq, cfg)
+    try:
+        want_lg = r.feed(prompt)
+        want_k, want_v = r.kv(n_prompt)
+        want = r.greedy(want_lg, steps)
+    finally:
+        r.close()
+    dec = make(gpu, path, 1, max_seq)
+    try:
+        dec.set_pos(0)
+        first, lg = dec.prefill(prompt, logits=True)
+        got_k, got_v = device_kv(gpu, dec, 0, n_prompt)
+        got = [first] + dec.generate(first, steps - 1)[:, 0].tolist()
+    finally:
+        dec.close()
+    assert first == int(np.argmax(lg))
+    assert maxabs_rel(got_k, want_k) < 2e-2
+    assert maxabs_rel(got_v, want_v) < 2e-2
+    assert maxabs_rel(lg, want_lg) < 2e-2
+    assert got == want
+
+
+def test_prefill_after_decode_steps(gpu, ref, tmp_path):
+    """Prompt, three decode steps, a second prompt at the new position, then
+    greedy decoding: as the reference fed the same tokens one by one."""
+    cfg = TINY
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, 7)
+    rng = np.random.default_rng(7)
+    p1, p2 = rng.integers(0, cfg.vocab, 20), rng.integers(0, cfg.vocab, 15)
+    r = RefSeq(ref, path, 128, cfg)
+    try:
+        lg = r.feed(p1)
+        fed = r.greedy(lg, 3)                 # tokens fed by the three steps
+        lg = r.feed(p2)
+        want = r.greedy(lg, 5)
+    finally:
+        r.close()
+    dec = make(gpu, path, 1, 128)
+    try:
+        dec.set_pos(0)
+        t = dec.prefill(p1)
+        steps = []
+        for _ in range(3):
+            steps.append(t)
+            t = int(dec.step(t)[0])
+        nxt = dec.prefill(p2)
+        got = [nxt] + dec.generate(nxt, 4)[:, 0].tolist()
+    finally:
+        dec.close()
+    assert steps == fed
+    assert got == want
+
+
+def test_prefill_sequences_of_a_batched_decoder(gpu, ref, tmp_path):
+    """Four sequences, each prefilled with its own prompt length, then decoded
+    together: every sequence as the reference's own context."""
+    cfg = TINY
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, 8)
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(0, cfg.vocab, n) for n in (10, 25, 3, 140)]
+    steps = 6
+    dec = make(gpu, path, 4, 256)
+    try:
+        dec.set_pos([0, 0, 0, 0])
+        firsts = [dec.prefill(p, seq=s) for s, p in enumerate(prompts)]
+        got = np.concatenate([np.array(firsts)[None], dec.generate(np.array(firsts), steps - 1)])
+    finally:
+        dec.close()
+    for s, p in enumerate(prompts):
+        r = RefSeq(ref, path, 256, cfg)
+        try:
+            want = r.greedy(r.feed(p), steps)
+        finally:
+            r.close()
+        assert got[:, s].tolist() == want, f"sequence {s}"
+
+
+def test_prefill_qwen2_3b_prompt(gpu, ref, tmp_path):
+    """The full Qwen2.5-3B shape: a 150-token prompt (two prefill passes),
+    last logits and three greedy tokens against the reference's feed."""
+    cfg = mlf2.QWEN2_3B
+    path = str(tmp_path / "qwen2_3b.mlf2")
+    mlf2.write_qwen2(path, cfg, 32)
+    prompt = np.random.default_rng(32).integers(0, cfg.vocab, 150)
+    r = RefSeq(ref, path, 160, cfg)
+    try:
+        want_lg = r.feed(prompt)
+        want = r.greedy(want_lg, 3)
+    finally:
+        r.close()
+    dec = make(gpu, path, 1, 160)
+    try:
+        dec.set_pos(0)
+        first, lg = dec.prefill(prompt, logits=True)
+        got = [first] + dec.generate(first, 2)[:, 0].tolist()
+    finally:
+        dec.close()
+    assert maxabs_rel(lg, want_lg) < 2e-3
+    assert got == want
+
+
+def test_prefill_rejects_bad_use(gpu, tmp_path):
+    from hako_amd.gpu import HakoGpuError
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, TINY, 9)
+    dec = make(gpu, path, 2, 32)
+    try:
+        dec.set_pos([0, 30])
+        with pytest.raises(HakoGpuError, match="no room"):
+            dec.prefill([1, 2, 3], seq=1)
+        with pytest.raises(HakoGpuError, match="sequence 2"):
+            dec.prefill([1], seq=2)
+        with pytest.raises(HakoGpuError, match="vocabulary"):
+            dec.prefill([1, TINY.vocab], seq=0)
+        assert isinstance(dec.prefill([1, 2, 3], seq=0), int)
+    finally:
+        dec.close()
