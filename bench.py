@@ -280,6 +280,67 @@ def bench_decode_batched(g, steps: int, cpu_steps: int, seed: int = 40, n_seq: i
         os.unlink(path)
 
 
+def bench_prompt(g, n_prompt: int, cpu_tokens: int, seed: int = 50) -> dict:
+    """A 512-token prompt fed to a Qwen2-7B-shaped model (28 layers, Q4_K
+    attn/gate/up, Q6_K down and untied output, random weights) from position
+    0: hako_gpu_decoder_prefill, 128 tokens per pass through the multi-token
+    matmuls. The reference feeds a prompt one hakm_forward per token
+    (src/hakm_api.c:105-111); its rate is timed on `cpu_tokens` tokens."""
+    import tempfile
+    from hako_amd import mlf2
+    from hako_amd.decoder import Decoder
+    cfg = mlf2.QWEN2_7B
+    fd, path = tempfile.mkstemp(suffix=".mlf2")
+    os.close(fd)
+    try:
+        info = mlf2.write_qwen2(path, cfg, seed)
+        prompt = np.random.default_rng(seed).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+        dec = Decoder(g, path, n_seq=1, max_seq=n_prompt + 8)
+        try:
+            dec.set_pos(0)
+            dec.prefill(prompt)         # warm: workspaces, first-touch
+            times = []
+            for _ in range(3):
+                dec.set_pos(0)
+                t0 = time.perf_counter()
+                dec.prefill(prompt)     # synchronous
+                times.append(time.perf_counter() - t0)
+        finally:
+            dec.close()
+        sec = float(np.median(times))
+        weight_bytes = sum(e[4] for name, e in info.items() if name != "token_embd.weight")
+        res = {"workload": f"Qwen2-7B-shaped prompt prefill, {n_prompt} tokens from position 0 (28 layers, Q4_K "
+                           "attn/gate/up, Q6_K down and untied output)",
+               "tokens": n_prompt, "ms": round(sec * 1e3, 2), "tok_per_s": round(n_prompt / sec, 1),
+               "weight_passes": (n_prompt + 127) // 128,
+               "weight_gbps": round(weight_bytes * ((n_prompt + 127) // 128) / sec / 1e9, 1),
+               "timing": "host wall clock around the synchronous call, median of 3 after one warm-up"}
+        if cpu_tokens > 0:
+            from oracle.hako_oracle import REF_LIB, RefLib
+            threads = min(os.cpu_count() or 1, 16)
+            ref = RefLib(REF_LIB, threads=threads)
+            lib = ref.lib
+            ctx = lib.hakm_ctx_new(path.encode(), n_prompt + 8)
+            assert ctx
+            try:
+                tt = []
+                for t in prompt[:cpu_tokens + 1]:
+                    t0 = time.perf_counter()
+                    lib.hakm_forward(ctx, int(t))
+                    tt.append(time.perf_counter() - t0)
+            finally:
+                lib.hakm_ctx_free(ctx)
+            med = float(np.median(tt[1:]))
+            res["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads,
+                                   "kind": "reference",
+                                   "sample": f"the first {cpu_tokens} prompt tokens (after one warm-up) fed with the "
+                                             f"reference's hakm_forward on the same model file, {threads} threads, "
+                                             f"median {med * 1e3:.1f} ms/token (its feed is one forward per token)"}
+        return res
+    finally:
+        os.unlink(path)
+
+
 def bench_prefill(g, launches: int) -> dict:
     """The 7B prefill matmuls: Q4_K 18944x3584 x 512 tokens (q8_32 quantize +
     int8-MFMA GEMM) and Q6_K 3584x18944 x 512 tokens (fp16-MFMA GEMM)."""
@@ -332,12 +393,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "decode", "decode16", "prefill"],
+    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "decode", "decode16", "prompt", "prefill"],
                     help="run one workload and print its timing only (profiling runs)")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     ap.add_argument("--decode-steps", type=int, default=100)
     ap.add_argument("--cpu-decode-steps", type=int, default=3)
     ap.add_argument("--batched-steps", type=int, default=30)
+    ap.add_argument("--prompt-tokens", type=int, default=512)
+    ap.add_argument("--cpu-prompt-tokens", type=int, default=4)
     ap.add_argument("--cpu-batched-steps", type=int, default=2)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -352,11 +415,13 @@ def main():
     info = g.info()
     log(f"device {info.name.decode()} CUs={info.compute_units} HBM={info.hbm_bytes / 2**30:.0f} GiB")
 
-    if args.only in ("decode", "decode16", "prefill"):
+    if args.only in ("decode", "decode16", "prompt", "prefill"):
         if args.only == "decode":
             r = bench_decode(g, args.decode_steps, 0)
         elif args.only == "decode16":
             r = bench_decode_batched(g, args.batched_steps, 0)
+        elif args.only == "prompt":
+            r = bench_prompt(g, args.prompt_tokens, 0)
         else:
             r = bench_prefill(g, 30)
         print(json.dumps(r), flush=True)
@@ -396,6 +461,11 @@ def main():
         log(f"decode x16: {batched['us_per_step']:.1f} us/step, {batched['tok_per_s']:.1f} tok/s, "
             f"{batched['gbps']:.0f} GB/s" + (f"; cpu {batched['cpu_baseline']['value']:.3f} tok/s"
                                            if 'cpu_baseline' in batched else ""))
+    prompt = None
+    if not args.no_prefill:
+        prompt = bench_prompt(g, args.prompt_tokens, 0 if args.no_cpu else args.cpu_prompt_tokens)
+        log(f"prompt: {prompt['tokens']} tokens in {prompt['ms']:.1f} ms, {prompt['tok_per_s']:.0f} tok/s"
+            + (f"; cpu {prompt['cpu_baseline']['value']:.2f} tok/s" if 'cpu_baseline' in prompt else ""))
     prefill = None
     if not args.no_prefill:
         prefill = bench_prefill(g, 30)
@@ -424,6 +494,7 @@ def main():
         "extra": extra,
         "decode": decode,
         "decode_batched": batched,
+        "prompt_prefill": prompt,
         "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
