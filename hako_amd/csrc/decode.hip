@@ -137,51 +137,117 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const float *__restric
 	for (int t = threadIdx.x; t < KV; t += 256) vd[t] = v[(size_t)i * KV + t];
 }
 
-// Row r of x (n floats): rmsnorm with weight w (when w is not null), then
-// q8_32 into xq[r][n], xs[r][n/32] — the activation of the batched Q4_K
-// matmuls. One workgroup per row; n <= 4096 (4 quads per thread).
-constexpr int kNqPer = 4;
-__global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                         float eps, int8_t *__restrict__ xq, float *__restrict__ xs,
-                                                         int n) {
-	__shared__ float red[4];
-	const float *xr = x + (size_t)blockIdx.x * n;
-	float4 v[kNqPer], wv[kNqPer];
+// Batched decode, row r (token) of the residual stream x (n floats): first
+// x += sum over splits of part[split][r][n] (the split partial sums of the
+// matmul that feeds the residual, in split order, when part is not null),
+// then rmsnorm with weight w (when w is not null), and q8_32 into xq[r][n],
+// xs[r][n/32] (the activation of the next Q4_K matmuls). One workgroup of
+// 1024 threads per row, a quad of the row per thread, every partial's load
+// issued before any is summed; n <= 4096.
+constexpr int kRowT = 1024, kRowSplits = 16;
+__device__ __forceinline__ float4 load_resid_quad(float *__restrict__ xr, const float *__restrict__ part, int nsplit,
+                                                  int r, int n) {
+	const int e = min((int)threadIdx.x * 4, n - 4);
+	float4 v = *(const float4 *)(xr + e);
+	if (!part) return v;
+	float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+	for (int s0 = 0; s0 < nsplit; s0 += kRowSplits) {
+		float4 p[kRowSplits];
 #pragma unroll
-	for (int k = 0; k < kNqPer; k++) {
-		const int e = min((int)(threadIdx.x + 256 * k) * 4, n - 4);
-		v[k] = *(const float4 *)(xr + e);
-		wv[k] = w ? *(const float4 *)(w + e) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-	}
-	if (w) {
-		float ss = 0.0f;
+		for (int k = 0; k < kRowSplits; k++)
+			if (s0 + k < nsplit) p[k] = *(const float4 *)(part + ((size_t)(s0 + k) * 16 + r) * n + e);
 #pragma unroll
-		for (int k = 0; k < kNqPer; k++) {
-			if ((int)(threadIdx.x + 256 * k) * 4 < n) {
-				ss = __builtin_fmaf(v[k].x, v[k].x, ss);
-				ss = __builtin_fmaf(v[k].y, v[k].y, ss);
-				ss = __builtin_fmaf(v[k].z, v[k].z, ss);
-				ss = __builtin_fmaf(v[k].w, v[k].w, ss);
+		for (int k = 0; k < kRowSplits; k++)
+			if (s0 + k < nsplit) {
+				y.x += p[k].x;
+				y.y += p[k].y;
+				y.z += p[k].z;
+				y.w += p[k].w;
 			}
-		}
-		ss = block_sum256(ss, red);
-		const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-#pragma unroll
-		for (int k = 0; k < kNqPer; k++) {
-			v[k].x = v[k].x * scale * wv[k].x;
-			v[k].y = v[k].y * scale * wv[k].y;
-			v[k].z = v[k].z * scale * wv[k].z;
-			v[k].w = v[k].w * scale * wv[k].w;
-		}
 	}
+	v.x += y.x;
+	v.y += y.y;
+	v.z += y.z;
+	v.w += y.w;
+	if ((int)threadIdx.x * 4 < n) *(float4 *)(xr + e) = v;
+	return v;
+}
+
+__device__ __forceinline__ float block_sum1024(float v, float *red) {
+	v = wave_sum(v);
+	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+	__syncthreads();
+	float t = 0.0f;
 #pragma unroll
-	for (int k = 0; k < kNqPer; k++) {
-		const int e = (threadIdx.x + 256 * k) * 4;
-		float sc;
-		const uint32_t packed = q8_quant4(v[k], sc);
-		if (e < n) {
-			*(uint32_t *)(xq + (size_t)blockIdx.x * n + e) = packed;
-			if ((threadIdx.x & 7) == 0) xs[(size_t)blockIdx.x * (n >> 5) + (e >> 5)] = sc;
+	for (int w = 0; w < kRowT / 64; w++) t += red[w];
+	__syncthreads();
+	return t;
+}
+
+__device__ __forceinline__ float4 rms_scale_quad(float4 v, const float *__restrict__ w, float eps, int n, float *red) {
+	const bool on = (int)threadIdx.x * 4 < n;
+	const float4 wv = *(const float4 *)(w + min((int)threadIdx.x * 4, n - 4));
+	float ss = 0.0f;
+	if (on) {
+		ss = __builtin_fmaf(v.x, v.x, ss);
+		ss = __builtin_fmaf(v.y, v.y, ss);
+		ss = __builtin_fmaf(v.z, v.z, ss);
+		ss = __builtin_fmaf(v.w, v.w, ss);
+	}
+	ss = block_sum1024(ss, red);
+	const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+	return make_float4(v.x * scale * wv.x, v.y * scale * wv.y, v.z * scale * wv.z, v.w * scale * wv.w);
+}
+
+__global__ __launch_bounds__(kRowT) void resid_rmsnorm_q8_kernel(float *__restrict__ x, const float *__restrict__ part,
+                                                                 int nsplit, const float *__restrict__ w, float eps,
+                                                                 int8_t *__restrict__ xq, float *__restrict__ xs,
+                                                                 int n) {
+	__shared__ float red[kRowT / 64];
+	const int r = blockIdx.x;
+	float4 v = load_resid_quad(x + (size_t)r * n, part, nsplit, r, n);
+	if (w) v = rms_scale_quad(v, w, eps, n, red);
+	const int e = threadIdx.x * 4;
+	float sc;
+	const uint32_t packed = q8_quant4(v, sc);   // every lane takes part in the 8-lane maxima
+	if (e < n) {
+		*(uint32_t *)(xq + (size_t)r * n + e) = packed;
+		if ((threadIdx.x & 7) == 0) xs[(size_t)r * (n >> 5) + (e >> 5)] = sc;
+	}
+}
+
+// As above, then the fp16 hi/lo split of the normalized row with one power of
+// two for the row (the lm_head's Q6_K activation): xh/xl[r][n], esc[r] = 2^e.
+__global__ __launch_bounds__(kRowT) void resid_rmsnorm_split_kernel(float *__restrict__ x,
+                                                                    const float *__restrict__ part, int nsplit,
+                                                                    const float *__restrict__ w, float eps,
+                                                                    _Float16 *__restrict__ xh,
+                                                                    _Float16 *__restrict__ xl,
+                                                                    float *__restrict__ esc, int n) {
+	__shared__ float red[kRowT / 64];
+	const int r = blockIdx.x;
+	float4 v = load_resid_quad(x + (size_t)r * n, part, nsplit, r, n);
+	v = rms_scale_quad(v, w, eps, n, red);
+	const bool on = (int)threadIdx.x * 4 < n;
+	float a = on ? __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+	                               __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)))
+	             : 0.0f;
+	a = wave_max(a);
+	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
+	__syncthreads();
+	a = red[0];
+#pragma unroll
+	for (int k = 1; k < kRowT / 64; k++) a = __builtin_fmaxf(a, red[k]);
+	const int e = f16_split_exp(a);
+	const float s = __builtin_ldexpf(1.0f, -e);
+	if (threadIdx.x == 0) esc[r] = __builtin_ldexpf(1.0f, e);
+	if (on) {
+		const float f[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
+#pragma unroll
+		for (int q = 0; q < 4; q++) {
+			const _Float16 h = (_Float16)f[q];
+			xh[(size_t)r * n + threadIdx.x * 4 + q] = h;
+			xl[(size_t)r * n + threadIdx.x * 4 + q] = (_Float16)(f[q] - (float)h);
 		}
 	}
 }
@@ -528,10 +594,14 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 // sq from its chunks' records — M = max m_c, weights e^(m_c - M) / L with
 // L = sum l_c e^(m_c - M), output sum over chunks of weight * o_c, in chunk
 // order. A launch of its own: the records of every chunk's workgroup are
-// visible at the kernel boundary, with no fence per workgroup.
+// visible at the kernel boundary, with no fence per workgroup. When xq is not
+// null the head's outputs are also quantized (q8_32: a head holds whole
+// 32-blocks) into xq[sq][H*HD] and xs[sq][H*HD/32], the activation of the
+// batched output projection.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict__ part, const int *__restrict__ posv,
-                                                        float *__restrict__ att, int H, int KVH, int max_seq,
+                                                        float *__restrict__ att, int8_t *__restrict__ xq,
+                                                        float *__restrict__ xs, int H, int KVH, int max_seq,
                                                         int max_chunks) {
 	constexpr int REC = HD + 2, NW = HD / 64;
 	constexpr size_t CS = (size_t)kMaxG * REC;   // floats between two chunks' records of one head
@@ -578,7 +648,17 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
 		}
 		for (; cc < nc; cc++) acc = __builtin_fmaf(r[cc * CS], w_s[cc], acc);
 	}
-	att[(size_t)sq * H * HD + (size_t)(kvh * G + g) * HD + tid] = acc;
+	const size_t o = (size_t)sq * H * HD + (size_t)(kvh * G + g) * HD + tid;
+	att[o] = acc;
+	if (xq) {
+		const float a = ftz(acc);
+		float amax = __builtin_fabsf(a);
+#pragma unroll
+		for (int k = 1; k < 32; k <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, k));
+		const float sc = q8_xs(amax);
+		xq[o] = (int8_t)q8_code(a, q8_inv(amax, sc));
+		if ((tid & 31) == 0) xs[o >> 5] = sc;
+	}
 }
 
 // ── greedy pick (reference src/sample.c:28-32) ──
@@ -742,8 +822,9 @@ int add(float *x, const float *y, int n) {
 	return HAKO_GPU_OK;
 }
 
-// Attention of layer l for every sequence: chunk records, then their merge.
-int attention(hako_gpu_decoder *d, int l) {
+// Attention of layer l for every sequence: chunk records, then their merge
+// (which also writes the q8 rows of the output to mxq/mxs when not null).
+int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nullptr) {
 	const hako_gpu_model &m = d->m;
 	const int KV = d->kv_dim, HD = m.head_dim, G = m.n_heads / m.n_kv_heads;
 	const float scale = 1.0f / sqrtf((float)HD);
@@ -754,14 +835,14 @@ int attention(hako_gpu_decoder *d, int l) {
 		hipLaunchKernelGGL((attn_kernel<128, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
 		HK_LAUNCHED("attention");
-		hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->part, d->pos, d->att, m.n_heads,
-		                   m.n_kv_heads, d->max_seq, d->max_chunks);
+		hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->part, d->pos, d->att, mxq, mxs,
+		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks);
 	} else {
 		hipLaunchKernelGGL((attn_kernel<64, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
 		HK_LAUNCHED("attention");
-		hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->part, d->pos, d->att, m.n_heads,
-		                   m.n_kv_heads, d->max_seq, d->max_chunks);
+		hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->part, d->pos, d->att, mxq, mxs,
+		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks);
 	}
 	HK_LAUNCHED("attention merge");
 	return HAKO_GPU_OK;
@@ -777,17 +858,21 @@ int argmax(hako_gpu_decoder *d) {
 	return HAKO_GPU_OK;
 }
 
-int rmsnorm_q8(hako_gpu_decoder *d, const float *x, const float *w, int n) {
-	hipLaunchKernelGGL(rmsnorm_q8_kernel, dim3(d->n_seq), dim3(256), 0, stream(), x, w, d->m.rms_eps, d->xq, d->xs, n);
-	HK_LAUNCHED("rmsnorm_q8");
+// x += the pending split partials (part, nsplit; none when part is null),
+// then rmsnorm (w) and q8 rows of x into d->xq / d->xs.
+int resid_rmsnorm_q8(hako_gpu_decoder *d, const float *part, int nsplit, const float *w, int n) {
+	hipLaunchKernelGGL(resid_rmsnorm_q8_kernel, dim3(d->n_seq), dim3(kRowT), 0, stream(), d->x, part, nsplit, w,
+	                   d->m.rms_eps, d->xq, d->xs, n);
+	HK_LAUNCHED("resid_rmsnorm_q8");
 	return HAKO_GPU_OK;
 }
 
 // The weight types the batched step runs (the Q4_K_M mix): Q4_K q/k/v/o/
 // gate/up, Q6_K down, Q4_K or Q6_K lm_head; d_model and kv_dim multiples of
-// 16 (skinny row segments start on 16-row boundaries).
+// 16 (skinny row segments start on 16-row boundaries) and d_model <= 4096 (a
+// quad per thread of a 1024-thread workgroup in the row kernels).
 bool batched_ok(const hako_gpu_model &m, const std::vector<hako_gpu_block> &blocks, int kv_dim) {
-	if (kv_dim % 16 || m.d_model % 16) return false;
+	if (kv_dim % 16 || m.d_model % 16 || m.d_model > 4 * kRowT) return false;
 	if (m.t_out != HAKO_TYPE_Q4_K && m.t_out != HAKO_TYPE_Q6_K) return false;
 	for (const hako_gpu_block &B : blocks)
 		if (B.t_q != HAKO_TYPE_Q4_K || B.t_k != HAKO_TYPE_Q4_K || B.t_v != HAKO_TYPE_Q4_K || B.t_o != HAKO_TYPE_Q4_K ||
@@ -797,54 +882,63 @@ bool batched_ok(const hako_gpu_model &m, const std::vector<hako_gpu_block> &bloc
 }
 
 // One step of n_seq > 1 sequences: every matmul a skinny MFMA GEMM that
-// streams the weights once for all sequences.
+// streams the weights once for all sequences. The o and down matmuls leave
+// their split partial sums for the next kernel, which adds them to the
+// residual stream on its way (rmsnorm + q8, or the lm_head's split); the
+// gate/up sums go straight into the fp16 form of the down matmul.
 int enqueue_batched_step(hako_gpu_decoder *d) {
 	const hako_gpu_model &m = d->m;
 	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, M = d->n_seq;
 	hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
 	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
 	HK_LAUNCHED("embed");
+	const int ns_o = q4k_skinny_splits(D, D), ns_down = q6k_skinny_splits(F, D);
+	const float *pend = nullptr;   // the previous down matmul's partials
+	int pend_ns = 0;
 	for (int l = 0; l < m.n_layers; l++) {
 		const hako_gpu_block &B = d->blocks[l];
-		// 1. q, k, v for every sequence: rows [q | k | v] of qkv[t][D + 2KV]
-		if (int rc = rmsnorm_q8(d, d->x, B.attn_norm, D)) return rc;
+		// 1. residual, rmsnorm, q8; q, k, v: rows [q | k | v] of qkv[t][D + 2KV]
+		if (int rc = resid_rmsnorm_q8(d, pend, pend_ns, B.attn_norm, D)) return rc;
 		SkSegs s{};
 		s.n = 3;
 		s.s[0] = {(const uint8_t *)B.wq, B.bq, d->qkv, 0, D, d->qkv_dim};
 		s.s[1] = {(const uint8_t *)B.wk, B.bk, d->qkv + D, D, KV, d->qkv_dim};
 		s.s[2] = {(const uint8_t *)B.wv, B.bv, d->qkv + D + KV, D + KV, KV, d->qkv_dim};
 		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, D + 2 * KV, d->skpart)) return rc;
-		// 2. attention, one grid over every sequence
-		if (int rc = attention(d, l)) return rc;
-		// 3. output projection added into the residual stream
-		if (int rc = rmsnorm_q8(d, d->att, nullptr, D)) return rc;
+		// 2. attention, one grid over every sequence; q8 rows of its output
+		if (int rc = attention(d, l, d->xq, d->xs)) return rc;
+		// 3. output projection: partials, added to the residual by step 4
 		s = SkSegs{};
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D, D};
-		if (int rc = q4k_skinny(s, kSkAdd, d->xq, d->xs, M, D, D, d->skpart)) return rc;
-		// 4. gate, up, SwiGLU
-		if (int rc = rmsnorm_q8(d, d->x, B.ffn_norm, D)) return rc;
+		if (int rc = q4k_skinny(s, kSkPart, d->xq, d->xs, M, D, D, d->skpart)) return rc;
+		// 4. residual, rmsnorm, q8; gate, up, SwiGLU
+		if (int rc = resid_rmsnorm_q8(d, d->skpart, ns_o, B.ffn_norm, D)) return rc;
 		s = SkSegs{};
 		s.n = 2;
 		s.s[0] = {(const uint8_t *)B.gate, nullptr, d->h, 0, F, F};
 		s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, F, F, F};
 		if (int rc = q4k_skinny(s, kSkSwiGLU, d->xq, d->xs, M, D, 2 * F, d->skpart)) return rc;
-		// 5. down projection added into the residual stream
+		// 5. the down matmul's fp16 hi/lo rows
 		if (int rc = f16_split(d->h, d->xh, d->xl, d->esc, M, F)) return rc;
+		// 6. down projection: partials, added to the residual by the next kernel
 		s = SkSegs{};
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.down, nullptr, d->x, 0, D, D};
-		if (int rc = q6k_skinny(s, kSkAdd, d->xh, d->xl, d->esc, M, F, D, d->skpart)) return rc;
+		if (int rc = q6k_skinny(s, kSkPart, d->xh, d->xl, d->esc, M, F, D, d->skpart)) return rc;
+		pend = d->skpart;
+		pend_ns = ns_down;
 	}
 	SkSegs s{};
 	s.n = 1;
 	s.s[0] = {(const uint8_t *)m.out_weight, nullptr, d->logits, 0, m.vocab, m.vocab};
 	if (m.t_out == HAKO_TYPE_Q4_K) {
-		if (int rc = rmsnorm_q8(d, d->x, m.out_norm, D)) return rc;
+		if (int rc = resid_rmsnorm_q8(d, pend, pend_ns, m.out_norm, D)) return rc;
 		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, m.vocab, d->skpart)) return rc;
 	} else {
-		if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, M)) return rc;
-		if (int rc = f16_split(d->xn, d->xh, d->xl, d->esc, M, D)) return rc;
+		hipLaunchKernelGGL(resid_rmsnorm_split_kernel, dim3(M), dim3(kRowT), 0, stream(), d->x, pend, pend_ns,
+		                   m.out_norm, m.rms_eps, d->xh, d->xl, d->esc, D);
+		HK_LAUNCHED("resid_rmsnorm_split");
 		if (int rc = q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, D, m.vocab, d->skpart)) return rc;
 	}
 	if (int rc = argmax(d)) return rc;
@@ -1019,12 +1113,14 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
+			                   nullptr, nullptr,
 			                   m.n_heads, KVH, d->max_seq, d->max_chunks);
 		} else {
 			hipLaunchKernelGGL((attn_kernel<64, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
 			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
+			                   nullptr, nullptr,
 			                   m.n_heads, KVH, d->max_seq, d->max_chunks);
 		}
 		HK_LAUNCHED("attention merge");
@@ -1078,7 +1174,8 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 		delete d;
 		return set_error(HAKO_GPU_ETYPE,
 		                 "batched decode (n_seq > 1) runs the Q4_K_M mix (Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or "
-		                 "Q6_K output) with d_model and n_kv_heads*head_dim multiples of 16");
+		                 "Q6_K output) with d_model <= %d, d_model and n_kv_heads*head_dim multiples of 16",
+		                 4 * kRowT);
 	}
 	d->m.blocks = nullptr;
 	d->n_seq = n_seq;
@@ -1113,10 +1210,10 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	// split-K partials of the largest skinny matmul of a step
 	size_t skpart = 0;
 	const int qkv_rows = D + 2 * d->kv_dim;
-	const size_t needs[6] = {q4k_skinny_part_floats(D, qkv_rows, kSkStore), q4k_skinny_part_floats(D, D, kSkAdd),
-	                         q4k_skinny_part_floats(D, 2 * F, kSkSwiGLU), q6k_skinny_part_floats(F, D),
+	const size_t needs[6] = {q4k_skinny_part_floats(D, qkv_rows, kSkStore), q4k_skinny_part_floats(D, D, kSkPart),
+	                         q4k_skinny_part_floats(D, 2 * F, kSkSwiGLU), q6k_skinny_part_floats(F, D, kSkPart),
 	                         m->t_out == HAKO_TYPE_Q4_K ? q4k_skinny_part_floats(D, m->vocab, kSkStore) : 0,
-	                         m->t_out == HAKO_TYPE_Q6_K ? q6k_skinny_part_floats(D, m->vocab) : 0};
+	                         m->t_out == HAKO_TYPE_Q6_K ? q6k_skinny_part_floats(D, m->vocab, kSkStore) : 0};
 	for (size_t nf : needs) skpart = nf > skpart ? nf : skpart;
 	if (n_seq > 1) {
 		HK_ALLOC(d->xq, (size_t)n_seq * D);

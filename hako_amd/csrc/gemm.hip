@@ -210,9 +210,9 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const uint8_t *__restrict
 
 // Token row t of x (K floats): s = 2^-e with max|x_t| in [2^e, 2^(e+1)),
 // hi = fp16(x*s), lo = fp16(x*s - hi), esc[t] = 2^e. The scaling is exact,
-// and x*s - hi is exact in fp32. 1024 threads per row; up to kSplitPer
-// float4 per thread are loaded once, all at the start, and kept in
-// registers for both passes (rows longer than that run the tail from memory).
+// and x*s - hi is exact in fp32. 1024 threads per row; up to kSplitPer float4 per thread are
+// loaded once, all at the start, and kept in registers for both passes
+// (rows longer than that run the tail from memory).
 constexpr int kSplitT = 1024, kSplitPer = 8;
 __global__ __launch_bounds__(kSplitT) void f16_split_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
                                                             _Float16 *__restrict__ xl, float *__restrict__ esc,
@@ -246,13 +246,7 @@ __global__ __launch_bounds__(kSplitT) void f16_split_kernel(const float *__restr
 	a = 0.0f;
 #pragma unroll
 	for (int w = 0; w < kSplitT / kWave; w++) a = __builtin_fmaxf(a, red[w]);
-	int e = 0;
-	if (a > 0.0f && __builtin_isfinite(a)) {
-		// exponent of a normal a; subnormal rows clamp to -126, which keeps 2^-e
-		// finite and loses nothing that matters at that size
-		e = (int)((__builtin_bit_cast(uint32_t, a) >> 23) & 0xFFu) - 127;
-		e = e < -126 ? -126 : e;
-	}
+	const int e = f16_split_exp(a);
 	const float s = __builtin_ldexpf(1.0f, -e);
 	if (threadIdx.x == 0) esc[blockIdx.x] = __builtin_ldexpf(1.0f, e);
 	auto put = [&](int i, float4 q) {
@@ -477,7 +471,7 @@ int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, 
 		segs.n = 1;
 		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
 		float *part = nullptr;
-		if (int rc = skinny_split_workspace(q6k_skinny_part_floats(n_in, n_out), &part)) return rc;
+		if (int rc = skinny_split_workspace(q6k_skinny_part_floats(n_in, n_out, kSkStore), &part)) return rc;
 		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part)) return rc;
 		return ok();
 	}

@@ -145,30 +145,47 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
 	}
 }
 
+// q8_32 of one block (reference quant.c:127-144 as compiled with
+// -ffast-math): inputs flushed to zero below FLT_MIN, xs = amax*RN(1/127),
+// inv = RN(127/amax) when xs > 0, codes round-half-even clamped to +-127.
+// A product that is not finite (only from inf/NaN inputs) converts to 0, as
+// the reference's 64-bit conversion yields the "indefinite" value whose low
+// 32 bits are 0. Clamping in float keeps the int conversion defined.
+__device__ __forceinline__ float q8_xs(float amax) { return ftz(amax * 0x1.020408p-7f); }   // RN(1/127) = 0x3C010204
+__device__ __forceinline__ float q8_inv(float amax, float xs) { return xs > 0.0f ? 127.0f / amax : 0.0f; }
+__device__ __forceinline__ uint32_t q8_code(float a, float inv) {
+	float r = __builtin_rintf(a * inv);
+	r = __builtin_isfinite(r) ? r : 0.0f;
+	r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+	return (uint32_t)((int)r & 0xFF);
+}
+
 // q8_32 quantization of four consecutive floats held by one lane, eight lanes
 // per 32-block (lanes 8k..8k+7 of the wave own block k of the call). Returns
-// the four int8 results packed little-endian and the block scale in `scale`
-// (reference quant.c:127-144 as compiled with -ffast-math:
-// xs = amax*RN(1/127), inv = RN(127/amax) when xs > 0, round-half-even,
-// clamp to +-127).
+// the four int8 results packed little-endian and the block scale in `scale`.
 __device__ __forceinline__ uint32_t q8_quant4(float4 v, float &scale) {
 	const float a0 = ftz(v.x), a1 = ftz(v.y), a2 = ftz(v.z), a3 = ftz(v.w);
 	float amax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(a0), __builtin_fabsf(a1)),
 	                             __builtin_fmaxf(__builtin_fabsf(a2), __builtin_fabsf(a3)));
 	amax = max8(amax);
-	const float xs = ftz(amax * 0x1.020408p-7f);      // RN(1/127) = 0x3C010204
-	const float inv = xs > 0.0f ? 127.0f / amax : 0.0f;
+	const float xs = q8_xs(amax);
+	const float inv = q8_inv(amax, xs);
 	scale = xs;
-	// A product that is not finite (only from inf/NaN inputs) converts to 0,
-	// as the reference's 64-bit conversion yields the "indefinite" value whose
-	// low 32 bits are 0. Clamping in float keeps the int conversion defined.
-	auto q = [inv](float a) -> uint32_t {
-		float r = __builtin_rintf(a * inv);
-		r = __builtin_isfinite(r) ? r : 0.0f;
-		r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
-		return (uint32_t)((int)r & 0xFF);
-	};
-	return q(a0) | (q(a1) << 8) | (q(a2) << 16) | (q(a3) << 24);
+	return q8_code(a0, inv) | (q8_code(a1, inv) << 8) | (q8_code(a2, inv) << 16) | (q8_code(a3, inv) << 24);
+}
+
+// Power-of-two scaling of a vector for the fp16 hi/lo representation: for
+// max|x| = a, e with a in [2^e, 2^(e+1)) (0 when a is 0 or not finite;
+// subnormal maxima clamp to -126, which keeps 2^-e finite and loses nothing
+// that matters at that size). x * 2^-e is then below 2, hi = fp16(x*2^-e),
+// lo = fp16(x*2^-e - hi); the scaling and the subtraction are exact.
+__device__ __forceinline__ int f16_split_exp(float a) {
+	int e = 0;
+	if (a > 0.0f && __builtin_isfinite(a)) {
+		e = (int)((__builtin_bit_cast(uint32_t, a) >> 23) & 0xFFu) - 127;
+		e = e < -126 ? -126 : e;
+	}
+	return e;
 }
 
 }  // namespace hako

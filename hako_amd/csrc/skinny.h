@@ -27,7 +27,9 @@ struct SkSegs {
 // Epilogues: Store out = y (+ bias); Add out += y (a residual); SwiGLU
 // (Q4_K only): segment 0 (gate, launch rows [0, F)) and segment 1 (up, rows
 // [F, 2F)), out (segment 0's) = silu(gate)*up.
-enum { kSkStore = 0, kSkAdd = 1, kSkSwiGLU = 2 };
+// Part leaves the splits' partial sums in `part` ([split][16][rows], every
+// split, tokens past m zero) for a consumer that sums them itself.
+enum { kSkStore = 0, kSkAdd = 1, kSkSwiGLU = 2, kSkPart = 3 };
 
 // Workgroups a launch aims for (4 per CU); K is split over workgroups to
 // reach it. Split results go to `part` (the *_part_floats count of floats),
@@ -39,13 +41,14 @@ int q4k_skinny_splits(int n_in, int vrows);
 size_t q4k_skinny_part_floats(int n_in, int vrows, int epi);
 int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
                float *part);
-// Q6_K x fp32 as fp16 hi/lo rows [m][n_in] with per-row powers of two esc[m];
-// Store or Add epilogue.
+// Q6_K x fp32 as fp16 hi/lo rows [m][n_in] with a power of two per token,
+// esc[m] (x = (hi + lo) * esc); Store, Add or Part.
 int q6k_skinny_splits(int n_in, int vrows);
-size_t q6k_skinny_part_floats(int n_in, int vrows);
+size_t q6k_skinny_part_floats(int n_in, int vrows, int epi);
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
                int n_in, int vrows, float *part);
-// The fp16 hi/lo split of m fp32 rows of n floats (gemm.hip).
+// The fp16 hi/lo split of m fp32 rows of n floats with one power of two per
+// row, esc[m] (gemm.hip).
 int f16_split(const float *x, _Float16 *xh, _Float16 *xl, float *esc, int m, int n);
 
 }  // namespace hako

@@ -104,7 +104,6 @@ struct Q4SkBuf {
 // super-blocks [kb_beg, kb_end) (at most kQ4SkBlocks). EPI kSkStore / kSkAdd
 // apply the epilogue directly (one split); kSkPart writes the partial sums
 // to part[split][t][vrow].
-constexpr int kSkPart = 3;
 template <int EPI>
 __global__ __launch_bounds__(kT) void q4k_skinny_kernel(SkSegs segs, const int8_t *__restrict__ xq,
                                                         const float *__restrict__ xs, int M, int K, int vrows,
@@ -242,13 +241,13 @@ struct Q6SkBuf {
 };
 
 // Workgroup (64-row tile, K split): the tile's rows over super-blocks
-// [kb_beg, kb_end). EPI kSkStore / kSkAdd apply the epilogue directly (one
-// split); kSkPart writes the partial sums to part[split][t][vrow].
+// [kb_beg, kb_end), the sums scaled by each token's power of two (esc) at
+// the end. EPI kSkStore / kSkAdd apply the epilogue directly (one split);
+// kSkPart writes the partial sums to part[split][t][vrow].
 template <int EPI>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6k_skinny_kernel(SkSegs segs, const _Float16 *__restrict__ xh,
-                                                        const _Float16 *__restrict__ xl,
-                                                        const float *__restrict__ esc, int M, int K, int vrows,
-                                                        int nsplit, float *__restrict__ part) {
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6k_skinny_kernel(
+    SkSegs segs, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, const float *__restrict__ esc,
+    int M, int K, int vrows, int nsplit, float *__restrict__ part) {
 	__shared__ __align__(16) _Float16 ah_s[2][16 * kHPadSk];
 	__shared__ __align__(16) _Float16 al_s[2][16 * kHPadSk];
 	const int tid = threadIdx.x, lane = tid & 63;
@@ -266,6 +265,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 	const uint32_t row_off = ok ? (uint32_t)wr * rb : kBufNone;
 	const __amdgpu_buffer_rsrc_t hrs = stream_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
 	const __amdgpu_buffer_rsrc_t lrs = stream_rsrc(xl, (uint32_t)M * (uint32_t)K * 2u);
+	const int t0 = 4 * kq;
 
 	auto issue = [&](Q6SkBuf &b, int kb) {
 		const uint32_t o = kb < kb_end ? row_off + (uint32_t)kb * kQ6Bytes : kBufNone;
@@ -347,7 +347,6 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 			}
 		}
 	}
-	const int t0 = 4 * kq;
 	float y[4];
 #pragma unroll
 	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? acc[v] * esc[t0 + v] : 0.0f;
@@ -415,14 +414,14 @@ int q4k_skinny_splits(int n_in, int vrows) {
 
 size_t q4k_skinny_part_floats(int n_in, int vrows, int epi) {
 	const int ns = q4k_skinny_splits(n_in, vrows);
-	return (ns > 1 || epi == kSkSwiGLU) ? (size_t)ns * 16 * vrows : 0;
+	return (ns > 1 || epi == kSkSwiGLU || epi == kSkPart) ? (size_t)ns * 16 * vrows : 0;
 }
 
 int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
                float *part) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
 	const int ns = q4k_skinny_splits(n_in, vrows);
-	const bool direct = ns == 1 && epi != kSkSwiGLU;
+	const bool direct = ns == 1 && epi != kSkSwiGLU && epi != kSkPart;
 	if (!direct && !part) return set_error(HAKO_GPU_EINVAL, "Q4_K skinny split needs a workspace");
 	const dim3 grid(tiles * ns);
 	if (!direct)
@@ -435,7 +434,7 @@ int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, i
 		hipLaunchKernelGGL(q4k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, 1,
 		                   part);
 	HK_LAUNCHED("q4k_skinny");
-	return direct ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
+	return (direct || epi == kSkPart) ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
 }
 
 int q6k_skinny_splits(int n_in, int vrows) {
@@ -445,18 +444,19 @@ int q6k_skinny_splits(int n_in, int vrows) {
 	return ns < 1 ? 1 : ns;
 }
 
-size_t q6k_skinny_part_floats(int n_in, int vrows) {
+size_t q6k_skinny_part_floats(int n_in, int vrows, int epi) {
 	const int ns = q6k_skinny_splits(n_in, vrows);
-	return ns > 1 ? (size_t)ns * 16 * vrows : 0;
+	return (ns > 1 || epi == kSkPart) ? (size_t)ns * 16 * vrows : 0;
 }
 
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
                int n_in, int vrows, float *part) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
 	const int ns = q6k_skinny_splits(n_in, vrows);
-	if (ns > 1 && !part) return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace");
+	const bool direct = ns == 1 && epi != kSkPart;
+	if (!direct && !part) return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace");
 	const dim3 grid(tiles * ns);
-	if (ns > 1)
+	if (!direct)
 		hipLaunchKernelGGL(q6k_skinny_kernel<kSkPart>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
 		                   vrows, ns, part);
 	else if (epi == kSkStore)
@@ -466,7 +466,7 @@ int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *
 		hipLaunchKernelGGL(q6k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
 		                   vrows, 1, part);
 	HK_LAUNCHED("q6k_skinny");
-	return ns > 1 ? reduce(segs, epi, part, ns, m, vrows) : HAKO_GPU_OK;
+	return (direct || epi == kSkPart) ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
 }
 
 }  // namespace hako
