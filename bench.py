@@ -283,7 +283,7 @@ def bench_decode_batched(g, steps: int, cpu_steps: int, seed: int = 40, n_seq: i
 def bench_prompt(g, n_prompt: int, cpu_tokens: int, seed: int = 50) -> dict:
     """A 512-token prompt fed to a Qwen2-7B-shaped model (28 layers, Q4_K
     attn/gate/up, Q6_K down and untied output, random weights) from position
-    0: hako_gpu_decoder_prefill, 128 tokens per pass through the multi-token
+    0: hako_gpu_decoder_prefill, 512 tokens per pass through the multi-token
     matmuls. The reference feeds a prompt one hakm_forward per token
     (src/hakm_api.c:105-111); its rate is timed on `cpu_tokens` tokens."""
     import tempfile
@@ -312,8 +312,8 @@ def bench_prompt(g, n_prompt: int, cpu_tokens: int, seed: int = 50) -> dict:
         res = {"workload": f"Qwen2-7B-shaped prompt prefill, {n_prompt} tokens from position 0 (28 layers, Q4_K "
                            "attn/gate/up, Q6_K down and untied output)",
                "tokens": n_prompt, "ms": round(sec * 1e3, 2), "tok_per_s": round(n_prompt / sec, 1),
-               "weight_passes": (n_prompt + 127) // 128,
-               "weight_gbps": round(weight_bytes * ((n_prompt + 127) // 128) / sec / 1e9, 1),
+               "weight_passes": (n_prompt + 511) // 512,
+               "weight_gbps": round(weight_bytes * ((n_prompt + 511) // 512) / sec / 1e9, 1),
                "timing": "host wall clock around the synchronous call, median of 3 after one warm-up"}
         if cpu_tokens > 0:
             from oracle.hako_oracle import REF_LIB, RefLib

@@ -769,6 +769,7 @@ struct hako_gpu_decoder {
 	float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr,
 	      *pf_tmp = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_part = nullptr;
 	int *pf_tok = nullptr, *pf_pos = nullptr;
+	int pf_chunk = 0;   // tokens per prefill pass
 	std::vector<void *> allocs;
 	hipGraphExec_t exec = nullptr;
 	hipGraph_t graph = nullptr;
@@ -1049,15 +1050,23 @@ int check_room(hako_gpu_decoder *d, int n) {
 }
 
 // ── prompt prefill: the reference's feed (src/hakm_api.c:105-111), one
-// hakm_forward per prompt token, as chunks of up to kPrefillChunk tokens
+// hakm_forward per prompt token, as passes of up to pf_chunk tokens
 // through the multi-token matmuls ──
 
-constexpr int kPrefillChunk = 128;
+// Tokens per pass: 512 (64-token GEMM tiles fill the chip and the weights
+// stream once per 512 tokens), halved while the attention records of a pass
+// (tokens x KV heads x max_seq/64 chunks x heads per KV head) exceed 1 GiB.
+constexpr int kPrefillMax = 512;
+constexpr size_t kPrefillRecordBytes = (size_t)1 << 30;
 
 int prefill_alloc(hako_gpu_decoder *d) {
 	if (d->pf_x) return HAKO_GPU_OK;
 	const hako_gpu_model &m = d->m;
-	const size_t C = kPrefillChunk, D = m.d_model, F = m.ffn_dim, KV = d->kv_dim;
+	const size_t rec_per_token = (size_t)4 * m.n_kv_heads * d->max_chunks * kMaxG * (m.head_dim + 2);
+	size_t C = kPrefillMax;
+	while (C > 16 && C * rec_per_token > kPrefillRecordBytes) C /= 2;
+	d->pf_chunk = (int)C;
+	const size_t D = m.d_model, F = m.ffn_dim, KV = d->kv_dim;
 	int rc = 0;
 #define HK_ALLOC(ptr, bytes) \
 	if (!rc) rc = dalloc(d, (bytes), (void **)&(ptr))
@@ -1070,7 +1079,7 @@ int prefill_alloc(hako_gpu_decoder *d) {
 	HK_ALLOC(d->pf_tmp, 4 * C * D);
 	HK_ALLOC(d->pf_g, 4 * C * F);
 	HK_ALLOC(d->pf_u, 4 * C * F);
-	HK_ALLOC(d->pf_part, 4 * C * m.n_kv_heads * d->max_chunks * kMaxG * (m.head_dim + 2));
+	HK_ALLOC(d->pf_part, C * rec_per_token);
 	HK_ALLOC(d->pf_tok, 4 * C);
 	HK_ALLOC(d->pf_pos, 4 * C);
 #undef HK_ALLOC
@@ -1078,17 +1087,17 @@ int prefill_alloc(hako_gpu_decoder *d) {
 	return rc;
 }
 
-// Tokens [0, n) of sequence seq at positions pos0.. (n <= kPrefillChunk):
+// Tokens [0, n) of sequence seq at positions pos0.. (n <= pf_chunk):
 // every layer for all of them, each matmul one multi-token launch, causal
 // attention over the cache (the chunk's keys and values appended first).
 int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int pos0) {
 	const hako_gpu_model &m = d->m;
 	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, HD = m.head_dim, KVH = m.n_kv_heads;
 	const int G = m.n_heads / KVH;
-	int posv[kPrefillChunk];
+	std::vector<int> posv(n);
 	for (int i = 0; i < n; i++) posv[i] = pos0 + i;
 	HK_HIP(hipMemcpyAsync(d->pf_tok, tokens, sizeof(int) * n, hipMemcpyHostToDevice, stream()));
-	HK_HIP(hipMemcpyAsync(d->pf_pos, posv, sizeof(int) * n, hipMemcpyHostToDevice, stream()));
+	HK_HIP(hipMemcpyAsync(d->pf_pos, posv.data(), sizeof(int) * n, hipMemcpyHostToDevice, stream()));
 	HK_HIP(hipStreamSynchronize(stream()));   // posv is this frame's
 	hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
 	                   row_bytes(m.t_embd, D), d->pf_tok, d->pf_x, D, m.vocab);
@@ -1321,8 +1330,8 @@ int hako_gpu_decoder_prefill(hako_gpu_decoder *d, int seq, const int *tokens, in
 	if (int rc = prefill_alloc(d)) return rc;
 	const int D = m.d_model;
 	int last = 0;
-	for (int c0 = 0; c0 < n; c0 += kPrefillChunk) {
-		last = n - c0 < kPrefillChunk ? n - c0 : kPrefillChunk;
+	for (int c0 = 0; c0 < n; c0 += d->pf_chunk) {
+		last = n - c0 < d->pf_chunk ? n - c0 : d->pf_chunk;
 		if (int rc = prefill_chunk(d, seq, tokens + c0, last, pos0 + c0)) return rc;
 	}
 	// logits of the last prompt token (what feed returns), into the

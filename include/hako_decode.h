@@ -86,7 +86,8 @@ int hako_gpu_decoder_generate(hako_gpu_decoder *dec, const int *tokens, int n, i
 
 /* Feeds n prompt tokens (host) to sequence seq from its current position,
  * as the reference's feed (src/hakm_api.c:105-111, one hakm_forward per
- * token) but through the multi-token matmuls, up to 128 tokens per pass,
+ * token) but through the multi-token matmuls, up to 512 tokens per pass
+ * (fewer when max_seq makes the attention records of a pass exceed 1 GiB),
  * with causal attention over the sequence's cache: the keys and values of
  * every prompt position are written, the position advances by n, and the
  * logits of the last prompt token go to logits[vocab] (host, may be NULL)

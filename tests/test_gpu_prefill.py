@@ -18,7 +18,7 @@ from helpers import maxabs_rel
 pytestmark = pytest.mark.gpu
 
 TINY = mlf2.Qwen2Config(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512,
-                        vocab=1024, ctx=512)
+                        vocab=1024, ctx=40000)
 TINY_UNTIED = mlf2.Qwen2Config(n_layers=2, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=768,
                                vocab=768, ctx=256, tied=False, embd_type=synth.TYPE_Q4_K)
 SMALL_128 = mlf2.Qwen2Config(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=2816,
@@ -89,12 +89,24 @@ def make(gpu, path, n_seq, max_seq):
     return Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
 
 
-@pytest.mark.parametrize("cfg,seed,n_prompt", [(TINY, 1, 37), (TINY_UNTIED, 2, 50), (SMALL_128, 3, 140),
-                                               (DENSE, 4, 21), (TINY, 5, 300)])
-def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt):
+# The reference's forward keeps the attention scores of a head in its
+# ffn_dim-float gate buffer (src/model.c:123-124, "needs pos+1 <= F"): a
+# context longer than ffn_dim overruns its heap, so long prompts run on a
+# model whose ffn_dim covers them.
+TINY_LONG = mlf2.Qwen2Config(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=1024,
+                             vocab=1024, ctx=40000)
+
+
+# (cfg, seed, prompt length, max_seq): 600 tokens cross a 512-token pass;
+# max_seq 40000 makes the pass 256 tokens (records capped at 1 GiB), which
+# 300 tokens cross
+@pytest.mark.parametrize("cfg,seed,n_prompt,max_seq", [(TINY, 1, 37, 384), (TINY_UNTIED, 2, 50, 384),
+                                                       (SMALL_128, 3, 140, 384), (DENSE, 4, 21, 384),
+                                                       (TINY_LONG, 5, 600, 640), (TINY, 6, 300, 40000)])
+def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt, max_seq):
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, seed)
-    max_seq, steps = 384, 8
+    steps = 8
     prompt = np.random.default_rng(seed).integers(0, cfg.vocab, n_prompt).astype(np.int32)
     r = RefSeq(ref, path, max_seq, cfg)
     try:
@@ -176,8 +188,8 @@ def test_prefill_sequences_of_a_batched_decoder(gpu, ref, tmp_path):
 
 
 def test_prefill_qwen2_3b_prompt(gpu, ref, tmp_path):
-    """The full Qwen2.5-3B shape: a 150-token prompt (two prefill passes),
-    last logits and three greedy tokens against the reference's feed."""
+    """The full Qwen2.5-3B shape: a 150-token prompt, last logits and three
+    greedy tokens against the reference's feed."""
     cfg = mlf2.QWEN2_3B
     path = str(tmp_path / "qwen2_3b.mlf2")
     mlf2.write_qwen2(path, cfg, 32)
