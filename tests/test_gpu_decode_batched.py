@@ -174,3 +174,35 @@ def test_qwen2_7b_sixteen_sequences(gpu, ref, tmp_path):
         assert np.all(np.isfinite(want_logits))
         assert got[:, s].tolist() == want, f"sequence {s} (position {pos[s]})"
         assert maxabs_rel(lg[s], want_logits[0]) < 2e-3, f"sequence {s}"
+
+
+def test_batched_sequences_reach_max_seq(gpu, ref, tmp_path):
+    """Sequences at different positions, one of them one step from max_seq:
+    that step is taken (the last cache row of that sequence is written and
+    its tokens match the reference); the next step is refused for everyone."""
+    from dropin import prefilled_greedy
+    from hako_amd.decoder import Decoder
+    from hako_amd.gpu import HakoGpuError
+    cfg = TINY
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, 14)
+    n_seq, max_seq = 3, 128
+    pos = np.array([0, 60, max_seq - 1], np.int32)
+    rng = np.random.default_rng(14)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    kvs = [rng.standard_normal((2, cfg.n_layers, int(p), kvd)).astype(np.float32) for p in pos]
+    starts = np.array([3, 4, 5], np.int32)
+    dec = Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
+    try:
+        fill_kv(gpu, dec, kvs, cfg.n_layers)
+        dec.set_pos(pos)
+        toks, lg = dec.step(starts, logits=True)
+        with pytest.raises(HakoGpuError, match="no room"):
+            dec.step(toks)
+    finally:
+        dec.close()
+    for s in range(n_seq):
+        want, want_lg = prefilled_greedy(ref, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=1,
+                                         vocab=cfg.vocab, max_seq=max_seq)
+        assert int(toks[s]) == want[0]
+        assert maxabs_rel(lg[s], want_lg[0]) < 2e-2

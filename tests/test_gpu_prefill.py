@@ -227,3 +227,46 @@ def test_prefill_rejects_bad_use(gpu, tmp_path):
         assert isinstance(dec.prefill([1, 2, 3], seq=0), int)
     finally:
         dec.close()
+
+
+def test_prefill_of_one_token_equals_a_step(gpu, tmp_path):
+    """A one-token prompt is one forward: the same logits as a decode step
+    from the same state (the pass's matmuls are the single-token GEMVs)."""
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, SMALL_128, 10)
+    dec = make(gpu, path, 1, 64)
+    try:
+        dec.set_pos(0)
+        t = dec.prefill([5, 6, 7])
+        _, a = dec.prefill([t], logits=True)
+        dec.set_pos(0)
+        dec.prefill([5, 6, 7])
+        _, b = dec.step(t, logits=True)
+    finally:
+        dec.close()
+    assert maxabs_rel(a, b[0]) < 2e-3
+
+
+def test_prefill_fills_the_cache_to_max_seq(gpu, ref, tmp_path):
+    """A prompt that ends exactly at max_seq: the last position is written,
+    the logits are the reference's, and no further step fits."""
+    from hako_amd.gpu import HakoGpuError
+    cfg = TINY
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, 11)
+    max_seq = 96
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab, max_seq)
+    r = RefSeq(ref, path, max_seq, cfg)
+    try:
+        want_lg = r.feed(prompt)
+    finally:
+        r.close()
+    dec = make(gpu, path, 1, max_seq)
+    try:
+        dec.set_pos(0)
+        _, lg = dec.prefill(prompt, logits=True)
+        with pytest.raises(HakoGpuError, match="no room"):
+            dec.step(1)
+    finally:
+        dec.close()
+    assert maxabs_rel(lg, want_lg) < 2e-2
