@@ -341,9 +341,10 @@ def bench_prompt(g, n_prompt: int, cpu_tokens: int, seed: int = 50) -> dict:
         os.unlink(path)
 
 
-def bench_prefill(g, launches: int) -> dict:
+def bench_prefill(g, launches: int, eager: bool = False) -> dict:
     """The 7B prefill matmuls: Q4_K 18944x3584 x 512 tokens (q8_32 quantize +
-    int8-MFMA GEMM) and Q6_K 3584x18944 x 512 tokens (fp16-MFMA GEMM)."""
+    int8-MFMA GEMM) and Q6_K 3584x18944 x 512 tokens (fp16-MFMA GEMM).
+    `eager` launches from Python (per-dispatch counter collection)."""
     out = {}
     for name, qt, m, n_out, n_in in (("q4k_7b_ffn_up_512x18944x3584", synth.TYPE_Q4_K, 512, 18944, 3584),
                                      ("q6k_7b_ffn_down_512x3584x18944", synth.TYPE_Q6_K, 512, 3584, 18944)):
@@ -353,7 +354,7 @@ def bench_prefill(g, launches: int) -> dict:
         dw, dx, dy = g.upload(w), g.upload(x), g.alloc(m * n_out * 4)
         g.matmul_batch(dy, dx, qt, dw, None, m, n_out, n_in)   # sizes the workspace outside the capture
         g.sync()
-        r = _time_launches(g, lambda k: g.matmul_batch(dy, dx, qt, dw, None, m, n_out, n_in), launches, 3, False)
+        r = _time_launches(g, lambda k: g.matmul_batch(dy, dx, qt, dw, None, m, n_out, n_in), launches, 3, eager)
         for b in (dw, dx, dy):
             b.free()
         ops = 2.0 * m * n_out * n_in
@@ -423,7 +424,7 @@ def main():
         elif args.only == "prompt":
             r = bench_prompt(g, args.prompt_tokens, 0)
         else:
-            r = bench_prefill(g, 30)
+            r = bench_prefill(g, 30, args.eager)
         print(json.dumps(r), flush=True)
         return
     if args.only:
