@@ -150,6 +150,8 @@ int hako_gpu_tune(int knob, int value) {
 	case HAKO_TUNE_Q4K_WAVES: q4k_set_waves(value); return ok();
 	case HAKO_TUNE_Q6K_WAVES: q6k_set_waves(value); return ok();
 	case HAKO_TUNE_Q4K_FLAT_ITEMS: q4k_set_flat_items(value); return ok();
+	case HAKO_TUNE_SKINNY_Q4K_WGS: q4k_skinny_set_target_wgs(value); return ok();
+	case HAKO_TUNE_SKINNY_Q6K_WGS: q6k_skinny_set_target_wgs(value); return ok();
 	default: return set_error(HAKO_GPU_EINVAL, "unknown tuning knob %d", knob);
 	}
 }
@@ -284,14 +286,14 @@ int hako_gpu_mirror_upload(const void *host, size_t bytes, void **dev) {
 	State &s = st();
 	std::lock_guard<std::mutex> lk(s.mu);
 	const uint8_t *h = (const uint8_t *)host;
-	for (auto &m : s.mirrors) {
-		if (h >= m.host && h + bytes <= m.host + m.bytes) {
-			if (dev) *dev = m.dev + (h - m.host);
-			return ok();
-		}
+	// An overlap is refused, never reused: the older mirror may hold memory
+	// that was freed or unmapped since, now holding other bytes.
+	for (auto &m : s.mirrors)
 		if (h < m.host + m.bytes && m.host < h + bytes)
-			return set_error(HAKO_GPU_EINVAL, "range overlaps an existing mirror only in part");
-	}
+			return set_error(HAKO_GPU_EINVAL,
+			                 "host range [%p, +%zu) overlaps the mirror of [%p, +%zu): release that mirror first "
+			                 "(host memory freed or unmapped while mirrored leaves its mirror in place)",
+			                 (const void *)h, bytes, (const void *)m.host, m.bytes);
 	Mirror m{h, bytes, nullptr};
 	if (hipMalloc((void **)&m.dev, bytes ? bytes : 1) != hipSuccess) {
 		(void)hipGetLastError();

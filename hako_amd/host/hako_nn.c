@@ -54,7 +54,7 @@ void rope_neox(float *vec, int head_dim, int pos, float theta) {
  * One entry per mapped model: its data section lives in HBM for as long as
  * the entry does. A different file mapped at the same address is told apart
  * by its size, header and a sampled signature of its data, and replaces the
- * stale mirror. */
+ * stale mirror; so does one mapped over part of a stale entry's range. */
 
 typedef struct {
 	const void *map;
@@ -108,6 +108,14 @@ static int upload_locked(const hakm_model *m) {
 		    memcmp(&e->h, &m->h, sizeof e->h) == 0)
 			return 0;
 		drop_model(i);
+	}
+	/* an entry whose bytes overlap this live mapping belongs to a model
+	 * unmapped since (two live mappings never overlap): stale, dropped */
+	const unsigned char *lo = m->data, *hi = m->data + data_extent(m);
+	for (int k = g_nmodels - 1; k >= 0; k--) {
+		const unsigned char *elo = g_models[k].data;
+		const unsigned char *ehi = (const unsigned char *)g_models[k].map + g_models[k].map_size;
+		if (elo < hi && lo < ehi) drop_model(k);
 	}
 	if (g_nmodels == HK_MAX_MODELS) drop_model(0);
 	rc = hako_gpu_mirror_upload(m->data, data_extent(m), NULL);

@@ -58,6 +58,11 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_Q4K_WAVES      3
 #define HAKO_TUNE_Q6K_WAVES      4
 #define HAKO_TUNE_Q4K_FLAT_ITEMS 5   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
+/* Workgroups a skinny (2..16 token) Q4_K / Q6_K launch aims for through its
+ * K split (0: the defaults, 512 and 1024). A decoder sizes its split workspace when it is
+ * created; a later, larger target makes its steps fail with EINVAL. */
+#define HAKO_TUNE_SKINNY_Q4K_WGS 6
+#define HAKO_TUNE_SKINNY_Q6K_WGS 7
 int hako_gpu_tune(int knob, int value);
 
 typedef struct {
@@ -102,7 +107,10 @@ int hako_gpu_graph_destroy(void *graph);
  * remembers the range, so that any host pointer p inside it maps to
  * dev + (p - host). This is how an mmap'd MLF2 data section (reference
  * src/loader.c:12-52; tensors at data + data_off, src/loader.c:66-68) is put
- * in HBM byte for byte. A range already mirrored is not copied again. */
+ * in HBM byte for byte. A range that overlaps a mirror is refused (EINVAL):
+ * release the older mirror first — memory freed or unmapped while mirrored
+ * keeps its mirror until hako_gpu_mirror_release, and a later buffer at
+ * those addresses holds other bytes. */
 int hako_gpu_mirror_upload(const void *host, size_t bytes, void **dev);
 int hako_gpu_mirror_release(const void *host);
 /* Device address of host pointer p inside a mirror; NULL if none holds it. */

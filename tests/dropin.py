@@ -63,9 +63,11 @@ def bind_ctx(lib: C.CDLL) -> C.CDLL:
     return lib
 
 
-def greedy(lib: C.CDLL, path: str, start: int, steps: int, vocab: int, max_seq: int = 64):
+def greedy(lib: C.CDLL, path: str, start: int, steps: int, vocab: int, max_seq: int = 64, release=None):
     """Greedy decode through a library exporting the reference's model.h API:
-    returns the token ids and the logits of every step."""
+    returns the token ids and the logits of every step. `release(ctx)`, when
+    given, runs before hakm_ctx_free unmaps the model (the drop-in's
+    hako_model_release: the model's HBM mirror goes with its mapping)."""
     ctx = lib.hakm_ctx_new(path.encode(), max_seq)
     assert ctx, f"hakm_ctx_new({path}) failed"
     toks, logits = [start], []
@@ -76,6 +78,8 @@ def greedy(lib: C.CDLL, path: str, start: int, steps: int, vocab: int, max_seq: 
             logits.append(lg)
             toks.append(int(np.argmax(lg)))   # first maximum, as src/sample.c:28-32
     finally:
+        if release is not None:
+            release(ctx)
         lib.hakm_ctx_free(ctx)
     return toks[1:], np.stack(logits)
 

@@ -99,7 +99,7 @@ def test_reference_model_c_on_dropin(host, tmp_path, cfg, seed):
     dropin = bind_ctx(C.CDLL(REF_MODEL_LIB))        # model.c + loader.c -> libhako.so
     assert os.path.exists(REF_MODEL_LIB)
     t_ref, l_ref = greedy(ref, path, start=1, steps=8, vocab=cfg.vocab)
-    t_gpu, l_gpu = greedy(dropin, path, start=1, steps=8, vocab=cfg.vocab)
+    t_gpu, l_gpu = greedy(dropin, path, start=1, steps=8, vocab=cfg.vocab, release=host.hako_model_release)
     assert t_gpu == t_ref
     # logits drift only through ±1 flips of re-quantized activations
     assert maxabs_rel(l_gpu, l_ref) < 2e-2

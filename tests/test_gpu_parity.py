@@ -243,6 +243,26 @@ def test_matmul_host_uses_mirror(gpu, oracle):
     assert maxabs_rel(out, oracle.matmul(Q4, w, x, 600, 2048)) < TOL
 
 
+def test_mirror_overlaps_are_refused(gpu):
+    """A range overlapping a live mirror (inside it, or across its end) is
+    refused rather than served from the older copy; after the release the
+    same bytes upload again."""
+    from hako_amd.gpu import HakoGpuError
+    buf = np.arange(4096, dtype=np.uint8)
+    gpu.mirror_upload(buf[1024:3072])
+    try:
+        for view in (buf[1024:3072], buf[2048:2560], buf[0:1500], buf[3000:]):
+            with pytest.raises(HakoGpuError, match="overlaps"):
+                gpu.mirror_upload(view)
+        gpu.mirror_upload(buf[:1024])        # adjacent, disjoint
+        gpu.mirror_release(buf[:1024])
+    finally:
+        gpu.mirror_release(buf[1024:3072])
+    d = gpu.mirror_upload(buf[0:1500])
+    gpu.mirror_release(buf[0:1500])
+    assert d
+
+
 def test_bad_shapes_are_rejected(gpu):
     from hako_amd.gpu import HakoGpuError
     dw, dx, do = gpu.alloc(4096), gpu.alloc(4096), gpu.alloc(4096)
