@@ -764,6 +764,7 @@ struct hako_gpu_decoder {
 	// batched steps (n_seq > 1): q8 and fp16 hi/lo activations, split-K state
 	int8_t *xq = nullptr;
 	float *xs = nullptr, *esc = nullptr, *skpart = nullptr;
+	size_t skpart_floats = 0;   // capacity of skpart
 	_Float16 *xh = nullptr, *xl = nullptr;
 	// prompt prefill (allocated on first use): chunk activations and records
 	float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr,
@@ -905,28 +906,28 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 		s.s[0] = {(const uint8_t *)B.wq, B.bq, d->qkv, 0, D, d->qkv_dim};
 		s.s[1] = {(const uint8_t *)B.wk, B.bk, d->qkv + D, D, KV, d->qkv_dim};
 		s.s[2] = {(const uint8_t *)B.wv, B.bv, d->qkv + D + KV, D + KV, KV, d->qkv_dim};
-		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, D + 2 * KV, d->skpart)) return rc;
+		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, D + 2 * KV, d->skpart, d->skpart_floats)) return rc;
 		// 2. attention, one grid over every sequence; q8 rows of its output
 		if (int rc = attention(d, l, d->xq, d->xs)) return rc;
 		// 3. output projection: partials, added to the residual by step 4
 		s = SkSegs{};
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D, D};
-		if (int rc = q4k_skinny(s, kSkPart, d->xq, d->xs, M, D, D, d->skpart)) return rc;
+		if (int rc = q4k_skinny(s, kSkPart, d->xq, d->xs, M, D, D, d->skpart, d->skpart_floats)) return rc;
 		// 4. residual, rmsnorm, q8; gate, up, SwiGLU
 		if (int rc = resid_rmsnorm_q8(d, d->skpart, ns_o, B.ffn_norm, D)) return rc;
 		s = SkSegs{};
 		s.n = 2;
 		s.s[0] = {(const uint8_t *)B.gate, nullptr, d->h, 0, F, F};
 		s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, F, F, F};
-		if (int rc = q4k_skinny(s, kSkSwiGLU, d->xq, d->xs, M, D, 2 * F, d->skpart)) return rc;
+		if (int rc = q4k_skinny(s, kSkSwiGLU, d->xq, d->xs, M, D, 2 * F, d->skpart, d->skpart_floats)) return rc;
 		// 5. the down matmul's fp16 hi/lo rows
 		if (int rc = f16_split(d->h, d->xh, d->xl, d->esc, M, F)) return rc;
 		// 6. down projection: partials, added to the residual by the next kernel
 		s = SkSegs{};
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.down, nullptr, d->x, 0, D, D};
-		if (int rc = q6k_skinny(s, kSkPart, d->xh, d->xl, d->esc, M, F, D, d->skpart)) return rc;
+		if (int rc = q6k_skinny(s, kSkPart, d->xh, d->xl, d->esc, M, F, D, d->skpart, d->skpart_floats)) return rc;
 		pend = d->skpart;
 		pend_ns = ns_down;
 	}
@@ -935,12 +936,12 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 	s.s[0] = {(const uint8_t *)m.out_weight, nullptr, d->logits, 0, m.vocab, m.vocab};
 	if (m.t_out == HAKO_TYPE_Q4_K) {
 		if (int rc = resid_rmsnorm_q8(d, pend, pend_ns, m.out_norm, D)) return rc;
-		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, m.vocab, d->skpart)) return rc;
+		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, m.vocab, d->skpart, d->skpart_floats)) return rc;
 	} else {
 		hipLaunchKernelGGL(resid_rmsnorm_split_kernel, dim3(M), dim3(kRowT), 0, stream(), d->x, pend, pend_ns,
 		                   m.out_norm, m.rms_eps, d->xh, d->xl, d->esc, D);
 		HK_LAUNCHED("resid_rmsnorm_split");
-		if (int rc = q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, D, m.vocab, d->skpart)) return rc;
+		if (int rc = q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, D, m.vocab, d->skpart, d->skpart_floats)) return rc;
 	}
 	if (int rc = argmax(d)) return rc;
 	return HAKO_GPU_OK;
@@ -1231,6 +1232,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 		HK_ALLOC(d->xl, sizeof(_Float16) * n_seq * DF);
 		HK_ALLOC(d->esc, sizeof(float) * n_seq);
 		HK_ALLOC(d->skpart, sizeof(float) * (skpart ? skpart : 1));
+		d->skpart_floats = skpart;
 	}
 #undef HK_ALLOC
 	if (rc) {

@@ -439,8 +439,9 @@ int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const f
 		segs.n = 1;
 		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
 		float *part = nullptr;
-		if (int rc = skinny_split_workspace(q4k_skinny_part_floats(n_in, n_out, kSkStore), &part)) return rc;
-		if (int rc = q4k_skinny(segs, kSkStore, xq, xs, m, n_in, n_out, part)) return rc;
+		const size_t pf = q4k_skinny_part_floats(n_in, n_out, kSkStore);
+		if (int rc = skinny_split_workspace(pf, &part)) return rc;
+		if (int rc = q4k_skinny(segs, kSkStore, xq, xs, m, n_in, n_out, part, pf)) return rc;
 		return ok();
 	}
 	hipLaunchKernelGGL(q4k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
@@ -471,8 +472,9 @@ int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, 
 		segs.n = 1;
 		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
 		float *part = nullptr;
-		if (int rc = skinny_split_workspace(q6k_skinny_part_floats(n_in, n_out, kSkStore), &part)) return rc;
-		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part)) return rc;
+		const size_t pf = q6k_skinny_part_floats(n_in, n_out, kSkStore);
+		if (int rc = skinny_split_workspace(pf, &part)) return rc;
+		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part, pf)) return rc;
 		return ok();
 	}
 	hipLaunchKernelGGL(q6k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,

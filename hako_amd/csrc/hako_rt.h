@@ -27,6 +27,9 @@ void q6k_set_wgs_per_cu(int v);
 void q4k_set_waves(int v);
 void q6k_set_waves(int v);
 void q4k_set_flat_items(int v);
+// Target workgroups of the skinny (<= 16 token) launches (0: default).
+void q4k_skinny_set_target_wgs(int wgs);
+void q6k_skinny_set_target_wgs(int wgs);
 // Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
 int workspace(int slot, size_t bytes, void **ptr);
 

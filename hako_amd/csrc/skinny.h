@@ -31,22 +31,27 @@ struct SkSegs {
 // split, tokens past m zero) for a consumer that sums them itself.
 enum { kSkStore = 0, kSkAdd = 1, kSkSwiGLU = 2, kSkPart = 3 };
 
-// Workgroups a launch aims for (4 per CU); K is split over workgroups to
-// reach it. Split results go to `part` (the *_part_floats count of floats),
-// summed by a second launch that applies the epilogue.
+// Workgroups a launch aims for; K is split over workgroups to reach it.
+// Split results go to `part` (the *_part_floats count of floats; part_cap is
+// what the caller holds), summed by a second launch that applies the
+// epilogue. Q4_K: 2 per CU. Q6_K: 4 per CU — its waves wait on one
+// super-block of weights per barrier, so more of them in flight pay (the
+// 7B down matmul over 16 tokens: 18 splits instead of 10, 3.4% of a
+// 16-sequence step). Both are launch-shape knobs (hako_gpu_tune).
 constexpr int kSkTargetWgs = 512;
+constexpr int kSkTargetWgsQ6 = 1024;
 
 // Q4_K x q8: xq [m][n_in] int8 and xs [m][n_in/32] (q8_32 rows), m <= 16.
 int q4k_skinny_splits(int n_in, int vrows);
 size_t q4k_skinny_part_floats(int n_in, int vrows, int epi);
 int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
-               float *part);
+               float *part, size_t part_cap);
 // Q6_K x fp32 as fp16 hi/lo rows [m][n_in] with a power of two per token,
 // esc[m] (x = (hi + lo) * esc); Store, Add or Part.
 int q6k_skinny_splits(int n_in, int vrows);
 size_t q6k_skinny_part_floats(int n_in, int vrows, int epi);
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
-               int n_in, int vrows, float *part);
+               int n_in, int vrows, float *part, size_t part_cap);
 // The fp16 hi/lo split of m fp32 rows of n floats with one power of two per
 // row, esc[m] (gemm.hip).
 int f16_split(const float *x, _Float16 *xh, _Float16 *xl, float *esc, int m, int n);

@@ -404,9 +404,16 @@ int reduce(const SkSegs &segs, int epi, const float *part, int nsplit, int m, in
 
 }  // namespace
 
+namespace {
+int g_q4_target = kSkTargetWgs, g_q6_target = kSkTargetWgsQ6;
+}
+
+void q4k_skinny_set_target_wgs(int wgs) { g_q4_target = wgs > 0 ? wgs : kSkTargetWgs; }
+void q6k_skinny_set_target_wgs(int wgs) { g_q6_target = wgs > 0 ? wgs : kSkTargetWgsQ6; }
+
 int q4k_skinny_splits(int n_in, int vrows) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
-	int ns = (kSkTargetWgs + tiles - 1) / tiles;           // enough workgroups to fill the chip
+	int ns = (g_q4_target + tiles - 1) / tiles;            // enough workgroups to fill the chip
 	const int need = (nb + kQ4SkBlocks - 1) / kQ4SkBlocks;  // at most kQ4SkBlocks per workgroup
 	ns = ns < need ? need : ns;
 	return ns > nb ? nb : ns;
@@ -418,11 +425,13 @@ size_t q4k_skinny_part_floats(int n_in, int vrows, int epi) {
 }
 
 int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
-               float *part) {
+               float *part, size_t part_cap) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
 	const int ns = q4k_skinny_splits(n_in, vrows);
 	const bool direct = ns == 1 && epi != kSkSwiGLU && epi != kSkPart;
-	if (!direct && !part) return set_error(HAKO_GPU_EINVAL, "Q4_K skinny split needs a workspace");
+	if (!direct && (!part || part_cap < q4k_skinny_part_floats(n_in, vrows, epi)))
+		return set_error(HAKO_GPU_EINVAL, "Q4_K skinny split needs a workspace of %zu floats (has %zu)",
+		                 q4k_skinny_part_floats(n_in, vrows, epi), part ? part_cap : (size_t)0);
 	const dim3 grid(tiles * ns);
 	if (!direct)
 		hipLaunchKernelGGL(q4k_skinny_kernel<kSkPart>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, ns,
@@ -439,7 +448,7 @@ int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, i
 
 int q6k_skinny_splits(int n_in, int vrows) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
-	int ns = (kSkTargetWgs + tiles - 1) / tiles;       // enough workgroups to fill the chip
+	int ns = (g_q6_target + tiles - 1) / tiles;        // enough workgroups to fill the chip
 	ns = ns > nb / 4 ? nb / 4 : ns;                    // at least four super-blocks per split
 	return ns < 1 ? 1 : ns;
 }
@@ -450,11 +459,13 @@ size_t q6k_skinny_part_floats(int n_in, int vrows, int epi) {
 }
 
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
-               int n_in, int vrows, float *part) {
+               int n_in, int vrows, float *part, size_t part_cap) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
 	const int ns = q6k_skinny_splits(n_in, vrows);
 	const bool direct = ns == 1 && epi != kSkPart;
-	if (!direct && !part) return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace");
+	if (!direct && (!part || part_cap < q6k_skinny_part_floats(n_in, vrows, epi)))
+		return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace of %zu floats (has %zu)",
+		                 q6k_skinny_part_floats(n_in, vrows, epi), part ? part_cap : (size_t)0);
 	const dim3 grid(tiles * ns);
 	if (!direct)
 		hipLaunchKernelGGL(q6k_skinny_kernel<kSkPart>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,

@@ -26,6 +26,11 @@ SMALL_128 = mlf2.Qwen2Config(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, 
 UNTIED_Q4_OUT = mlf2.Qwen2Config(n_layers=2, d_model=1792, n_heads=14, n_kv_heads=2, head_dim=128, ffn_dim=1536,
                                  vocab=2000, ctx=256, tied=False, embd_type=synth.TYPE_Q4_K,
                                  out_type=synth.TYPE_Q4_K)
+# long contexts (the reference keeps a head's scores in its ffn_dim-float
+# gate buffer, src/model.c:123-124, so ffn_dim covers max_seq): several
+# workgroups of chunks per sequence, the last one partial
+LONG = mlf2.Qwen2Config(n_layers=2, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=2304,
+                        vocab=1024, ctx=2304)
 
 
 @pytest.fixture(scope="module")
@@ -54,15 +59,17 @@ def seq_setup(cfg, n_seq, seed, max_pos):
     return pos.astype(np.int32), starts.astype(np.int32), kvs
 
 
-@pytest.mark.parametrize("cfg,n_seq,seed", [(TINY, 4, 1), (TINY, 16, 2), (SMALL_128, 16, 3),
-                                            (UNTIED_Q4_OUT, 5, 4)])
-def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, n_seq, seed):
+@pytest.mark.parametrize("cfg,n_seq,seed,max_seq,max_pos", [(TINY, 4, 1, 256, 200), (TINY, 16, 2, 256, 200),
+                                                             (SMALL_128, 16, 3, 256, 200),
+                                                             (UNTIED_Q4_OUT, 5, 4, 256, 200),
+                                                             (LONG, 6, 5, 2304, 2200)])
+def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, n_seq, seed, max_seq, max_pos):
     from dropin import prefilled_greedy
     from hako_amd.decoder import Decoder
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, seed)
-    max_seq, steps = 256, 8
-    pos, starts, kvs = seq_setup(cfg, n_seq, seed, 200)
+    steps = 8
+    pos, starts, kvs = seq_setup(cfg, n_seq, seed, max_pos)
     dec = Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
     try:
         fill_kv(gpu, dec, kvs, cfg.n_layers)
