@@ -604,6 +604,7 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
                                                         float *__restrict__ xs, int H, int KVH, int max_seq,
                                                         int max_chunks) {
 	constexpr int REC = HD + 2, NW = HD / 64;
+	constexpr int OB = 16;                       // o rows in flight per thread
 	constexpr size_t CS = (size_t)kMaxG * REC;   // floats between two chunks' records of one head
 	__shared__ float w_s[HD];
 	__shared__ float r_s[2][NW];
@@ -614,16 +615,26 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
 	if (pos < 0 || pos >= max_seq) return;
 	const int nact = pos / kChunk + 1;
 	const float *grp = part + ((size_t)(sq * KVH + kvh) * max_chunks * kMaxG + g) * REC;
-	float mx = -INFINITY;
-	for (int cc = tid; cc < nact; cc += HD) mx = __builtin_fmaxf(mx, grp[cc * CS + HD]);
+	// one round trip for the common case (nact <= HD chunks): every thread's
+	// (m, l) of chunk tid and its value dim of the first OB chunks, issued together
+	float m0 = -INFINITY, l0 = 0.0f;
+	if (tid < nact) {
+		m0 = grp[tid * CS + HD];
+		l0 = grp[tid * CS + HD + 1];
+	}
+	float ov[OB];
+#pragma unroll
+	for (int j = 0; j < OB; j++) ov[j] = j < nact ? grp[j * CS + tid] : 0.0f;
+	float mx = m0;
+	for (int cc = tid + HD; cc < nact; cc += HD) mx = __builtin_fmaxf(mx, grp[cc * CS + HD]);
 	mx = wave_max(mx);
 	if (lane == 0) r_s[0][wave] = mx;
 	__syncthreads();
 	mx = r_s[0][0];
 #pragma unroll
 	for (int w = 1; w < NW; w++) mx = __builtin_fmaxf(mx, r_s[0][w]);
-	float lsum = 0.0f;
-	for (int cc = tid; cc < nact; cc += HD) lsum += grp[cc * CS + HD + 1] * expf(grp[cc * CS + HD] - mx);
+	float lsum = tid < nact ? l0 * expf(m0 - mx) : 0.0f;
+	for (int cc = tid + HD; cc < nact; cc += HD) lsum += grp[cc * CS + HD + 1] * expf(grp[cc * CS + HD] - mx);
 	lsum = wave_sum(lsum);
 	if (lane == 0) r_s[1][wave] = lsum;
 	__syncthreads();
@@ -631,20 +642,27 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
 #pragma unroll
 	for (int w = 1; w < NW; w++) lsum += r_s[1][w];
 	const float inv = 1.0f / lsum;
+	// output: sum over chunks, in chunk order, of weight * o
 	float acc = 0.0f;
 	for (int c0 = 0; c0 < nact; c0 += HD) {
 		const int nc = min(HD, nact - c0);
-		__syncthreads();   // w_s of the previous batch is consumed
-		if (tid < nc) w_s[tid] = expf(grp[(c0 + tid) * CS + HD] - mx) * inv;
+		if (c0) __syncthreads();   // w_s of the previous batch is consumed
+		if (tid < nc) w_s[tid] = expf((c0 ? grp[(c0 + tid) * CS + HD] : m0) - mx) * inv;
 		__syncthreads();
 		const float *r = grp + c0 * CS + tid;
 		int cc = 0;
-		for (; cc + 8 <= nc; cc += 8) {
-			float o[8];
+		if (c0 == 0) {
 #pragma unroll
-			for (int j = 0; j < 8; j++) o[j] = r[(cc + j) * CS];
+			for (int j = 0; j < OB; j++)
+				if (j < nc) acc = __builtin_fmaf(ov[j], w_s[j], acc);
+			cc = min(OB, nc);
+		}
+		for (; cc + OB <= nc; cc += OB) {
+			float o[OB];
 #pragma unroll
-			for (int j = 0; j < 8; j++) acc = __builtin_fmaf(o[j], w_s[cc + j], acc);
+			for (int j = 0; j < OB; j++) o[j] = r[(cc + j) * CS];
+#pragma unroll
+			for (int j = 0; j < OB; j++) acc = __builtin_fmaf(o[j], w_s[cc + j], acc);
 		}
 		for (; cc < nc; cc++) acc = __builtin_fmaf(r[cc * CS], w_s[cc], acc);
 	}
