@@ -167,6 +167,13 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 
 	Q6Col col;
 	q6_col_load(x, cc, col);   // issued first: these loads return first
+	// The residual and bias of the row this thread finishes, loaded now: at
+	// the end they would add a round trip after the weight stream.
+	float res0 = 0.0f, bias0 = 0.0f;
+	if (threadIdx.x < nrows) {
+		if (acc_out) res0 = out[r0 + threadIdx.x];
+		if (bias) bias0 = bias[r0 + threadIdx.x];
+	}
 	// Keep every weight load below the activation loads (completion is in
 	// issue order).
 	__builtin_amdgcn_sched_barrier(0);
@@ -217,8 +224,9 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 		for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
 			float v = 0.0f;
 			for (int p = 0; p < G.tpr; p++) v += red_s[r * G.tpr + p];
-			if (bias) v += bias[r0 + r];
-			out[r0 + r] = acc_out ? out[r0 + r] + v : v;
+			const bool first = r == (int)threadIdx.x;
+			if (bias) v += first ? bias0 : bias[r0 + r];
+			out[r0 + r] = acc_out ? (first ? res0 : out[r0 + r]) + v : v;
 		}
 	}
 }
