@@ -417,8 +417,9 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 
 // Workgroup (chunk c, KV head kvh, sequence sq) of 256 threads: positions
 // [64c, 64c+64) up to pos. Every key and value load of the chunk is issued
-// first (thread = position x quarter of the head dims for keys, value dims x
-// 16-position group for values), so the chunk costs one memory latency. The
+// first (thread = position x every fourth float4 of the head dims for keys,
+// value dims x 16-position group for values), so the chunk costs one memory
+// latency. The
 // group's query heads are rotated into LDS (NeoX, the rope table holding
 // cos/sin of pos*theta^(-2i/hd)); the workgroup whose chunk holds pos also
 // rotates the new key, appends it and the new value to the caches and uses
@@ -437,13 +438,19 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	constexpr int KQ = HD / 16;      // float4 of a key row per thread (4 threads per position)
 	constexpr int DV = HD / 64;      // value dims per thread
 	constexpr int PG = 16;           // positions per value group (4 groups)
-	__shared__ float q_s[kMaxG][HD];
-	__shared__ float s_s[kMaxG][kChunk];        // scores, then e^(score - m)
+	constexpr int QR = HD;           // query row in LDS
+	// LDS: the rotated queries and the scores are dead once the value sums are
+	// in registers; their space then holds the four groups' value sums.
+	constexpr int QS = kMaxG * QR, SS = kMaxG * kChunk, OS = 4 * kMaxG * HD;
+	__shared__ __align__(16) float u_s[QS + SS > OS ? QS + SS : OS];
+	float *q_s = u_s;                // [kMaxG][QR]
+	float *s_s = u_s + QS;           // [kMaxG][kChunk]: scores, then e^(score - m)
+	float *o_s = u_s;                // [4][kMaxG][HD]: value sums per position group
 	__shared__ float ml_s[kMaxG][2];
-	__shared__ float o_s[4][kMaxG][HD];         // value sums per position group
 	__shared__ float kn_s[HD], vn_s[HD];
 	const int c = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z;
-	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: value rows in SGPRs
 	const int G = H / KVH, KV = KVH * HD, D = H * HD;
 	const int pos = posv[sq];
 	if (pos < 0 || pos >= max_seq) return;   // no room left: the host refuses such steps
@@ -453,26 +460,34 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	const float *q = qkv + (size_t)sq * qkv_stride;
 	float *kcs = kc + (size_t)sq * kv_seq_stride + kvh * HD;
 	float *vcs = vc + (size_t)sq * kv_seq_stride + kvh * HD;
-
 	// 1. every key and value load of the chunk (rows past pos read row pos:
-	//    in bounds, discarded)
+	//    in bounds, discarded): raw buffer loads over this sequence's layer
+	//    cache. Keys: load j of the position's four threads reads float4s
+	//    kq + 4j, so the four cover 64 contiguous bytes and two consecutive
+	//    loads whole cache lines. Values: one lane offset plus a wave-uniform
+	//    row offset.
+	const uint32_t cache_bytes = (uint32_t)((size_t)max_seq * KV * 4);
+	const __amdgpu_buffer_rsrc_t krs = stream_rsrc(kc + (size_t)sq * kv_seq_stride, cache_bytes);
+	const __amdgpu_buffer_rsrc_t vrs = stream_rsrc(vc + (size_t)sq * kv_seq_stride, cache_bytes);
 	const int kp = tid >> 2, kq = tid & 3;
 	const int ks = c * kChunk + kp;
-	const float *krow = kcs + (size_t)min(ks, pos) * KV + kq * (HD / 4);
+	const uint32_t koff = ((uint32_t)min(ks, pos) * KV + kvh * HD + 4 * kq) * 4u;
 	float4 kr[KQ];
 #pragma unroll
-	for (int j = 0; j < KQ; j++) kr[j] = *(const float4 *)(krow + 4 * j);
+	for (int j = 0; j < KQ; j++) kr[j] = __builtin_bit_cast(float4, ld_b128(krs, koff + 64u * j));
 	const int vd = DV * lane, vg = wave;
+	const uint32_t voff = (uint32_t)(kvh * HD + vd) * 4u;
 	float vr[PG][DV];
 #pragma unroll
 	for (int j = 0; j < PG; j++) {
-		const float *row = vcs + (size_t)min(c * kChunk + PG * vg + j, pos) * KV + vd;
+		const int row = min(c * kChunk + PG * vg + j, pos);
+		const int soff = row * KV * 4;
 		if (DV == 2) {
-			const float2 t = *(const float2 *)row;
+			const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(vrs, (int)voff, soff, 0));
 			vr[j][0] = t.x;
 			vr[j][DV - 1] = t.y;
 		} else {
-			vr[j][0] = row[0];
+			vr[j][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vrs, (int)voff, soff, 0));
 		}
 	}
 	// rows past pos carry weight 0; zero them too, so no stale value reaches a sum
@@ -488,8 +503,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 		const int g = t / HALF, i = t - g * HALF;
 		const float2 cs = rp[i];
 		const float a = q[(kvh * G + g) * HD + i], b = q[(kvh * G + g) * HD + i + HALF];
-		q_s[g][i] = a * cs.x - b * cs.y;
-		q_s[g][i + HALF] = a * cs.y + b * cs.x;
+		q_s[g * QR + i] = a * cs.x - b * cs.y;
+		q_s[g * QR + i + HALF] = a * cs.y + b * cs.x;
 	}
 	if (has_pos) {
 		for (int i = tid; i < HALF; i += 256) {
@@ -509,26 +524,27 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	}
 	__syncthreads();
 
-	// 3. scores: 4 threads per position, a quarter of the dims each
+	// 3. scores: 4 threads per position, every fourth float4 of the dims each
 	if (APPEND && ks == pos) {
 #pragma unroll
-		for (int j = 0; j < KQ; j++) kr[j] = *(const float4 *)(kn_s + kq * (HD / 4) + 4 * j);
+		for (int j = 0; j < KQ; j++) kr[j] = *(const float4 *)(kn_s + 4 * kq + 16 * j);
 	}
 #pragma unroll
 	for (int g = 0; g < kMaxG; g++) {
 		if (g < G) {
 			float a = 0.0f;
-			const float *qg = q_s[g] + kq * (HD / 4);
+			const float *qg = q_s + g * QR + 4 * kq;
 #pragma unroll
 			for (int j = 0; j < KQ; j++) {
-				a = __builtin_fmaf(qg[4 * j], kr[j].x, a);
-				a = __builtin_fmaf(qg[4 * j + 1], kr[j].y, a);
-				a = __builtin_fmaf(qg[4 * j + 2], kr[j].z, a);
-				a = __builtin_fmaf(qg[4 * j + 3], kr[j].w, a);
+				const float4 qv = *(const float4 *)(qg + 16 * j);
+				a = __builtin_fmaf(qv.x, kr[j].x, a);
+				a = __builtin_fmaf(qv.y, kr[j].y, a);
+				a = __builtin_fmaf(qv.z, kr[j].z, a);
+				a = __builtin_fmaf(qv.w, kr[j].w, a);
 			}
 			a += dpp_f<kDppQuadSwap1>(a);
 			a += dpp_f<kDppQuadSwap2>(a);
-			if (kq == 0) s_s[g][kp] = ks <= pos ? a * scale : -INFINITY;
+			if (kq == 0) s_s[g * kChunk + kp] = ks <= pos ? a * scale : -INFINITY;
 		}
 	}
 	__syncthreads();
@@ -538,11 +554,11 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	for (int h = 0; h < kMaxG / 4; h++) {
 		const int g = wave + 4 * h;
 		if (g < G) {
-			const float v = s_s[g][lane];
+			const float v = s_s[g * kChunk + lane];
 			const float m = wave_max(v);
 			const float e = v == -INFINITY ? 0.0f : expf(v - m);
 			const float l = wave_sum(e);
-			s_s[g][lane] = e;
+			s_s[g * kChunk + lane] = e;
 			if (lane == 0) {
 				ml_s[g][0] = m;
 				ml_s[g][1] = l;
@@ -551,7 +567,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	}
 	__syncthreads();
 
-	// 5. weighted values over this thread's 16 positions, then over the 4 groups
+	// 5. weighted values over this thread's 16 positions (kept in registers
+	//    until every wave is done with the scores), then over the 4 groups
 	if (has_pos) {
 		const int j = pos - c * kChunk - PG * vg;
 		if (j >= 0 && j < PG) {
@@ -562,27 +579,32 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 					for (int u = 0; u < DV; u++) vr[jj][u] = vn_s[vd + u];
 		}
 	}
+	float o[kMaxG][DV];
 #pragma unroll
 	for (int g = 0; g < kMaxG; g++) {
-		if (g < G) {
-			float o[DV];
 #pragma unroll
-			for (int u = 0; u < DV; u++) o[u] = 0.0f;
+		for (int u = 0; u < DV; u++) o[g][u] = 0.0f;
+		if (g < G) {
 #pragma unroll
 			for (int j = 0; j < PG; j++) {
-				const float w = s_s[g][PG * vg + j];
+				const float w = s_s[g * kChunk + PG * vg + j];
 #pragma unroll
-				for (int u = 0; u < DV; u++) o[u] = __builtin_fmaf(w, vr[j][u], o[u]);
+				for (int u = 0; u < DV; u++) o[g][u] = __builtin_fmaf(w, vr[j][u], o[g][u]);
 			}
-#pragma unroll
-			for (int u = 0; u < DV; u++) o_s[vg][g][vd + u] = o[u];
 		}
 	}
+	__syncthreads();   // scores consumed: their space takes the value sums
+#pragma unroll
+	for (int g = 0; g < kMaxG; g++)
+		if (g < G)
+#pragma unroll
+			for (int u = 0; u < DV; u++) o_s[(vg * kMaxG + g) * HD + vd + u] = o[g][u];
 	__syncthreads();
 	float *rec0 = part + (((size_t)(sq * KVH + kvh) * max_chunks + c) * kMaxG) * REC;
 	for (int t = tid; t < G * HD; t += 256) {
 		const int g = t / HD, d = t - g * HD;
-		rec0[(size_t)g * REC + d] = o_s[0][g][d] + o_s[1][g][d] + o_s[2][g][d] + o_s[3][g][d];
+		rec0[(size_t)g * REC + d] = o_s[(0 * kMaxG + g) * HD + d] + o_s[(1 * kMaxG + g) * HD + d] +
+		                            o_s[(2 * kMaxG + g) * HD + d] + o_s[(3 * kMaxG + g) * HD + d];
 	}
 	if (tid < G) {
 		rec0[(size_t)tid * REC + HD] = ml_s[tid][0];
@@ -1185,6 +1207,10 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 		                 "max_seq %d",
 		                 m->n_layers, m->d_model, m->n_heads, m->n_kv_heads, m->head_dim, m->ffn_dim, m->vocab,
 		                 max_seq);
+	// one sequence's layer cache is read through 32-bit buffer offsets
+	if ((size_t)max_seq * m->n_kv_heads * m->head_dim * 4 >= kBufNone)
+		return set_error(HAKO_GPU_EINVAL, "max_seq %d x kv_dim %d: a layer's cache of one sequence exceeds 2 GiB",
+		                 max_seq, m->n_kv_heads * m->head_dim);
 	if (!known_type(m->t_embd) || !known_type(m->t_out) || !m->tok_embd || !m->out_weight || !m->out_norm)
 		return set_error(HAKO_GPU_ETYPE, "embedding / output types %d / %d", m->t_embd, m->t_out);
 	for (int l = 0; l < m->n_layers; l++) {
