@@ -240,6 +240,17 @@ struct Q6SkBuf {
 	uint32_t d;
 };
 
+// Weight staging of one wave: its 16 rows' super-block, fetched as 16-byte
+// pieces (lane = piece p < 13 of row 4i + lane/16 in load i: bytes 0..207 of
+// each row as one contiguous run; blocks are 2-byte aligned, so the pieces
+// are unaligned loads) plus one 2-byte load of d per row (lane = row), written
+// to a per-wave LDS tile and read back in the MFMA lane layout. Every byte
+// read lies inside the block. A row of the tile is 240 bytes (60 dwords,
+// -4 mod 64 banks: the dword reads of 16 rows x 4 lanes fall in 64 distinct
+// banks).
+constexpr int kQ6Pieces = 13;                 // 16-byte pieces of bytes 0..207 (d at 208 apart)
+constexpr int kQ6TileRow = 240;               // bytes per staged row
+
 // Workgroup (64-row tile, K split): the tile's rows over super-blocks
 // [kb_beg, kb_end), the sums scaled by each token's power of two (esc) at
 // the end. EPI kSkStore / kSkAdd apply the epilogue directly (one split);
@@ -250,6 +261,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
     int M, int K, int vrows, int nsplit, float *__restrict__ part) {
 	__shared__ __align__(16) _Float16 ah_s[2][16 * kHPadSk];
 	__shared__ __align__(16) _Float16 al_s[2][16 * kHPadSk];
+	__shared__ __align__(16) uint8_t w_s[4][16 * kQ6TileRow];
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment and descriptors in SGPRs
 	const int j = lane & 15, kq = lane >> 4;
@@ -262,22 +274,52 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 	const bool ok = vrow < vrows && wr < S.rows;
 	const uint32_t rb = (uint32_t)NB * kQ6Bytes;
 	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, (uint32_t)S.rows * rb);   // the wave's segment
-	const uint32_t row_off = ok ? (uint32_t)wr * rb : kBufNone;
+	// staging loads: piece lp of row 4i + lr (i = 0..3), and d of row `lane`;
+	// rows outside the segment or the launch, pieces 13..15 and lanes 16..63
+	// of the d load read nothing
+	const int lp = lane & 15, lr = lane >> 4;
+	uint32_t srow_off[4];
+#pragma unroll
+	for (int i = 0; i < 4; i++) {
+		const int r = wrow0 + 4 * i + lr, rr = r - S.row0;
+		srow_off[i] = (lp < kQ6Pieces && r < vrows && rr < S.rows) ? (uint32_t)rr * rb + 16u * lp : kBufNone;
+	}
+	uint32_t d_off;
+	{
+		const int r = wrow0 + lane, rr = r - S.row0;
+		d_off = (lane < 16 && r < vrows && rr < S.rows) ? (uint32_t)rr * rb + 208u : kBufNone;
+	}
+	uint8_t *wt = w_s[wave];
 	const __amdgpu_buffer_rsrc_t hrs = stream_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
 	const __amdgpu_buffer_rsrc_t lrs = stream_rsrc(xl, (uint32_t)M * (uint32_t)K * 2u);
 	const int t0 = 4 * kq;
 
-	auto issue = [&](Q6SkBuf &b, int kb) {
-		const uint32_t o = kb < kb_end ? row_off + (uint32_t)kb * kQ6Bytes : kBufNone;
+	auto issue = [&](uint4 (&wv)[4], uint32_t &dv, int kb) {
+#pragma unroll
+		for (int i = 0; i < 4; i++)
+			wv[i] = ld_b128(wrs, kb < kb_end && srow_off[i] != kBufNone ? srow_off[i] + (uint32_t)kb * kQ6Bytes
+			                                                             : kBufNone);
+		dv = ld_b16(wrs, kb < kb_end && d_off != kBufNone ? d_off + (uint32_t)kb * kQ6Bytes : kBufNone);
+	};
+	// the staged pieces to the wave's tile, then this lane's fields of row j
+	auto unstage = [&](const uint4 (&wv)[4], uint32_t dv, Q6SkBuf &b) {
+		if (lp < kQ6Pieces) {
+#pragma unroll
+			for (int i = 0; i < 4; i++) *(uint4 *)(wt + (4 * i + lr) * kQ6TileRow + 16 * lp) = wv[i];
+		}
+		if (lane < 16) *(uint16_t *)(wt + lane * kQ6TileRow + 208) = (uint16_t)dv;
+		__builtin_amdgcn_wave_barrier();
+		const uint8_t *row = wt + j * kQ6TileRow;
 #pragma unroll
 		for (int n = 0; n < 2; n++) {
 #pragma unroll
-			for (int q = 0; q < 4; q++) b.ql[n][q] = ld_b32(wrs, o + 64 * n + 16 * q + 4 * kq);
+			for (int q = 0; q < 4; q++) b.ql[n][q] = *(const uint32_t *)(row + 64 * n + 16 * q + 4 * kq);
 #pragma unroll
-			for (int p = 0; p < 2; p++) b.qh[n][p] = ld_b32(wrs, o + 128 + 32 * n + 16 * p + 4 * kq);
+			for (int p = 0; p < 2; p++) b.qh[n][p] = *(const uint32_t *)(row + 128 + 32 * n + 16 * p + 4 * kq);
 		}
-		b.sc = ld_b128(wrs, o + 192);
-		b.d = ld_b16(wrs, o + 208);
+		b.sc = *(const uint4 *)(row + 192);
+		b.d = *(const uint16_t *)(row + 208);
+		__builtin_amdgcn_wave_barrier();   // read before the next block's pieces land
 	};
 	// activation stage of block kb: 16 tokens x 256 K of hi and lo (zeros past M)
 	uint4 hreg[2], lreg[2];
@@ -299,9 +341,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 		}
 	};
 
-	Q6SkBuf b0, b1;
-	issue(b0, kb_beg);
-	issue(b1, kb_beg + 1);
+	uint4 wv0[4], wv1[4];
+	uint32_t dv0, dv1;
+	issue(wv0, dv0, kb_beg);
+	issue(wv1, dv1, kb_beg + 1);
 	load_stage(kb_beg);
 	store_stage(0);
 	__syncthreads();
@@ -314,7 +357,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 			if (kb < kb_end) {
 				const bool more = kb + 1 < kb_end;
 				if (more) load_stage(kb + 1);
-				Q6SkBuf &b = half ? b1 : b0;
+				Q6SkBuf b;
+				unstage(half ? wv1 : wv0, half ? dv1 : dv0, b);
+				issue(half ? wv1 : wv0, half ? dv1 : dv0, kb + 2);
 				const _Float16 *ah = ah_s[half] + j * kHPadSk + 4 * kq;
 				const _Float16 *al = al_s[half] + j * kHPadSk + 4 * kq;
 				const float dd = f16_to_f32(b.d);
@@ -339,7 +384,6 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 					acc[2] = __builtin_fmaf(pr[2], s, acc[2]);
 					acc[3] = __builtin_fmaf(pr[3], s, acc[3]);
 				}
-				issue(b, kb + 2);
 				if (more) {
 					store_stage(half ^ 1);
 					__syncthreads();
