@@ -10,15 +10,18 @@
 // is nibble (k>>1) of ql[64n + 32(k&1) + l] with bits 2k..2k+1 of qh[32n + l]
 // on top, minus 32, times d*scales[8n + 2k + l/16].
 //
-// Lane work. Chunk c = 8i + s of a row is block i, half n = s/4, l in
-// [l0, l0+8) with l0 = 8*(s%4): 8-byte loads of ql at 64n+l0 and 64n+32+l0
-// and of qh at 32n+l0 give 32 weights (k = 0..3, 8 each), each k inside one
-// 16-wide scale group. Blocks are only 2-byte aligned in the verbatim stream
-// (210 = 2*105), so those loads are unaligned; gfx950 serves them in the HSA
-// unaligned-access mode the compiler itself assumes for byte copies. The
-// 6-bit values are assembled four to a dword (nibbles | qh bits moved to bits
-// 4-5 of each byte), converted per byte (v_cvt_f32_ubyteN) and multiplied into
-// the lane's fp32 activations; per scale group the sum is Σq·x − 32·Σx with
+// Lane work. Chunk c = 8i + s of a row is block i, half n = s/4, k pair
+// kp = (s/2)%2 and l half lh = s%2: the 32 weights k in {kp, kp+2}, l in
+// [16lh, 16lh+16) of half n, two 16-wide scale groups. They come from one
+// 16-byte load of ql at 64n+32kp+16lh (low nibbles k = kp, high k = kp+2),
+// one of qh at 32n+16lh (bits 2k..2k+1), 8 bytes of scales and d: the eight
+// lanes of a block read its ql as one 128-byte run and its qh as 32-byte
+// runs. Blocks are only 2-byte aligned in the verbatim stream (210 = 2*105),
+// so the loads are unaligned; gfx950 serves them in the HSA unaligned-access
+// mode the compiler itself assumes for byte copies. The 6-bit values are
+// assembled four to a dword (nibbles | qh bits moved to bits 4-5 of each
+// byte), converted per byte (v_cvt_f32_ubyteN) and multiplied into the
+// lane's fp32 activations; per scale group the sum is Σq·x − 32·Σx with
 // −32·Σx precomputed.
 //
 // Grid. Persistent: about one workgroup per CU, each owning a contiguous row
@@ -38,68 +41,65 @@ constexpr int kQ6Depth = 4;
 constexpr int kQ6MaxWaves = 16;
 
 struct Q6Buf {
-	uint2 a, b, h, s;
+	uint4 ql, qh;
+	uint2 s;         // scales 8n .. 8n+8
 	uint32_t d;
 };
 
-// The lane's activation columns for one chunk: xv[k][j] = x at weight
-// 128n + 32k + l0 + j of block i, and -32·Σ_j xv[k][j].
+// The lane's activation columns for one chunk: xv[kk][j] = x at weight
+// 128n + 32(kp + 2kk) + 16lh + j of block i, and -32·Σ_j xv[kk][j].
 struct Q6Col {
-	float xv[4][8];
-	float nsx[4];
+	float xv[2][16];
+	float nsx[2];
 };
 
 __device__ __forceinline__ void q6_col_load(const float *__restrict__ x, int c, Q6Col &col) {
-	const int i = c >> 3, s = c & 7, n = s >> 2, l0 = 8 * (s & 3);
-	const float *xb = x + kQK * i + 128 * n + l0;
+	const int i = c >> 3, s = c & 7, n = s >> 2, kp = (s >> 1) & 1, lh = s & 1;
+	const float *xb = x + kQK * i + 128 * n + 32 * kp + 16 * lh;
 #pragma unroll
-	for (int k = 0; k < 4; k++) {
-		const float4 u = *(const float4 *)(xb + 32 * k);
-		const float4 v = *(const float4 *)(xb + 32 * k + 4);
-		col.xv[k][0] = u.x; col.xv[k][1] = u.y; col.xv[k][2] = u.z; col.xv[k][3] = u.w;
-		col.xv[k][4] = v.x; col.xv[k][5] = v.y; col.xv[k][6] = v.z; col.xv[k][7] = v.w;
+	for (int kk = 0; kk < 2; kk++) {
+#pragma unroll
+		for (int m = 0; m < 4; m++) {
+			const float4 u = *(const float4 *)(xb + 64 * kk + 4 * m);
+			col.xv[kk][4 * m] = u.x; col.xv[kk][4 * m + 1] = u.y;
+			col.xv[kk][4 * m + 2] = u.z; col.xv[kk][4 * m + 3] = u.w;
+		}
 	}
 }
 
 __device__ __forceinline__ void q6_col_sums(Q6Col &col) {
 #pragma unroll
-	for (int k = 0; k < 4; k++) {
+	for (int kk = 0; kk < 2; kk++) {
 		float t = 0.0f;
 #pragma unroll
-		for (int j = 0; j < 8; j++) t += col.xv[k][j];
-		col.nsx[k] = -32.0f * t;
+		for (int j = 0; j < 16; j++) t += col.xv[kk][j];
+		col.nsx[kk] = -32.0f * t;
 	}
 }
 
 __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 
-// d · Σ_k sc_k · (Σ_j q_kj·x_kj − 32·Σ_j x_kj) over the lane's 32 weights.
-__device__ __forceinline__ float q6_dot(const Q6Buf &W, const Q6Col &col, int sel) {
-	float acc0 = col.nsx[0], acc1 = col.nsx[1], acc2 = col.nsx[2], acc3 = col.nsx[3];
-	const uint32_t lo = 0x0F0F0F0Fu, hi = 0x30303030u;
+// d · Σ_kk sc_kk · (Σ_j q_kk,j·x_kk,j − 32·Σ_j x_kk,j) over the lane's 32
+// weights (k = kp + 2kk; qh bits 2k..2k+1 taken at shift 2kp, 2kp+4).
+__device__ __forceinline__ float q6_dot(const Q6Buf &W, const Q6Col &col, int kp, int sel) {
+	float acc0 = col.nsx[0], acc1 = col.nsx[1];
+	const uint32_t lo = 0x0F0F0F0Fu, m2 = 0x03030303u;
+	const uint32_t ql[4] = {W.ql.x, W.ql.y, W.ql.z, W.ql.w}, qh[4] = {W.qh.x, W.qh.y, W.qh.z, W.qh.w};
+	const int sh = 2 * kp;
 #pragma unroll
-	for (int u = 0; u < 2; u++) {
-		const uint32_t l0 = u ? W.a.y : W.a.x, l1 = u ? W.b.y : W.b.x, hh = u ? W.h.y : W.h.x;
-		const uint32_t w0 = (l0 & lo) | ((hh << 4) & hi);
-		const uint32_t w1 = (l1 & lo) | ((hh << 2) & hi);
-		const uint32_t w2 = ((l0 >> 4) & lo) | (hh & hi);
-		const uint32_t w3 = ((l1 >> 4) & lo) | ((hh >> 2) & hi);
+	for (int u = 0; u < 4; u++) {
+		const uint32_t w0 = (ql[u] & lo) | (((qh[u] >> sh) & m2) << 4);
+		const uint32_t w1 = ((ql[u] >> 4) & lo) | (((qh[u] >> (sh + 4)) & m2) << 4);
 #pragma unroll
 		for (int b = 0; b < 4; b++) {
 			acc0 = __builtin_fmaf(byte_f(w0, b), col.xv[0][4 * u + b], acc0);
 			acc1 = __builtin_fmaf(byte_f(w1, b), col.xv[1][4 * u + b], acc1);
-			acc2 = __builtin_fmaf(byte_f(w2, b), col.xv[2][4 * u + b], acc2);
-			acc3 = __builtin_fmaf(byte_f(w3, b), col.xv[3][4 * u + b], acc3);
 		}
 	}
-	// scales[8n + sel + 2k]: k = 0,1 in the first dword, k = 2,3 in the second.
-	const int sh0 = 8 * sel, sh1 = 8 * (sel + 2);
-	const float s0 = (float)(int8_t)((W.s.x >> sh0) & 0xFFu);
-	const float s1 = (float)(int8_t)((W.s.x >> sh1) & 0xFFu);
-	const float s2 = (float)(int8_t)((W.s.y >> sh0) & 0xFFu);
-	const float s3 = (float)(int8_t)((W.s.y >> sh1) & 0xFFu);
-	const float part = s0 * acc0 + s1 * acc1 + s2 * acc2 + s3 * acc3;
-	return f16_to_f32(W.d) * part;
+	// scales[8n + 2k + lh]: byte sel = 2kp + lh of each dword (k = kp, kp+2)
+	const float s0 = (float)(int8_t)((W.s.x >> (8 * sel)) & 0xFFu);
+	const float s1 = (float)(int8_t)((W.s.y >> (8 * sel)) & 0xFFu);
+	return f16_to_f32(W.d) * (s0 * acc0 + s1 * acc1);
 }
 
 struct Q6Geom {
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 	auto item_row = [&](int it) -> int { return r0 + G.rt * (slice + G.rw * it) + rsub; };
 
 	const int cc = min(c, G.C - 1);           // in-bounds chunk for idle lanes' loads
-	const int i = cc >> 3, s = cc & 7, hn = s >> 2, l0 = 8 * (s & 3), sel = (s & 3) >> 1;
+	const int i = cc >> 3, s = cc & 7, hn = s >> 2, kp = (s >> 1) & 1, lh = s & 1, sel = 2 * kp + lh;
 	const size_t in_row = (size_t)i * kQ6Bytes;
 	// Weight loads are raw buffer loads, never predicated: slots with no work
 	// use an offset past the stream (zeros, no memory traffic). A branch
@@ -158,9 +158,8 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 		const int row = item_row(it);
 		const bool on = it < nit && row < r1 && lane_on;
 		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + in_row) : kBufNone;
-		b.a = ld_b64(wr, blk + 64 * hn + l0);
-		b.b = ld_b64(wr, blk + 64 * hn + 32 + l0);
-		b.h = ld_b64(wr, blk + 128 + 32 * hn + l0);
+		b.ql = ld_b128(wr, blk + 64 * hn + 32 * kp + 16 * lh);
+		b.qh = ld_b128(wr, blk + 128 + 32 * hn + 16 * lh);
 		b.s = ld_b64(wr, blk + 192 + 8 * hn);
 		b.d = ld_b16(wr, blk + 208);
 	};
@@ -198,7 +197,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 			const int row = item_row(it);
 			float d = 0.0f;
 			// Consume buf[j] in place, then reload it (no register rotation).
-			if (it < nit) d = q6_dot(buf[j], col, sel);
+			if (it < nit) d = q6_dot(buf[j], col, kp, sel);
 			issue(buf[j], it + kQ6Depth);
 			__builtin_amdgcn_sched_barrier(0);
 			rsum[j] = (lane_on && row < r1) ? d : 0.0f;
