@@ -460,12 +460,38 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	const float *q = qkv + (size_t)sq * qkv_stride;
 	float *kcs = kc + (size_t)sq * kv_seq_stride + kvh * HD;
 	float *vcs = vc + (size_t)sq * kv_seq_stride + kvh * HD;
-	// 1. every key and value load of the chunk (rows past pos read row pos:
-	//    in bounds, discarded): raw buffer loads over this sequence's layer
-	//    cache. Keys: load j of the position's four threads reads float4s
-	//    kq + 4j, so the four cover 64 contiguous bytes and two consecutive
-	//    loads whole cache lines. Values: one lane offset plus a wave-uniform
-	//    row offset.
+	// 1. the query rows, their rope factors and (chunk holding pos) the new
+	//    key and value first: the rotation below waits for these only
+	const float2 *rp = rope + (size_t)pos * HALF;
+	constexpr int QI = (kMaxG * HALF + 255) / 256;   // rotation items per thread
+	float qa[QI], qb[QI];
+	float2 qcs[QI];
+#pragma unroll
+	for (int r = 0; r < QI; r++) {
+		const int t = min(tid + 256 * r, G * HALF - 1);
+		const int g = t / HALF, i = t - g * HALF;
+		qcs[r] = rp[i];
+		qa[r] = q[(kvh * G + g) * HD + i];
+		qb[r] = q[(kvh * G + g) * HD + i + HALF];
+	}
+	float na = 0.0f, nb = 0.0f, nv = 0.0f;
+	float2 ncs = {0.0f, 0.0f};
+	if (has_pos) {
+		if (tid < HALF) {
+			ncs = rp[tid];
+			na = q[D + kvh * HD + tid];
+			nb = q[D + kvh * HD + tid + HALF];
+		}
+		if (tid < HD) nv = q[D + KV + kvh * HD + tid];
+	}
+	__builtin_amdgcn_sched_barrier(0);
+
+	// 2. every key, then every value load of the chunk (rows past pos read
+	//    row pos: in bounds, discarded): raw buffer loads over this
+	//    sequence's layer cache. Keys: load j of the position's four threads
+	//    reads float4s kq + 4j, so the four cover 64 contiguous bytes and two
+	//    consecutive loads whole cache lines. Values: one lane offset plus a
+	//    wave-uniform row offset. The scores wait for the keys only.
 	const uint32_t cache_bytes = (uint32_t)((size_t)max_seq * KV * 4);
 	const __amdgpu_buffer_rsrc_t krs = stream_rsrc(kc + (size_t)sq * kv_seq_stride, cache_bytes);
 	const __amdgpu_buffer_rsrc_t vrs = stream_rsrc(vc + (size_t)sq * kv_seq_stride, cache_bytes);
@@ -475,6 +501,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	float4 kr[KQ];
 #pragma unroll
 	for (int j = 0; j < KQ; j++) kr[j] = __builtin_bit_cast(float4, ld_b128(krs, koff + 64u * j));
+	__builtin_amdgcn_sched_barrier(0);
 	const int vd = DV * lane, vg = wave;
 	const uint32_t voff = (uint32_t)(kvh * HD + vd) * 4u;
 	float vr[PG][DV];
@@ -490,39 +517,40 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 			vr[j][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vrs, (int)voff, soff, 0));
 		}
 	}
+	__builtin_amdgcn_sched_barrier(0);
+
+	// 3. rotated query heads (and the new key, value) into LDS; the new key
+	//    and value appended to the caches
+#pragma unroll
+	for (int r = 0; r < QI; r++) {
+		const int t = tid + 256 * r;
+		if (t < G * HALF) {
+			const int g = t / HALF, i = t - g * HALF;
+			q_s[g * QR + i] = qa[r] * qcs[r].x - qb[r] * qcs[r].y;
+			q_s[g * QR + i + HALF] = qa[r] * qcs[r].y + qb[r] * qcs[r].x;
+		}
+	}
+	if (has_pos) {
+		if (tid < HALF) {
+			const float k0 = na * ncs.x - nb * ncs.y, k1 = na * ncs.y + nb * ncs.x;
+			kn_s[tid] = k0;
+			kn_s[tid + HALF] = k1;
+			kcs[(size_t)pos * KV + tid] = k0;
+			kcs[(size_t)pos * KV + tid + HALF] = k1;
+		}
+		if (tid < HD) {
+			vn_s[tid] = nv;
+			vcs[(size_t)pos * KV + tid] = nv;
+		}
+	}
+	__syncthreads();
+
 	// rows past pos carry weight 0; zero them too, so no stale value reaches a sum
 #pragma unroll
 	for (int j = 0; j < PG; j++)
 		if (c * kChunk + PG * vg + j > pos)
 #pragma unroll
 			for (int u = 0; u < DV; u++) vr[j][u] = 0.0f;
-
-	// 2. rotated query heads (and the new key, value) into LDS
-	const float2 *rp = rope + (size_t)pos * HALF;
-	for (int t = tid; t < G * HALF; t += 256) {
-		const int g = t / HALF, i = t - g * HALF;
-		const float2 cs = rp[i];
-		const float a = q[(kvh * G + g) * HD + i], b = q[(kvh * G + g) * HD + i + HALF];
-		q_s[g * QR + i] = a * cs.x - b * cs.y;
-		q_s[g * QR + i + HALF] = a * cs.y + b * cs.x;
-	}
-	if (has_pos) {
-		for (int i = tid; i < HALF; i += 256) {
-			const float2 cs = rp[i];
-			const float a = q[D + kvh * HD + i], b = q[D + kvh * HD + i + HALF];
-			const float k0 = a * cs.x - b * cs.y, k1 = a * cs.y + b * cs.x;
-			kn_s[i] = k0;
-			kn_s[i + HALF] = k1;
-			kcs[(size_t)pos * KV + i] = k0;
-			kcs[(size_t)pos * KV + i + HALF] = k1;
-		}
-		for (int i = tid; i < HD; i += 256) {
-			const float v = q[D + KV + kvh * HD + i];
-			vn_s[i] = v;
-			vcs[(size_t)pos * KV + i] = v;
-		}
-	}
-	__syncthreads();
 
 	// 3. scores: 4 threads per position, every fourth float4 of the dims each
 	if (APPEND && ks == pos) {
