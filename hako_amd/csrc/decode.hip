@@ -415,8 +415,10 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 
 // ── attention (reference src/model.c:105-137) ──
 
-// Workgroup (chunk c, KV head kvh, sequence sq) of 256 threads: positions
-// [64c, 64c+64) up to pos. Every key and value load of the chunk is issued
+// Workgroup (chunk c x head part hg, KV head kvh, sequence sq) of 256
+// threads: positions [64c, 64c+64) up to pos, for the group's query heads
+// of part hg (hsplit parts: a small grid splits a group's heads over two
+// workgroups, which read the same keys and values). Every key and value load of the chunk is issued
 // first (thread = position x every fourth float4 of the head dims for keys,
 // value dims x 16-position group for values), so the chunk costs one memory
 // latency. The
@@ -432,7 +434,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
                                                    float *kc, float *vc, const int *__restrict__ posv,
                                                    float *part, int H, int KVH,
                                                    int max_seq, int max_chunks, size_t kv_seq_stride,
-                                                   int qkv_stride, float scale) {
+                                                   int qkv_stride, float scale, int hsplit) {
 	constexpr int HALF = HD / 2;
 	constexpr int REC = HD + 2;      // partial record: o[HD], m, l
 	constexpr int KQ = HD / 16;      // float4 of a key row per thread (4 threads per position)
@@ -448,15 +450,19 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	float *o_s = u_s;                // [4][kMaxG][HD]: value sums per position group
 	__shared__ float ml_s[kMaxG][2];
 	__shared__ float kn_s[HD], vn_s[HD];
-	const int c = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z;
+	const int c = blockIdx.x / hsplit, hg = blockIdx.x - c * hsplit, kvh = blockIdx.y, sq = blockIdx.z;
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: value rows in SGPRs
-	const int G = H / KVH, KV = KVH * HD, D = H * HD;
+	const int GA = H / KVH, KV = KVH * HD, D = H * HD;
+	// this workgroup's query heads of the group: g0 + [0, G)
+	const int GH = (GA + hsplit - 1) / hsplit, g0 = hg * GH, G = min(GH, GA - g0);
+	if (G <= 0) return;
 	const int pos = posv[sq];
 	if (pos < 0 || pos >= max_seq) return;   // no room left: the host refuses such steps
 	const int nact = pos / kChunk + 1;
 	if (c >= nact) return;
 	const bool has_pos = APPEND && c == nact - 1;
+	const bool writer = has_pos && hg == 0;   // appends the new key and value
 	const float *q = qkv + (size_t)sq * qkv_stride;
 	float *kcs = kc + (size_t)sq * kv_seq_stride + kvh * HD;
 	float *vcs = vc + (size_t)sq * kv_seq_stride + kvh * HD;
@@ -471,8 +477,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 		const int t = min(tid + 256 * r, G * HALF - 1);
 		const int g = t / HALF, i = t - g * HALF;
 		qcs[r] = rp[i];
-		qa[r] = q[(kvh * G + g) * HD + i];
-		qb[r] = q[(kvh * G + g) * HD + i + HALF];
+		qa[r] = q[(kvh * GA + g0 + g) * HD + i];
+		qb[r] = q[(kvh * GA + g0 + g) * HD + i + HALF];
 	}
 	float na = 0.0f, nb = 0.0f, nv = 0.0f;
 	float2 ncs = {0.0f, 0.0f};
@@ -535,12 +541,14 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 			const float k0 = na * ncs.x - nb * ncs.y, k1 = na * ncs.y + nb * ncs.x;
 			kn_s[tid] = k0;
 			kn_s[tid + HALF] = k1;
-			kcs[(size_t)pos * KV + tid] = k0;
-			kcs[(size_t)pos * KV + tid + HALF] = k1;
+			if (writer) {
+				kcs[(size_t)pos * KV + tid] = k0;
+				kcs[(size_t)pos * KV + tid + HALF] = k1;
+			}
 		}
 		if (tid < HD) {
 			vn_s[tid] = nv;
-			vcs[(size_t)pos * KV + tid] = nv;
+			if (writer) vcs[(size_t)pos * KV + tid] = nv;
 		}
 	}
 	__syncthreads();
@@ -628,7 +636,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 #pragma unroll
 			for (int u = 0; u < DV; u++) o_s[(vg * kMaxG + g) * HD + vd + u] = o[g][u];
 	__syncthreads();
-	float *rec0 = part + (((size_t)(sq * KVH + kvh) * max_chunks + c) * kMaxG) * REC;
+	float *rec0 = part + (((size_t)(sq * KVH + kvh) * max_chunks + c) * kMaxG + g0) * REC;
 	for (int t = tid; t < G * HD; t += 256) {
 		const int g = t / HD, d = t - g * HD;
 		rec0[(size_t)g * REC + d] = o_s[(0 * kMaxG + g) * HD + d] + o_s[(1 * kMaxG + g) * HD + d] +
@@ -900,16 +908,21 @@ int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nu
 	const float scale = 1.0f / sqrtf((float)HD);
 	const size_t kv_seq_stride = (size_t)m.n_layers * d->max_seq * KV;
 	float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
-	const dim3 ag(d->max_chunks, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
+	// one sequence: a grid of chunks x KV heads leaves most CUs idle, so each
+	// group's query heads are split over two workgroups
+	const int hsplit = d->n_seq == 1 && G >= 2 ? 2 : 1;
+	const dim3 ag(d->max_chunks * hsplit, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
 	if (HD == 128) {
 		hipLaunchKernelGGL((attn_kernel<128, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
-		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
+		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale,
+		                   hsplit);
 		HK_LAUNCHED("attention");
 		hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->part, d->pos, d->att, mxq, mxs,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks);
 	} else {
 		hipLaunchKernelGGL((attn_kernel<64, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
-		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale);
+		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale,
+		                   hsplit);
 		HK_LAUNCHED("attention");
 		hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->part, d->pos, d->att, mxq, mxs,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks);
@@ -1188,14 +1201,16 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 		const dim3 ag(d->max_chunks, KVH, n), mg(G, KVH, n);
 		if (HD == 128) {
 			hipLaunchKernelGGL((attn_kernel<128, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
-			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale);
+			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale,
+			                   1);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
 			                   nullptr, nullptr,
 			                   m.n_heads, KVH, d->max_seq, d->max_chunks);
 		} else {
 			hipLaunchKernelGGL((attn_kernel<64, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
-			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale);
+			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale,
+			                   1);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
 			                   nullptr, nullptr,
