@@ -417,7 +417,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 
 // Workgroup (chunk c x head part hg, KV head kvh, sequence sq) of 256
 // threads: positions [64c, 64c+64) up to pos, for the group's query heads
-// of part hg (hsplit parts: a small grid splits a group's heads over two
+// of part hg (hsplit parts: a small grid splits a group's heads over several
 // workgroups, which read the same keys and values). Every key and value load of the chunk is issued
 // first (thread = position x every fourth float4 of the head dims for keys,
 // value dims x 16-position group for values), so the chunk costs one memory
@@ -909,8 +909,9 @@ int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nu
 	const size_t kv_seq_stride = (size_t)m.n_layers * d->max_seq * KV;
 	float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
 	// one sequence: a grid of chunks x KV heads leaves most CUs idle, so each
-	// group's query heads are split over two workgroups
-	const int hsplit = d->n_seq == 1 && G >= 2 ? 2 : 1;
+	// group's query heads are split over (up to) four workgroups (3B decode at
+	// position 1024: 1374 / 1322 / 1304 / 1362 us per token for 1 / 2 / 4 / 8)
+	const int hsplit = d->n_seq == 1 ? (G < 4 ? G : 4) : 1;
 	const dim3 ag(d->max_chunks * hsplit, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
 	if (HD == 128) {
 		hipLaunchKernelGGL((attn_kernel<128, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
