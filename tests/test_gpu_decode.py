@@ -22,6 +22,13 @@ TINY_UNTIED = mlf2.Qwen2Config(n_layers=2, d_model=512, n_heads=8, n_kv_heads=2,
                                vocab=768, ctx=256, tied=False, embd_type=synth.TYPE_Q4_K)
 SMALL_128 = mlf2.Qwen2Config(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=2816,
                              vocab=4096, ctx=512)
+# 7 query heads per KV head (the 7B grouping): one sequence's attention
+# splits a group's heads 2 + 2 + 2 + 1 over four workgroups
+GQA7 = mlf2.Qwen2Config(n_layers=2, d_model=1792, n_heads=14, n_kv_heads=2, head_dim=128, ffn_dim=1536,
+                        vocab=2000, ctx=256)
+# one KV head per query head pair with head_dim 64 (two head parts of one head)
+GQA2 = mlf2.Qwen2Config(n_layers=2, d_model=512, n_heads=8, n_kv_heads=4, head_dim=64, ffn_dim=768,
+                        vocab=1024, ctx=256)
 
 
 @pytest.fixture(scope="module")
@@ -36,7 +43,7 @@ def make_decoder(gpu, path, max_seq):
     return Decoder(gpu, path, n_seq=1, max_seq=max_seq)
 
 
-@pytest.mark.parametrize("cfg,seed", [(TINY, 1), (TINY_UNTIED, 2), (SMALL_128, 3)])
+@pytest.mark.parametrize("cfg,seed", [(TINY, 1), (TINY_UNTIED, 2), (SMALL_128, 3), (GQA7, 4), (GQA2, 5)])
 def test_greedy_tokens_match_reference(gpu, ref, tmp_path, cfg, seed):
     from dropin import greedy
     path = str(tmp_path / "m.mlf2")
@@ -60,7 +67,7 @@ def test_greedy_tokens_match_reference(gpu, ref, tmp_path, cfg, seed):
     assert maxabs_rel(np.stack(logits), want_logits) < 2e-2
 
 
-@pytest.mark.parametrize("cfg,seed,pos", [(TINY, 4, 100), (SMALL_128, 5, 300)])
+@pytest.mark.parametrize("cfg,seed,pos", [(TINY, 4, 100), (SMALL_128, 5, 300), (GQA7, 6, 250)])
 def test_prefilled_cache_matches_reference(gpu, ref, tmp_path, cfg, seed, pos):
     """KV cache filled with seeded N(0,1) keys and values at 0..pos-1, as the
     decode benchmarks start: the attention spans several 64-position chunks."""
