@@ -450,7 +450,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	float *o_s = u_s;                // [4][kMaxG][HD]: value sums per position group
 	__shared__ float ml_s[kMaxG][2];
 	__shared__ float kn_s[HD], vn_s[HD];
-	const int c = blockIdx.x / hsplit, hg = blockIdx.x - c * hsplit, kvh = blockIdx.y, sq = blockIdx.z;
+	// block b -> chunk c, head part hg with b % 8 = c % 8: a chunk's parts run
+	// on one XCD (workgroups go to the XCDs round robin) and share its L2
+	const int hb = blockIdx.x >> 3;
+	const int c = (hb / hsplit) * 8 + (blockIdx.x & 7), hg = hb % hsplit, kvh = blockIdx.y, sq = blockIdx.z;
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: value rows in SGPRs
 	const int GA = H / KVH, KV = KVH * HD, D = H * HD;
@@ -911,8 +914,9 @@ int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nu
 	// one sequence: a grid of chunks x KV heads leaves most CUs idle, so each
 	// group's query heads are split over (up to) four workgroups (3B decode at
 	// position 1024: 1374 / 1322 / 1304 / 1362 us per token for 1 / 2 / 4 / 8)
+	// (16 sequences: two parts per group made the 7B step 4% slower)
 	const int hsplit = d->n_seq == 1 ? (G < 4 ? G : 4) : 1;
-	const dim3 ag(d->max_chunks * hsplit, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
+	const dim3 ag((d->max_chunks + 7) / 8 * 8 * hsplit, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
 	if (HD == 128) {
 		hipLaunchKernelGGL((attn_kernel<128, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale,
