@@ -43,16 +43,6 @@ constexpr int kMaxG = 8;     // query heads per KV head
 constexpr int kArgBlocks = 64;
 constexpr int kDecItems = 2; // row items per wave of the fused GEMV
 
-__device__ __forceinline__ float wave_max(float v) {
-	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap1>(v));
-	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap2>(v));
-	v = __builtin_fmaxf(v, dpp_f<kDppHalfMirror>(v));
-	v = __builtin_fmaxf(v, dpp_f<kDppMirror>(v));
-	v = __builtin_fmaxf(v, __shfl_xor(v, 16));
-	v = __builtin_fmaxf(v, __shfl_xor(v, 32));
-	return v;
-}
-
 // silu (reference src/nn.c:29)
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
@@ -842,7 +832,7 @@ struct hako_gpu_decoder {
 	int *tok = nullptr, *pos = nullptr, *ring = nullptr, *nout = nullptr;
 	// batched steps (n_seq > 1): q8 and fp16 hi/lo activations, split-K state
 	int8_t *xq = nullptr;
-	float *xs = nullptr, *esc = nullptr, *skpart = nullptr;
+	float *xs = nullptr, *esc = nullptr, *escb = nullptr, *skpart = nullptr;
 	size_t skpart_floats = 0;   // capacity of skpart
 	_Float16 *xh = nullptr, *xl = nullptr;
 	// prompt prefill (allocated on first use): chunk activations and records
@@ -980,7 +970,7 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 	hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
 	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
 	HK_LAUNCHED("embed");
-	const int ns_o = q4k_skinny_splits(D, D), ns_down = q6k_skinny_splits(F, D);
+	const int ns_o = q4k_skinny_splits(D, D), ns_gu = q4k_skinny_splits(D, 2 * F), ns_down = q6k_skinny_splits(F, D);
 	const float *pend = nullptr;   // the previous down matmul's partials
 	int pend_ns = 0;
 	for (int l = 0; l < m.n_layers; l++) {
@@ -1000,20 +990,22 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D, D};
 		if (int rc = q4k_skinny(s, kSkPart, d->xq, d->xs, M, D, D, d->skpart, d->skpart_floats)) return rc;
-		// 4. residual, rmsnorm, q8; gate, up, SwiGLU
+		// 4. residual, rmsnorm, q8; gate and up partials
 		if (int rc = resid_rmsnorm_q8(d, d->skpart, ns_o, B.ffn_norm, D)) return rc;
 		s = SkSegs{};
 		s.n = 2;
 		s.s[0] = {(const uint8_t *)B.gate, nullptr, d->h, 0, F, F};
 		s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, F, F, F};
-		if (int rc = q4k_skinny(s, kSkSwiGLU, d->xq, d->xs, M, D, 2 * F, d->skpart, d->skpart_floats)) return rc;
-		// 5. the down matmul's fp16 hi/lo rows
-		if (int rc = f16_split(d->h, d->xh, d->xl, d->esc, M, F)) return rc;
+		if (int rc = q4k_skinny(s, kSkPart, d->xq, d->xs, M, D, 2 * F, d->skpart, d->skpart_floats)) return rc;
+		// 5. SwiGLU of the gate/up partials, straight to the down matmul's fp16
+		//    hi/lo rows with a power of two per 256-row block
+		if (int rc = swiglu_split(d->skpart, ns_gu, F, M, d->xh, d->xl, d->escb)) return rc;
 		// 6. down projection: partials, added to the residual by the next kernel
 		s = SkSegs{};
 		s.n = 1;
 		s.s[0] = {(const uint8_t *)B.down, nullptr, d->x, 0, D, D};
-		if (int rc = q6k_skinny(s, kSkPart, d->xh, d->xl, d->esc, M, F, D, d->skpart, d->skpart_floats)) return rc;
+		if (int rc = q6k_skinny(s, kSkPart, d->xh, d->xl, d->escb, M, F, D, d->skpart, d->skpart_floats, true))
+			return rc;
 		pend = d->skpart;
 		pend_ns = ns_down;
 	}
@@ -1313,7 +1305,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	size_t skpart = 0;
 	const int qkv_rows = D + 2 * d->kv_dim;
 	const size_t needs[6] = {q4k_skinny_part_floats(D, qkv_rows, kSkStore), q4k_skinny_part_floats(D, D, kSkPart),
-	                         q4k_skinny_part_floats(D, 2 * F, kSkSwiGLU), q6k_skinny_part_floats(F, D, kSkPart),
+	                         q4k_skinny_part_floats(D, 2 * F, kSkPart), q6k_skinny_part_floats(F, D, kSkPart),
 	                         m->t_out == HAKO_TYPE_Q4_K ? q4k_skinny_part_floats(D, m->vocab, kSkStore) : 0,
 	                         m->t_out == HAKO_TYPE_Q6_K ? q6k_skinny_part_floats(D, m->vocab, kSkStore) : 0};
 	for (size_t nf : needs) skpart = nf > skpart ? nf : skpart;
@@ -1323,6 +1315,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 		HK_ALLOC(d->xh, sizeof(_Float16) * n_seq * DF);
 		HK_ALLOC(d->xl, sizeof(_Float16) * n_seq * DF);
 		HK_ALLOC(d->esc, sizeof(float) * n_seq);
+		HK_ALLOC(d->escb, sizeof(float) * n_seq * (F / kQK));
 		HK_ALLOC(d->skpart, sizeof(float) * (skpart ? skpart : 1));
 		d->skpart_floats = skpart;
 	}

@@ -55,6 +55,17 @@ __device__ __forceinline__ float wave_sum(float v) {
 	return v;
 }
 
+// Maximum over all 64 lanes; every lane receives it.
+__device__ __forceinline__ float wave_max(float v) {
+	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap1>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppQuadSwap2>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppHalfMirror>(v));
+	v = __builtin_fmaxf(v, dpp_f<kDppMirror>(v));
+	v = __builtin_fmaxf(v, __shfl_xor(v, 16));
+	v = __builtin_fmaxf(v, __shfl_xor(v, 32));
+	return v;
+}
+
 // Sum over aligned segments of `seg` lanes (a power of two, 4..64); every
 // lane of a segment receives the segment's sum.
 __device__ __forceinline__ float seg_sum(float v, int seg) {

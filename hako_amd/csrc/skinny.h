@@ -47,11 +47,16 @@ size_t q4k_skinny_part_floats(int n_in, int vrows, int epi);
 int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
                float *part, size_t part_cap);
 // Q6_K x fp32 as fp16 hi/lo rows [m][n_in] with a power of two per token,
-// esc[m] (x = (hi + lo) * esc); Store, Add or Part.
+// esc[m] (x = (hi + lo) * esc), or per token and 256-wide block,
+// esc[m][n_in/256] (esc_per_block); Store, Add or Part.
 int q6k_skinny_splits(int n_in, int vrows);
 size_t q6k_skinny_part_floats(int n_in, int vrows, int epi);
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
-               int n_in, int vrows, float *part, size_t part_cap);
+               int n_in, int vrows, float *part, size_t part_cap, bool esc_per_block = false);
+// The gate/up partials of a Part launch over rows [0, 2F) (gate rows r, up
+// rows F + r, nsplit splits) to h = silu(gate)*up as fp16 hi/lo rows [m][F]
+// with a power of two per token and 256-row block, escb[m][F/256].
+int swiglu_split(const float *part, int nsplit, int F, int m, _Float16 *xh, _Float16 *xl, float *escb);
 // The fp16 hi/lo split of m fp32 rows of n floats with one power of two per
 // row, esc[m] (gemm.hip).
 int f16_split(const float *x, _Float16 *xh, _Float16 *xl, float *esc, int m, int n);

@@ -257,16 +257,18 @@ constexpr int kQ6Pieces = 13;                 // 16-byte pieces of bytes 0..207 
 constexpr int kQ6TileRow = 240;               // bytes per staged row
 
 // Workgroup (64-row tile, K split): the tile's rows over super-blocks
-// [kb_beg, kb_end), the sums scaled by each token's power of two (esc) at
-// the end. EPI kSkStore / kSkAdd apply the epilogue directly (one split);
-// kSkPart writes the partial sums to part[split][t][vrow].
-template <int EPI>
+// [kb_beg, kb_end), the sums scaled by each token's power of two: esc[t] at
+// the end, or (BLK) esc[t][kb] per super-block. EPI kSkStore / kSkAdd apply
+// the epilogue directly (one split); kSkPart writes the partial sums to
+// part[split][t][vrow].
+template <int EPI, bool BLK>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6k_skinny_kernel(
     SkSegs segs, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, const float *__restrict__ esc,
     int M, int K, int vrows, int nsplit, float *__restrict__ part) {
 	__shared__ __align__(16) _Float16 ah_s[2][16 * kHPadSk];
 	__shared__ __align__(16) _Float16 al_s[2][16 * kHPadSk];
 	__shared__ __align__(16) uint8_t w_s[4][16 * kQ6TileRow];
+	__shared__ __align__(16) float es_s[2][16];   // BLK: esc[t][kb] of the staged block
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment and descriptors in SGPRs
 	const int j = lane & 15, kq = lane >> 4;
@@ -328,6 +330,8 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 	};
 	// activation stage of block kb: 16 tokens x 256 K of hi and lo (zeros past M)
 	uint4 hreg[2], lreg[2];
+	float ereg = 0.0f;
+	const __amdgpu_buffer_rsrc_t ers = stream_rsrc(esc, BLK ? (uint32_t)M * (uint32_t)NB * 4u : 0u);
 	auto load_stage = [&](int kb) {
 #pragma unroll
 		for (int u = 0; u < 2; u++) {
@@ -336,6 +340,8 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 			hreg[u] = ld_b128(hrs, off);
 			lreg[u] = ld_b128(lrs, off);
 		}
+		if (BLK)   // tokens past M: zero (their activations are zero too)
+			ereg = __builtin_bit_cast(float, ld_b32(ers, tid < M ? 4u * ((uint32_t)tid * NB + kb) : kBufNone));
 	};
 	auto store_stage = [&](int slot) {
 #pragma unroll
@@ -344,6 +350,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 			*(uint4 *)(ah_s[slot] + t * kHPadSk + 8 * p) = hreg[u];
 			*(uint4 *)(al_s[slot] + t * kHPadSk + 8 * p) = lreg[u];
 		}
+		if (BLK && tid < 16) es_s[slot][tid] = ereg;
 	};
 
 	uint4 wv0[4], wv1[4];
@@ -369,6 +376,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 				const _Float16 *al = al_s[half] + j * kHPadSk + 4 * kq;
 				const float dd = f16_to_f32(b.d);
 				const uint32_t scw[4] = {b.sc.x, b.sc.y, b.sc.z, b.sc.w};
+				v4f accb = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
 				for (int gg = 0; gg < 16; gg++) {
 					// K = 16gg + 4kq + e: half n = gg/8, k = (gg/2)%4, l = 16(gg%2) + 4kq + e
@@ -384,10 +392,26 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 					v4f pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(ah + 16 * gg), wv, zero, 0, 0, 0);
 					pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(al + 16 * gg), wv, pr, 0, 0, 0);
 					const float s = dd * (float)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 0xFFu);
-					acc[0] = __builtin_fmaf(pr[0], s, acc[0]);
-					acc[1] = __builtin_fmaf(pr[1], s, acc[1]);
-					acc[2] = __builtin_fmaf(pr[2], s, acc[2]);
-					acc[3] = __builtin_fmaf(pr[3], s, acc[3]);
+					if (BLK) {
+						accb[0] = __builtin_fmaf(pr[0], s, accb[0]);
+						accb[1] = __builtin_fmaf(pr[1], s, accb[1]);
+						accb[2] = __builtin_fmaf(pr[2], s, accb[2]);
+						accb[3] = __builtin_fmaf(pr[3], s, accb[3]);
+					} else {
+						acc[0] = __builtin_fmaf(pr[0], s, acc[0]);
+						acc[1] = __builtin_fmaf(pr[1], s, acc[1]);
+						acc[2] = __builtin_fmaf(pr[2], s, acc[2]);
+						acc[3] = __builtin_fmaf(pr[3], s, acc[3]);
+					}
+				}
+				if (BLK) {
+					// this block's powers of two of the lane's tokens, staged with the
+					// activations
+					const float4 eb = *(const float4 *)&es_s[half][t0];
+					acc[0] = __builtin_fmaf(accb[0], eb.x, acc[0]);
+					acc[1] = __builtin_fmaf(accb[1], eb.y, acc[1]);
+					acc[2] = __builtin_fmaf(accb[2], eb.z, acc[2]);
+					acc[3] = __builtin_fmaf(accb[3], eb.w, acc[3]);
 				}
 				if (more) {
 					store_stage(half ^ 1);
@@ -398,7 +422,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 	}
 	float y[4];
 #pragma unroll
-	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? acc[v] * esc[t0 + v] : 0.0f;
+	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? (BLK ? acc[v] : acc[v] * esc[t0 + v]) : 0.0f;
 	if (EPI == kSkPart) {
 		if (ok)
 #pragma unroll
@@ -436,6 +460,37 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkSegs segs, const f
 		*o += y;
 	else
 		*o = y + (S.bias ? S.bias[r] : 0.0f);
+}
+
+// Grid (F/256, m): the gate/up partials of one 256-row block of segment 0
+// (gate rows r, up rows F + r, splits summed in order as the SwiGLU reduce
+// does), h = silu(g)*u, then h as fp16 hi + lo scaled by one power of two
+// for the block: escb[t][block] = 2^e with e the exponent of the block's
+// largest |h| (f16_split_exp), x = (hi + lo) * escb.
+__global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restrict__ part, int nsplit, int F,
+                                                           _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+                                                           float *__restrict__ escb) {
+	__shared__ float red[4];
+	const int r = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y, lane = threadIdx.x & 63;
+	const int vrows = 2 * F;
+	float g = 0.0f, u = 0.0f;
+	for (int sp = 0; sp < nsplit; sp++) {
+		g += part[((size_t)sp * 16 + t) * vrows + r];
+		u += part[((size_t)sp * 16 + t) * vrows + F + r];
+	}
+	const float h = g / (1.0f + expf(-g)) * u;
+	float a = __builtin_fabsf(h);
+	a = __builtin_isfinite(a) ? a : 0.0f;
+	a = wave_max(a);
+	if (lane == 0) red[threadIdx.x >> 6] = a;
+	__syncthreads();
+	a = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+	const int e = f16_split_exp(a);
+	const float f = h * __builtin_ldexpf(1.0f, -e);
+	const _Float16 hi = (_Float16)f;
+	xh[(size_t)t * F + r] = hi;
+	xl[(size_t)t * F + r] = (_Float16)(f - (float)hi);
+	if (threadIdx.x == 0) escb[(size_t)t * (F >> 8) + blockIdx.x] = __builtin_ldexpf(1.0f, e);
 }
 
 int reduce(const SkSegs &segs, int epi, const float *part, int nsplit, int m, int vrows) {
@@ -495,6 +550,13 @@ int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, i
 	return (direct || epi == kSkPart) ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
 }
 
+int swiglu_split(const float *part, int nsplit, int F, int m, _Float16 *xh, _Float16 *xl, float *escb) {
+	if (F % kQK) return set_error(HAKO_GPU_EINVAL, "SwiGLU split needs whole 256-row blocks (F = %d)", F);
+	hipLaunchKernelGGL(swiglu_split_kernel, dim3(F / kQK, m), dim3(256), 0, stream(), part, nsplit, F, xh, xl, escb);
+	HK_LAUNCHED("swiglu_split");
+	return HAKO_GPU_OK;
+}
+
 int q6k_skinny_splits(int n_in, int vrows) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
 	int ns = (g_q6_target + tiles - 1) / tiles;        // enough workgroups to fill the chip
@@ -508,7 +570,7 @@ size_t q6k_skinny_part_floats(int n_in, int vrows, int epi) {
 }
 
 int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *xl, const float *esc, int m,
-               int n_in, int vrows, float *part, size_t part_cap) {
+               int n_in, int vrows, float *part, size_t part_cap, bool esc_per_block) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
 	const int ns = q6k_skinny_splits(n_in, vrows);
 	const bool direct = ns == 1 && epi != kSkPart;
@@ -516,15 +578,19 @@ int q6k_skinny(const SkSegs &segs, int epi, const _Float16 *xh, const _Float16 *
 		return set_error(HAKO_GPU_EINVAL, "Q6_K skinny split needs a workspace of %zu floats (has %zu)",
 		                 q6k_skinny_part_floats(n_in, vrows, epi), part ? part_cap : (size_t)0);
 	const dim3 grid(tiles * ns);
-	if (!direct)
-		hipLaunchKernelGGL(q6k_skinny_kernel<kSkPart>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
-		                   vrows, ns, part);
-	else if (epi == kSkStore)
-		hipLaunchKernelGGL(q6k_skinny_kernel<kSkStore>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
-		                   vrows, 1, part);
-	else
-		hipLaunchKernelGGL(q6k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in,
-		                   vrows, 1, part);
+#define HK_Q6SK(E, B, NS) \
+	hipLaunchKernelGGL((q6k_skinny_kernel<E, B>), grid, dim3(kT), 0, stream(), segs, xh, xl, esc, m, n_in, vrows, NS, part)
+	if (!direct) {
+		if (esc_per_block) HK_Q6SK(kSkPart, true, ns);
+		else HK_Q6SK(kSkPart, false, ns);
+	} else if (epi == kSkStore) {
+		if (esc_per_block) HK_Q6SK(kSkStore, true, 1);
+		else HK_Q6SK(kSkStore, false, 1);
+	} else {
+		if (esc_per_block) HK_Q6SK(kSkAdd, true, 1);
+		else HK_Q6SK(kSkAdd, false, 1);
+	}
+#undef HK_Q6SK
 	HK_LAUNCHED("q6k_skinny");
 	return (direct || epi == kSkPart) ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
 }
