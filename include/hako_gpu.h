@@ -59,8 +59,10 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_Q6K_WAVES      4
 #define HAKO_TUNE_Q4K_FLAT_ITEMS 5   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
 /* Workgroups a skinny (2..16 token) Q4_K / Q6_K launch aims for through its
- * K split (0: the defaults, 512 and 1024). A decoder sizes its split workspace when it is
- * created; a later, larger target makes its steps fail with EINVAL. */
+ * K split (0: the defaults, 512 and 1024); the split count sets the order in
+ * which the fp32 partial sums are added. A decoder sizes its split workspace
+ * when it is created; a later, larger target makes its steps fail with
+ * EINVAL. */
 #define HAKO_TUNE_SKINNY_Q4K_WGS 6
 #define HAKO_TUNE_SKINNY_Q6K_WGS 7
 int hako_gpu_tune(int knob, int value);
