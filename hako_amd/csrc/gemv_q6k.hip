@@ -83,13 +83,16 @@ __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >
 // weights (k = kp + 2kk; qh bits 2k..2k+1 taken at shift 2kp, 2kp+4).
 __device__ __forceinline__ float q6_dot(const Q6Buf &W, const Q6Col &col, int kp, int sel) {
 	float acc0 = col.nsx[0], acc1 = col.nsx[1];
-	const uint32_t lo = 0x0F0F0F0Fu, m2 = 0x03030303u;
+	const uint32_t lo = 0x0F0F0F0Fu, hb = 0x30303030u;
 	const uint32_t ql[4] = {W.ql.x, W.ql.y, W.ql.z, W.ql.w}, qh[4] = {W.qh.x, W.qh.y, W.qh.z, W.qh.w};
 	const int sh = 2 * kp;
 #pragma unroll
 	for (int u = 0; u < 4; u++) {
-		const uint32_t w0 = (ql[u] & lo) | (((qh[u] >> sh) & m2) << 4);
-		const uint32_t w1 = ((ql[u] >> 4) & lo) | (((qh[u] >> (sh + 4)) & m2) << 4);
+		// qh bits 2k, 2k+1 of each byte to bits 4, 5 with one shift each (k = kp:
+		// left by 4 - 2kp; k = kp + 2: right by 2kp); what other bytes shift in
+		// lands outside bits 4-5
+		const uint32_t w0 = (ql[u] & lo) | ((qh[u] << (4 - sh)) & hb);
+		const uint32_t w1 = ((ql[u] >> 4) & lo) | ((qh[u] >> sh) & hb);
 #pragma unroll
 		for (int b = 0; b < 4; b++) {
 			acc0 = __builtin_fmaf(byte_f(w0, b), col.xv[0][4 * u + b], acc0);
