@@ -641,10 +641,85 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	}
 }
 
+// The merge of one query head's chunk records by the HD threads of its waves
+// (waves hw0 .. hw0 + HD/64 - 1 of the workgroup; thread ht = value dim):
+// M = max m_c, weights e^(m_c - M) / L with L = sum l_c e^(m_c - M), output
+// sum over chunks of weight * o_c, in chunk order. grp: the head's record of
+// chunk 0 (chunk c at grp + c * kMaxG * (HD + 2)); nact chunks; r_s and ws
+// (HD floats) are this head's LDS. Every thread of the workgroup calls it
+// with the same nact (it holds barriers).
+template <int HD>
+__device__ __forceinline__ float merge_head(const float *__restrict__ grp, int nact, int ht, int lane, int wave,
+                                            int hw0, float (*r_s)[4], float *ws) {
+	constexpr int REC = HD + 2, NWH = HD / 64;
+	constexpr int OB = 16;                       // o rows in flight per thread
+	constexpr size_t CS = (size_t)kMaxG * REC;   // floats between two chunks' records of one head
+	// one round trip for the common case (nact <= HD chunks): every thread's
+	// (m, l) of chunk ht and its value dim of the first OB chunks, issued together
+	float m0 = -INFINITY, l0 = 0.0f;
+	if (ht < nact) {
+		m0 = grp[ht * CS + HD];
+		l0 = grp[ht * CS + HD + 1];
+	}
+	float ov[OB];
+#pragma unroll
+	for (int j = 0; j < OB; j++) ov[j] = j < nact ? grp[j * CS + ht] : 0.0f;
+	float mx = m0;
+	for (int cc = ht + HD; cc < nact; cc += HD) mx = __builtin_fmaxf(mx, grp[cc * CS + HD]);
+	mx = wave_max(mx);
+	if (lane == 0) r_s[0][wave] = mx;
+	__syncthreads();
+	mx = r_s[0][hw0];
+#pragma unroll
+	for (int w = 1; w < NWH; w++) mx = __builtin_fmaxf(mx, r_s[0][hw0 + w]);
+	float lsum = ht < nact ? l0 * expf(m0 - mx) : 0.0f;
+	for (int cc = ht + HD; cc < nact; cc += HD) lsum += grp[cc * CS + HD + 1] * expf(grp[cc * CS + HD] - mx);
+	lsum = wave_sum(lsum);
+	if (lane == 0) r_s[1][wave] = lsum;
+	__syncthreads();
+	lsum = r_s[1][hw0];
+#pragma unroll
+	for (int w = 1; w < NWH; w++) lsum += r_s[1][hw0 + w];
+	const float inv = 1.0f / lsum;
+	float acc = 0.0f;
+	for (int c0 = 0; c0 < nact; c0 += HD) {
+		const int nc = min(HD, nact - c0);
+		if (c0) __syncthreads();   // ws of the previous batch is consumed
+		if (ht < nc) ws[ht] = expf((c0 ? grp[(c0 + ht) * CS + HD] : m0) - mx) * inv;
+		__syncthreads();
+		const float *r = grp + c0 * CS + ht;
+		int cc = 0;
+		if (c0 == 0) {
+#pragma unroll
+			for (int j = 0; j < OB; j++)
+				if (j < nc) acc = __builtin_fmaf(ov[j], ws[j], acc);
+			cc = min(OB, nc);
+		}
+		for (; cc + OB <= nc; cc += OB) {
+			float o[OB];
+#pragma unroll
+			for (int j = 0; j < OB; j++) o[j] = r[(cc + j) * CS];
+#pragma unroll
+			for (int j = 0; j < OB; j++) acc = __builtin_fmaf(o[j], ws[cc + j], acc);
+		}
+		for (; cc < nc; cc++) acc = __builtin_fmaf(r[cc * CS], ws[cc], acc);
+	}
+	return acc;
+}
+
+// q8_32 code of this lane's value a, the 32-block being the lanes of equal
+// lane / 32; sc = the block's scale (quantize_row_q8_32, src/quant.c:127-144).
+__device__ __forceinline__ int8_t q8_lane32(float a, float &sc) {
+	a = ftz(a);
+	float amax = __builtin_fabsf(a);
+#pragma unroll
+	for (int k = 1; k < 32; k <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, k));
+	sc = q8_xs(amax);
+	return (int8_t)q8_code(a, q8_inv(amax, sc));
+}
+
 // Grid (G, n_kv_heads, n_seq), HD threads: query head kvh*G + g of sequence
-// sq from its chunks' records — M = max m_c, weights e^(m_c - M) / L with
-// L = sum l_c e^(m_c - M), output sum over chunks of weight * o_c, in chunk
-// order. A launch of its own: the records of every chunk's workgroup are
+// sq from its chunks' records (merge_head). A launch of its own: the records of every chunk's workgroup are
 // visible at the kernel boundary, with no fence per workgroup. When xq is not
 // null the head's outputs are also quantized (q8_32: a head holds whole
 // 32-blocks) into xq[sq][H*HD] and xs[sq][H*HD/32], the activation of the
@@ -654,80 +729,81 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
                                                         float *__restrict__ att, int8_t *__restrict__ xq,
                                                         float *__restrict__ xs, int H, int KVH, int max_seq,
                                                         int max_chunks) {
-	constexpr int REC = HD + 2, NW = HD / 64;
-	constexpr int OB = 16;                       // o rows in flight per thread
-	constexpr size_t CS = (size_t)kMaxG * REC;   // floats between two chunks' records of one head
+	constexpr int REC = HD + 2;
 	__shared__ float w_s[HD];
-	__shared__ float r_s[2][NW];
-	const int g = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z, tid = threadIdx.x, lane = tid & 63,
-	          wave = tid >> 6;
+	__shared__ float r_s[2][4];
+	const int g = blockIdx.x, kvh = blockIdx.y, sq = blockIdx.z, tid = threadIdx.x;
 	const int G = H / KVH;
 	const int pos = posv[sq];
 	if (pos < 0 || pos >= max_seq) return;
-	const int nact = pos / kChunk + 1;
 	const float *grp = part + ((size_t)(sq * KVH + kvh) * max_chunks * kMaxG + g) * REC;
-	// one round trip for the common case (nact <= HD chunks): every thread's
-	// (m, l) of chunk tid and its value dim of the first OB chunks, issued together
-	float m0 = -INFINITY, l0 = 0.0f;
-	if (tid < nact) {
-		m0 = grp[tid * CS + HD];
-		l0 = grp[tid * CS + HD + 1];
-	}
-	float ov[OB];
-#pragma unroll
-	for (int j = 0; j < OB; j++) ov[j] = j < nact ? grp[j * CS + tid] : 0.0f;
-	float mx = m0;
-	for (int cc = tid + HD; cc < nact; cc += HD) mx = __builtin_fmaxf(mx, grp[cc * CS + HD]);
-	mx = wave_max(mx);
-	if (lane == 0) r_s[0][wave] = mx;
-	__syncthreads();
-	mx = r_s[0][0];
-#pragma unroll
-	for (int w = 1; w < NW; w++) mx = __builtin_fmaxf(mx, r_s[0][w]);
-	float lsum = tid < nact ? l0 * expf(m0 - mx) : 0.0f;
-	for (int cc = tid + HD; cc < nact; cc += HD) lsum += grp[cc * CS + HD + 1] * expf(grp[cc * CS + HD] - mx);
-	lsum = wave_sum(lsum);
-	if (lane == 0) r_s[1][wave] = lsum;
-	__syncthreads();
-	lsum = r_s[1][0];
-#pragma unroll
-	for (int w = 1; w < NW; w++) lsum += r_s[1][w];
-	const float inv = 1.0f / lsum;
-	// output: sum over chunks, in chunk order, of weight * o
-	float acc = 0.0f;
-	for (int c0 = 0; c0 < nact; c0 += HD) {
-		const int nc = min(HD, nact - c0);
-		if (c0) __syncthreads();   // w_s of the previous batch is consumed
-		if (tid < nc) w_s[tid] = expf((c0 ? grp[(c0 + tid) * CS + HD] : m0) - mx) * inv;
-		__syncthreads();
-		const float *r = grp + c0 * CS + tid;
-		int cc = 0;
-		if (c0 == 0) {
-#pragma unroll
-			for (int j = 0; j < OB; j++)
-				if (j < nc) acc = __builtin_fmaf(ov[j], w_s[j], acc);
-			cc = min(OB, nc);
-		}
-		for (; cc + OB <= nc; cc += OB) {
-			float o[OB];
-#pragma unroll
-			for (int j = 0; j < OB; j++) o[j] = r[(cc + j) * CS];
-#pragma unroll
-			for (int j = 0; j < OB; j++) acc = __builtin_fmaf(o[j], w_s[cc + j], acc);
-		}
-		for (; cc < nc; cc++) acc = __builtin_fmaf(r[cc * CS], w_s[cc], acc);
-	}
+	const float acc = merge_head<HD>(grp, pos / kChunk + 1, tid, tid & 63, tid >> 6, 0, r_s, w_s);
 	const size_t o = (size_t)sq * H * HD + (size_t)(kvh * G + g) * HD + tid;
 	att[o] = acc;
 	if (xq) {
-		const float a = ftz(acc);
-		float amax = __builtin_fabsf(a);
-#pragma unroll
-		for (int k = 1; k < 32; k <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, k));
-		const float sc = q8_xs(amax);
-		xq[o] = (int8_t)q8_code(a, q8_inv(amax, sc));
+		float sc;
+		xq[o] = q8_lane32(acc, sc);
 		if ((tid & 31) == 0) xs[o >> 5] = sc;
 	}
+}
+
+// One sequence: the merge above, the output projection (Q4_K) and its
+// residual add in one launch. Grid (D/256 input blocks, D/64 row chunks),
+// 256 threads: workgroup (b, rc) merges the 256/HD query heads whose outputs
+// are input block b of the projection (thread t: head 256b/HD + t/HD, dim
+// t % HD, merge_head), quantizes them with q8_32 (a
+// block holds whole 32-blocks, so the codes and scales are those of the full
+// row), and adds block b's terms of q4k_vec_dot (its eight sub-blocks,
+// reference src/quant.c:150-232) for the 64 rows of chunk rc to x with a
+// float atomic add. The D/256 blocks' sums meet in x in the order their
+// atomics arrive: every term is computed as in the two-kernel path, the order
+// of the per-block additions varies from run to run.
+template <int HD>
+__global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ part, const int *__restrict__ posv,
+                                                      const uint8_t *__restrict__ wo, float *__restrict__ x, int H,
+                                                      int KVH, int max_seq, int max_chunks, int D) {
+	__shared__ float w_s[256];
+	__shared__ float r_s[2][4];
+	__shared__ __align__(16) int8_t xq_s[256];
+	__shared__ __align__(16) float xs_s[8];
+	const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int pos = posv[0];
+	if (pos < 0 || pos >= max_seq) return;
+
+	// 1. this lane's weights: row 64*rc + 16*wave + lane/4, 64-weight group g of block b
+	const int g = lane & 3, row = blockIdx.y * 64 + 16 * wave + (lane >> 2);
+	const uint32_t rb = (uint32_t)(D / kQK) * kQ4Bytes;
+	const __amdgpu_buffer_rsrc_t wr = stream_rsrc(wo, (uint32_t)D * rb);
+	const uint32_t bo = row < D ? (uint32_t)row * rb + (uint32_t)b * kQ4Bytes : kBufNone;
+	Q4Buf wb;
+	wb.h = ld_b128(wr, bo);
+	wb.q0 = ld_b128(wr, bo + 16 + 32 * g);
+	wb.q1 = ld_b128(wr, bo + 32 + 32 * g);
+	__builtin_amdgcn_sched_barrier(0);
+
+	// 2. merge of head hh (kvh = hh / G, g = hh % G), HD threads per head
+	const int hs = tid / HD, hh = b * (256 / HD) + hs, G = H / KVH;
+	const float *grp = part + ((size_t)(hh / G) * max_chunks * kMaxG + hh % G) * (HD + 2);
+	const float acc =
+	    merge_head<HD>(grp, pos / kChunk + 1, tid % HD, lane, wave, hs * (HD / 64), r_s, w_s + hs * HD);
+
+	// 3. q8_32 of the block's 256 outputs (32 lanes per 32-block)
+	{
+		float sc;
+		xq_s[tid] = q8_lane32(acc, sc);
+		if ((tid & 31) == 0) xs_s[tid >> 5] = sc;
+	}
+	__syncthreads();
+
+	// 4. block b's terms of the lane's row, the row's four lanes summed, one atomic add
+	Q4Col col;
+	q4_col(xq_s, xs_s, g, col);
+	int ia, ib;
+	q4_isum(wb, col, ia, ib);
+	float f = q4_fold(wb, 16u * (g & 1), g >= 2 ? ~0u : 0u, ia, ib, col);
+	f += __shfl_xor(f, 1);
+	f += __shfl_xor(f, 2);
+	if (g == 0 && row < D) unsafeAtomicAdd(x + row, f);
 }
 
 // ── greedy pick (reference src/sample.c:28-32) ──
@@ -895,7 +971,7 @@ int add(float *x, const float *y, int n) {
 
 // Attention of layer l for every sequence: chunk records, then their merge
 // (which also writes the q8 rows of the output to mxq/mxs when not null).
-int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nullptr) {
+int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nullptr, bool merge = true) {
 	const hako_gpu_model &m = d->m;
 	const int KV = d->kv_dim, HD = m.head_dim, G = m.n_heads / m.n_kv_heads;
 	const float scale = 1.0f / sqrtf((float)HD);
@@ -912,6 +988,7 @@ int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nu
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale,
 		                   hsplit);
 		HK_LAUNCHED("attention");
+		if (!merge) return HAKO_GPU_OK;
 		hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->part, d->pos, d->att, mxq, mxs,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks);
 	} else {
@@ -919,6 +996,7 @@ int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nu
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks, kv_seq_stride, d->qkv_dim, scale,
 		                   hsplit);
 		HK_LAUNCHED("attention");
+		if (!merge) return HAKO_GPU_OK;
 		hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->part, d->pos, d->att, mxq, mxs,
 		                   m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks);
 	}
@@ -1052,10 +1130,22 @@ int enqueue_step(hako_gpu_decoder *d) {
 			if (int rc = hako_gpu_matmul(k, d->xn, B.t_k, B.wk, B.bk, KV, D)) return rc;
 			if (int rc = hako_gpu_matmul(v, d->xn, B.t_v, B.wv, B.bv, KV, D)) return rc;
 		}
-		// 2. rope, cache append, attention
-		if (int rc = attention(d, l)) return rc;
-		// 3. output projection + residual
-		if (B.t_o == HAKO_TYPE_Q4_K && fusable_q4(D) && D % rpw == 0) {
+		// 2. rope, cache append, attention; 3. output projection + residual
+		// (merged with the attention records in one launch for Q4_K)
+		const bool merge_o = B.t_o == HAKO_TYPE_Q4_K && D % kQK == 0 && kQK % m.head_dim == 0;
+		if (int rc = attention(d, l, nullptr, nullptr, !merge_o)) return rc;
+		if (merge_o) {
+			const dim3 grid(D / kQK, (D + 63) / 64);
+			if (m.head_dim == 128)
+				hipLaunchKernelGGL(merge_o_kernel<128>, grid, dim3(256), 0, stream(), d->part, d->pos,
+				                   (const uint8_t *)B.wo, d->x, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
+				                   D);
+			else
+				hipLaunchKernelGGL(merge_o_kernel<64>, grid, dim3(256), 0, stream(), d->part, d->pos,
+				                   (const uint8_t *)B.wo, d->x, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
+				                   D);
+			HK_LAUNCHED("attention merge + o");
+		} else if (B.t_o == HAKO_TYPE_Q4_K && fusable_q4(D) && D % rpw == 0) {
 			DecSegs s{};
 			s.n = 1;
 			s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D};

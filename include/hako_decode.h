@@ -59,7 +59,11 @@ typedef struct hako_gpu_decoder hako_gpu_decoder;
  * 1 <= n_seq <= 16. With n_seq > 1 every step advances all sequences
  * together, each matmul streaming its weights once for all of them (the
  * Q4_K_M mix: Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or Q6_K lm_head, and
- * d_model <= 4096); n_seq == 1 takes any F32/F16/Q4_K/Q6_K mix. */
+ * d_model <= 4096); n_seq == 1 takes any F32/F16/Q4_K/Q6_K mix. With
+ * n_seq == 1 and a Q4_K output projection, that projection's 256-input
+ * blocks are added to the residual with float atomics: the order of those
+ * additions, and so the last bits of the activations, may differ between
+ * runs (every other sum has a fixed order). */
 int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec);
 int hako_gpu_decoder_destroy(hako_gpu_decoder *dec);
 
