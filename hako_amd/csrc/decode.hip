@@ -43,9 +43,6 @@ constexpr int kMaxG = 8;     // query heads per KV head
 constexpr int kArgBlocks = 64;
 constexpr int kDecItems = 2; // row items per wave of the fused GEMV
 
-// silu (reference src/nn.c:29)
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
-
 // ── embedding row (deq_row, reference src/nn.c:55-59) ──
 
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ emb, int type, size_t row_bytes,
@@ -914,6 +911,9 @@ struct hako_gpu_decoder {
 	// prompt prefill (allocated on first use): chunk activations and records
 	float *pf_x = nullptr, *pf_xn = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr,
 	      *pf_tmp = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_part = nullptr;
+	int8_t *pf_xq = nullptr;                    // q8 rows [chunk][max(d_model, ffn)] and their scales
+	float *pf_xs = nullptr, *pf_esc = nullptr;  // fp16 split of the SwiGLU rows: hi, lo [chunk][ffn], esc[chunk]
+	_Float16 *pf_xh = nullptr, *pf_xl = nullptr;
 	int *pf_tok = nullptr, *pf_pos = nullptr;
 	int pf_chunk = 0;   // tokens per prefill pass
 	std::vector<void *> allocs;
@@ -960,6 +960,15 @@ bool fusable_q4(int n_in) { return n_in % kQK == 0 && n_in / kQK * 4 <= 64; }
 int rmsnorm(const float *x, const float *w, float *y, int n, float eps, int rows) {
 	hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream(), x, w, y, n, eps);
 	HK_LAUNCHED("rmsnorm");
+	return HAKO_GPU_OK;
+}
+
+// rmsnorm (weight w) and q8_32 of `rows` rows of x (n floats, n <= 4096) into
+// xq[rows][n], xs[rows][n/32]: the activation of multi-token Q4_K matmuls.
+int rmsnorm_q8_rows(const float *x, const float *w, float eps, int8_t *xq, float *xs, int n, int rows) {
+	hipLaunchKernelGGL(resid_rmsnorm_q8_kernel, dim3(rows), dim3(kRowT), 0, stream(), const_cast<float *>(x), nullptr,
+	                   0, w, eps, xq, xs, n);
+	HK_LAUNCHED("rmsnorm_q8");
 	return HAKO_GPU_OK;
 }
 
@@ -1249,6 +1258,11 @@ int prefill_alloc(hako_gpu_decoder *d) {
 	HK_ALLOC(d->pf_g, 4 * C * F);
 	HK_ALLOC(d->pf_u, 4 * C * F);
 	HK_ALLOC(d->pf_part, C * rec_per_token);
+	HK_ALLOC(d->pf_xq, C * (D > F ? D : F));
+	HK_ALLOC(d->pf_xs, 4 * C * (D > F ? D : F) / 32);
+	HK_ALLOC(d->pf_xh, 2 * C * F);
+	HK_ALLOC(d->pf_xl, 2 * C * F);
+	HK_ALLOC(d->pf_esc, 4 * C);
 	HK_ALLOC(d->pf_tok, 4 * C);
 	HK_ALLOC(d->pf_pos, 4 * C);
 #undef HK_ALLOC
@@ -1277,14 +1291,35 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 		const hako_gpu_block &B = d->blocks[l];
 		float *kcl = d->kc + seq_off + (size_t)l * d->max_seq * KV;
 		float *vcl = d->vc + seq_off + (size_t)l * d->max_seq * KV;
-		if (int rc = rmsnorm(d->pf_x, B.attn_norm, d->pf_xn, D, m.rms_eps, n)) return rc;
-		if (int rc = hako_gpu_matmul_batch(d->pf_q, d->pf_xn, B.t_q, B.wq, B.bq, n, D, D)) return rc;
-		if (int rc = hako_gpu_matmul_batch(d->pf_k, d->pf_xn, B.t_k, B.wk, B.bk, n, KV, D)) return rc;
-		if (int rc = hako_gpu_matmul_batch(d->pf_v, d->pf_xn, B.t_v, B.wv, B.bv, n, KV, D)) return rc;
+		// Q4_K matmuls of more than 16 tokens run fused: one rmsnorm+q8 launch
+		// per input, q/k/v as one launch over three row segments, gate/up as
+		// one launch writing silu(gate)*up, the residual added by the o and
+		// down launches; other types and short passes take one call per matmul.
+		const bool multi = n > kSkMaxTokens && D <= 4 * kRowT;
+		const bool f_qkv = multi && B.t_q == HAKO_TYPE_Q4_K && B.t_k == HAKO_TYPE_Q4_K && B.t_v == HAKO_TYPE_Q4_K;
+		const bool f_o = multi && B.t_o == HAKO_TYPE_Q4_K;
+		const bool f_gu = multi && B.t_gate == HAKO_TYPE_Q4_K && B.t_up == HAKO_TYPE_Q4_K;
+		if (f_qkv) {
+			if (int rc = rmsnorm_q8_rows(d->pf_x, B.attn_norm, m.rms_eps, d->pf_xq, d->pf_xs, D, n)) return rc;
+			SkSegs s{};
+			s.n = 3;
+			s.s[0] = {(const uint8_t *)B.wq, B.bq, d->pf_q, 0, D, D};
+			s.s[1] = {(const uint8_t *)B.wk, B.bk, d->pf_k, D, KV, KV};
+			s.s[2] = {(const uint8_t *)B.wv, B.bv, d->pf_v, D + KV, KV, KV};
+			if (int rc = q4k_gemm_segs(s, kSkStore, d->pf_xq, d->pf_xs, n, D, D + 2 * KV)) return rc;
+		} else {
+			if (int rc = rmsnorm(d->pf_x, B.attn_norm, d->pf_xn, D, m.rms_eps, n)) return rc;
+			if (int rc = hako_gpu_matmul_batch(d->pf_q, d->pf_xn, B.t_q, B.wq, B.bq, n, D, D)) return rc;
+			if (int rc = hako_gpu_matmul_batch(d->pf_k, d->pf_xn, B.t_k, B.wk, B.bk, n, KV, D)) return rc;
+			if (int rc = hako_gpu_matmul_batch(d->pf_v, d->pf_xn, B.t_v, B.wv, B.bv, n, KV, D)) return rc;
+		}
 		hipLaunchKernelGGL(rope_append_kernel, dim3(n), dim3(256), 0, stream(), d->pf_k, d->pf_v, d->rope, d->pf_pos,
 		                   kcl, vcl, KVH, HD, d->max_seq);
 		HK_LAUNCHED("rope_append");
-		// token i attends over positions [0, pos0 + i] of the sequence's cache
+		// token i attends over positions [0, pos0 + i] of the sequence's cache;
+		// the merge also writes the q8 rows of its output for a fused o
+		int8_t *mxq = f_o ? d->pf_xq : nullptr;
+		float *mxs = f_o ? d->pf_xs : nullptr;
 		const dim3 ag(d->max_chunks, KVH, n), mg(G, KVH, n);
 		if (HD == 128) {
 			hipLaunchKernelGGL((attn_kernel<128, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
@@ -1292,28 +1327,55 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 			                   1);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
-			                   nullptr, nullptr,
-			                   m.n_heads, KVH, d->max_seq, d->max_chunks);
+			                   mxq, mxs, m.n_heads, KVH, d->max_seq, d->max_chunks);
 		} else {
 			hipLaunchKernelGGL((attn_kernel<64, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
 			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale,
 			                   1);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
-			                   nullptr, nullptr,
-			                   m.n_heads, KVH, d->max_seq, d->max_chunks);
+			                   mxq, mxs, m.n_heads, KVH, d->max_seq, d->max_chunks);
 		}
 		HK_LAUNCHED("attention merge");
-		if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_att, B.t_o, B.wo, nullptr, n, D, D)) return rc;
-		if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
-		if (int rc = rmsnorm(d->pf_x, B.ffn_norm, d->pf_xn, D, m.rms_eps, n)) return rc;
-		if (int rc = hako_gpu_matmul_batch(d->pf_g, d->pf_xn, B.t_gate, B.gate, nullptr, n, F, D)) return rc;
-		if (int rc = hako_gpu_matmul_batch(d->pf_u, d->pf_xn, B.t_up, B.up, nullptr, n, F, D)) return rc;
-		hipLaunchKernelGGL(silu_mul_kernel, dim3((n * F + 255) / 256), dim3(256), 0, stream(), d->pf_g, d->pf_g,
-		                   d->pf_u, n * F);
-		HK_LAUNCHED("silu_mul");
-		if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_g, B.t_down, B.down, nullptr, n, D, F)) return rc;
-		if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
+		if (f_o) {
+			SkSegs s{};
+			s.n = 1;
+			s.s[0] = {(const uint8_t *)B.wo, nullptr, d->pf_x, 0, D, D};
+			if (int rc = q4k_gemm_segs(s, kSkAdd, d->pf_xq, d->pf_xs, n, D, D)) return rc;
+		} else {
+			if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_att, B.t_o, B.wo, nullptr, n, D, D)) return rc;
+			if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
+		}
+		if (f_gu) {
+			if (int rc = rmsnorm_q8_rows(d->pf_x, B.ffn_norm, m.rms_eps, d->pf_xq, d->pf_xs, D, n)) return rc;
+			SkSegs s{};
+			s.n = 2;
+			s.s[0] = {(const uint8_t *)B.gate, nullptr, d->pf_g, 0, F, F};
+			s.s[1] = {(const uint8_t *)B.up, nullptr, d->pf_g, 0, F, F};
+			if (int rc = q4k_gemm_segs(s, kSkSwiGLU, d->pf_xq, d->pf_xs, n, D, 2 * F)) return rc;
+		} else {
+			if (int rc = rmsnorm(d->pf_x, B.ffn_norm, d->pf_xn, D, m.rms_eps, n)) return rc;
+			if (int rc = hako_gpu_matmul_batch(d->pf_g, d->pf_xn, B.t_gate, B.gate, nullptr, n, F, D)) return rc;
+			if (int rc = hako_gpu_matmul_batch(d->pf_u, d->pf_xn, B.t_up, B.up, nullptr, n, F, D)) return rc;
+			hipLaunchKernelGGL(silu_mul_kernel, dim3((n * F + 255) / 256), dim3(256), 0, stream(), d->pf_g, d->pf_g,
+			                   d->pf_u, n * F);
+			HK_LAUNCHED("silu_mul");
+		}
+		// down + residual: h = pf_g
+		if (n > kSkMaxTokens && B.t_down == HAKO_TYPE_Q6_K) {
+			if (int rc = f16_split(d->pf_g, d->pf_xh, d->pf_xl, d->pf_esc, n, F)) return rc;
+			if (int rc = q6k_gemm_split(d->pf_x, B.down, d->pf_xh, d->pf_xl, d->pf_esc, nullptr, n, D, F, true))
+				return rc;
+		} else if (n > kSkMaxTokens && B.t_down == HAKO_TYPE_Q4_K) {
+			if (int rc = hako_gpu_quantize_q8_32(d->pf_g, n, F, d->pf_xq, d->pf_xs)) return rc;
+			SkSegs s{};
+			s.n = 1;
+			s.s[0] = {(const uint8_t *)B.down, nullptr, d->pf_x, 0, D, D};
+			if (int rc = q4k_gemm_segs(s, kSkAdd, d->pf_xq, d->pf_xs, n, F, D)) return rc;
+		} else {
+			if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_g, B.t_down, B.down, nullptr, n, D, F)) return rc;
+			if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
+		}
 	}
 	return HAKO_GPU_OK;
 }

@@ -63,11 +63,15 @@ __device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 
 constexpr int kAPad = 272;   // bytes per staged token row: 256 + 16 (conflict-free 16-byte reads)
 
-__global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const uint8_t *__restrict__ w,
-                                                       const int8_t *__restrict__ xq,
-                                                       const float *__restrict__ xs,
-                                                       const float *__restrict__ bias,
-                                                       float *__restrict__ y, int M, int N, int K) {
+// Rows of a launch come from up to three segments (SkSegs: weight rows
+// [row0, row0 + rows) of the launch's N rows, each with its own output matrix
+// out[t*ld + r] and bias); a 64-row tile lies in one segment (segment starts
+// are multiples of 64). Epilogues: Store out = y (+ bias), Add out += y (a
+// residual), SwiGLU: N = 2F rows, tile j holds gate rows 32j.. (segment 0) and
+// the same up rows (segment 1); out (segment 0's) = silu(gate)*up.
+template <int EPI>
+__global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const int8_t *__restrict__ xq,
+                                                       const float *__restrict__ xs, int M, int N, int K) {
 	__shared__ __align__(16) uint8_t w_s[kTN * kQ4Bytes];   // this stage's block of each row
 	__shared__ __align__(16) int8_t a_s[kTM * kAPad];       // this stage's 256 xq of each token
 	__shared__ __align__(16) float ds_s[8][kTN];            // d*s   [sub-block][row]
@@ -78,24 +82,46 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const uint8_t *__restrict
 	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
 	if (tile >= mtiles * ntiles) return;
 	const int m0 = (tile / ntiles) * kTM, n0 = (tile % ntiles) * kTN;
-	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 	const int wr = wave & 1, wt = wave >> 1, li = lane & 31, kh = lane >> 5;
 	const int NB = K >> 8, NS = K >> 5;
 	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
-	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(w, rb * (uint32_t)N);
+	// the tile's segment (Store / Add), or for SwiGLU the matrix this wave
+	// stages (waves 0-1 gate rows, 2-3 up rows) and the tile's first output row
+	const int si = EPI == kSkSwiGLU ? (wave >> 1)
+	               : (segs.n > 2 && n0 >= segs.s[2].row0) ? 2 : (segs.n > 1 && n0 >= segs.s[1].row0) ? 1 : 0;
+	const SkSeg S = si == 0 ? segs.s[0] : (si == 1 ? segs.s[1] : segs.s[2]);
+	const int r0 = EPI == kSkSwiGLU ? 32 * (n0 / kTN) : n0 - S.row0;   // first row of the tile in S
+	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, rb * (uint32_t)S.rows);
 	const __amdgpu_buffer_rsrc_t ars = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
 	const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
 
-	// Stage map: weights 64 rows x 9 pieces of 16 B (3 per thread), xq 64
-	// tokens x 16 pieces (4 per thread), xs 64 tokens x 8 (2 per thread).
+	// Stage map: weights 64 rows x 9 pieces of 16 B (3 per thread; SwiGLU:
+	// each half of the workgroup 32 rows of its matrix), xq 64 tokens x 16
+	// pieces (4 per thread), xs 64 tokens x 8 (2 per thread).
+	auto wpiece = [&](int u, int &row, int &piece, int &srow) -> bool {   // tile row, piece, row in S
+		if (EPI == kSkSwiGLU) {
+			const int c = (tid & 127) + 128 * u;
+			row = 32 * (wave >> 1) + c / 9;
+			piece = c % 9;
+			srow = r0 + c / 9;
+			return c < 32 * 9;
+		}
+		const int c = tid + kGT * u;
+		row = c / 9;
+		piece = c - row * 9;
+		srow = r0 + row;
+		return c < kTN * 9;
+	};
 	uint4 wreg[3], areg[4];
 	float sreg[2];
 	auto load_stage = [&](int kb) {
 #pragma unroll
 		for (int u = 0; u < 3; u++) {
-			const int c = tid + kGT * u, row = c / 9, piece = c - row * 9;
-			const bool on = c < kTN * 9 && n0 + row < N;
-			wreg[u] = ld_b128(wrs, on ? (uint32_t)(n0 + row) * rb + (uint32_t)kb * kQ4Bytes + 16u * piece : kBufNone);
+			int row, piece, srow;
+			const bool on = wpiece(u, row, piece, srow) && srow < S.rows;
+			wreg[u] = ld_b128(wrs, on ? (uint32_t)srow * rb + (uint32_t)kb * kQ4Bytes + 16u * piece : kBufNone);
 		}
 #pragma unroll
 		for (int u = 0; u < 4; u++) {
@@ -113,8 +139,8 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const uint8_t *__restrict
 	auto store_stage = [&]() {
 #pragma unroll
 		for (int u = 0; u < 3; u++) {
-			const int c = tid + kGT * u, row = c / 9, piece = c - row * 9;
-			if (c < kTN * 9) *(uint4 *)(w_s + row * kQ4Bytes + 16 * piece) = wreg[u];
+			int row, piece, srow;
+			if (wpiece(u, row, piece, srow)) *(uint4 *)(w_s + row * kQ4Bytes + 16 * piece) = wreg[u];
 		}
 #pragma unroll
 		for (int u = 0; u < 4; u++) {
@@ -190,18 +216,38 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const uint8_t *__restrict
 		}
 		__syncthreads();   // before the next stage overwrites LDS
 	}
-	// lane: token m0+32wt+li, rows n0+32wr+8q4+4kh+r
+	// lane: token m0+32wt+li, tile rows 32wr+8q4+4kh+r
 	const int tok = m0 + 32 * wt + li;
+	if (EPI == kSkSwiGLU) {
+		// the up half (wr = 1) hands its sums to the gate half through LDS
+		// (the loop ended with a barrier: a_s is free)
+		float *up_s = (float *)a_s + (wt * 64 + lane) * 16;
+		if (wr == 1)
+#pragma unroll
+			for (int v = 0; v < 16; v++) up_s[v] = acc[v] + accm[v];
+		__syncthreads();
+		if (wr == 1 || tok >= M) return;
+		float *hr = segs.s[0].out + (size_t)tok * segs.s[0].ld;
+#pragma unroll
+		for (int q4 = 0; q4 < 4; q4++) {
+			const int f = r0 + 8 * q4 + 4 * kh;
+#pragma unroll
+			for (int r = 0; r < 4; r++)
+				if (f + r < segs.s[0].rows) hr[f + r] = silu(acc[4 * q4 + r] + accm[4 * q4 + r]) * up_s[4 * q4 + r];
+		}
+		return;
+	}
 	if (tok >= M) return;
-	float *yr = y + (size_t)tok * N;
+	float *yr = S.out + (size_t)tok * S.ld;
 #pragma unroll
 	for (int q4 = 0; q4 < 4; q4++) {
-		const int row = n0 + 32 * wr + 8 * q4 + 4 * kh;
+		const int row = r0 + 32 * wr + 8 * q4 + 4 * kh;
 #pragma unroll
 		for (int r = 0; r < 4; r++)
-			if (row + r < N) {
+			if (row + r < S.rows) {
 				const float v = acc[4 * q4 + r] + accm[4 * q4 + r];
-				yr[row + r] = bias ? v + bias[row + r] : v;
+				if (EPI == kSkAdd) yr[row + r] += v;
+				else yr[row + r] = S.bias ? v + S.bias[row + r] : v;
 			}
 	}
 }
@@ -287,7 +333,7 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
                                                        const _Float16 *__restrict__ xl,
                                                        const float *__restrict__ esc,
                                                        const float *__restrict__ bias,
-                                                       float *__restrict__ y, int M, int N, int K) {
+                                                       float *__restrict__ y, int M, int N, int K, int add) {
 	__shared__ __align__(16) _Float16 ah_s[kTM * kHPad];   // activation hi [token][k]
 	__shared__ __align__(16) _Float16 al_s[kTM * kHPad];   // activation lo
 	__shared__ __align__(16) _Float16 wq_s[kTN * kHPad];   // q - 32 [row][k]
@@ -397,7 +443,11 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 #pragma unroll
 	for (int v = 0; v < 16; v++) {
 		const int tok = m0 + 32 * wt + 8 * (v >> 2) + 4 * kh + (v & 3);
-		if (tok < M) y[(size_t)tok * N + row] = acc[v] * esc[tok] + bv;
+		if (tok < M) {
+			float *o = y + (size_t)tok * N + row;
+			const float r = acc[v] * esc[tok] + bv;
+			*o = add ? *o + r : r;
+		}
 	}
 }
 
@@ -434,18 +484,40 @@ int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const f
 	if (int rc = check_gemm("Q4_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ4Bytes, w)) return rc;
 	if (((uintptr_t)w & 15) || ((uintptr_t)xq & 15) || ((uintptr_t)xs & 3))
 		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM needs w and xq 16-byte aligned");
+	SkSegs segs{};
+	segs.n = 1;
+	segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
 	if (m <= kSkMaxTokens) {   // a few tokens: the skinny kernel
-		SkSegs segs{};
-		segs.n = 1;
-		segs.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, n_out};
 		float *part = nullptr;
 		const size_t pf = q4k_skinny_part_floats(n_in, n_out, kSkStore);
 		if (int rc = skinny_split_workspace(pf, &part)) return rc;
 		if (int rc = q4k_skinny(segs, kSkStore, xq, xs, m, n_in, n_out, part, pf)) return rc;
 		return ok();
 	}
-	hipLaunchKernelGGL(q4k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
-	                   xq, xs, bias, y, m, n_out, n_in);
+	return q4k_gemm_segs(segs, kSkStore, xq, xs, m, n_in, n_out);
+}
+
+int q4k_gemm_segs(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows) {
+	if (m <= kSkMaxTokens || n_in % kQK || segs.n < 1 || segs.n > 3 || (epi == kSkSwiGLU && segs.n != 2))
+		return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM segments: m %d > %d, n_in %% 256 == 0, 1-3 segments", m,
+		                 kSkMaxTokens);
+	for (int i = 0; i < segs.n; i++) {
+		const SkSeg &g = segs.s[i];
+		if (int rc = check_gemm("Q4_K GEMM", m, g.rows, n_in, (size_t)n_in / kQK * kQ4Bytes, g.w)) return rc;
+		if (((uintptr_t)g.w & 15) || ((uintptr_t)xq & 15) || ((uintptr_t)xs & 3))
+			return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM needs w and xq 16-byte aligned");
+		const bool tiled = epi == kSkSwiGLU ? g.row0 == 0 && g.rows == segs.s[0].rows && g.rows % 32 == 0
+		                                    : g.row0 % kTN == 0 && (i + 1 == segs.n || g.row0 + g.rows == segs.s[i + 1].row0);
+		if (!tiled) return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM segment %d does not fit the 64-row tiles", i);
+	}
+	const int N = epi == kSkSwiGLU ? 2 * segs.s[0].rows : vrows;
+	const dim3 grid(gemm_grid(m, N));
+	switch (epi) {
+	case kSkStore: hipLaunchKernelGGL(q4k_gemm_kernel<kSkStore>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in); break;
+	case kSkAdd: hipLaunchKernelGGL(q4k_gemm_kernel<kSkAdd>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in); break;
+	case kSkSwiGLU: hipLaunchKernelGGL(q4k_gemm_kernel<kSkSwiGLU>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in); break;
+	default: return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM epilogue %d", epi);
+	}
 	HK_LAUNCHED("q4k_gemm");
 	return ok();
 }
@@ -477,8 +549,15 @@ int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, 
 		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part, pf)) return rc;
 		return ok();
 	}
+	return q6k_gemm_split(y, w, xh, xl, esc, bias, m, n_out, n_in, false);
+}
+
+int q6k_gemm_split(float *y, const void *w, const _Float16 *xh, const _Float16 *xl, const float *esc,
+                   const float *bias, int m, int n_out, int n_in, bool add) {
+	if (int rc = check_gemm("Q6_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ6Bytes, w)) return rc;
+	if (m <= kSkMaxTokens) return set_error(HAKO_GPU_EINVAL, "Q6_K GEMM on split rows needs m > %d", kSkMaxTokens);
 	hipLaunchKernelGGL(q6k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
-	                   xh, xl, esc, bias, y, m, n_out, n_in);
+	                   xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0);
 	HK_LAUNCHED("q6k_gemm");
 	return ok();
 }

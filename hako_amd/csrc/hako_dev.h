@@ -26,6 +26,9 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
 // denormal mode.
 __device__ __forceinline__ float ftz(float v) { return __builtin_fabsf(v) < kFltMin ? 0.0f : v; }
 
+// silu (reference src/nn.c:29)
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
 	return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);

@@ -61,4 +61,14 @@ int swiglu_split(const float *part, int nsplit, int F, int m, _Float16 *xh, _Flo
 // row, esc[m] (gemm.hip).
 int f16_split(const float *x, _Float16 *xh, _Float16 *xl, float *esc, int m, int n);
 
+// Multi-token (m > 16) matmuls of gemm.hip. Q4_K x q8 over row segments of
+// vrows launch rows (segment starts multiples of 64; each segment's out is
+// [m][ld]): Store, Add, or SwiGLU (segment 0 gate and segment 1 up, both
+// rows [0, F) with F % 32 == 0; out of segment 0 = silu(gate)*up).
+int q4k_gemm_segs(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows);
+// Q6_K x the fp16 hi/lo rows of f16_split: y[m][n_out] = (or += when add)
+// W x (+ bias).
+int q6k_gemm_split(float *y, const void *w, const _Float16 *xh, const _Float16 *xl, const float *esc,
+                   const float *bias, int m, int n_out, int n_in, bool add);
+
 }  // namespace hako

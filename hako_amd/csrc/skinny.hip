@@ -478,7 +478,7 @@ __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restri
 		g += part[((size_t)sp * 16 + t) * vrows + r];
 		u += part[((size_t)sp * 16 + t) * vrows + F + r];
 	}
-	const float h = g / (1.0f + expf(-g)) * u;
+	const float h = silu(g) * u;
 	float a = __builtin_fabsf(h);
 	a = __builtin_isfinite(a) ? a : 0.0f;
 	a = wave_max(a);
