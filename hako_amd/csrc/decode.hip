@@ -41,7 +41,7 @@ namespace {
 constexpr int kChunk = 64;   // cache positions per attention workgroup
 constexpr int kMaxG = 8;     // query heads per KV head
 constexpr int kArgBlocks = 64;
-constexpr int kDecItems = 2; // row items per wave of the fused GEMV
+constexpr int kDecItems = 4; // row items per wave of the fused GEMV
 
 // ── embedding row (deq_row, reference src/nn.c:55-59) ──
 
@@ -256,12 +256,13 @@ enum { kProQ8 = 0, kProNorm = 1 };
 enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2 };
 
 // Flat grid (as the standalone Q4_K GEMV): a wave owns ITEMS row items of
-// rt rows, every weight load issued at once behind the activation loads.
-// Row space: segments one after the other (Store, Add; a wave never
-// straddles two), or for SwiGLU gate row r = 2r and up row r = 2r+1, so the
-// two sums of a row land in one wave. The activation x (n_in floats) is
-// quantized with the q8_32 scheme in the prologue, after rmsnorm with weight
-// nw for kProNorm.
+// rt rows, every weight load issued at once behind the activation loads, as
+// raw buffer loads from the item's matrix (idle slots read nothing). Row
+// space: segments one after the other (Store, Add; a wave never straddles
+// two), or for SwiGLU 2F rows where a wave's even items are gate rows and
+// its odd items the same up rows, so the two sums of a row meet in
+// neighbouring lanes. The activation x (n_in floats) is quantized with the
+// q8_32 scheme in the prologue, after rmsnorm with weight nw for kProNorm.
 template <int PRO, int EPI, int XP, int ITEMS>
 __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float *__restrict__ x,
                                                       const float *__restrict__ nw, float eps, int n_in,
@@ -272,12 +273,13 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 	float *red_s = xs_s + (n_in >> 5);
 	constexpr int T = 256, WAVES = 4;
 	constexpr int NG = (ITEMS + 3) / 4;
-	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+	static_assert(EPI != kEpiSwiGLU || ITEMS % 2 == 0, "SwiGLU pairs a gate item with the next (up) item");
+	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int NB = n_in >> 8, C = NB * 4;
 	const int seg = next_pow2(C), rt = 64 / seg;
 	const int sub = lane & (seg - 1), rsub = lane / seg;
 	const size_t rb = (size_t)NB * kQ4Bytes;
-	const int wrow0 = (blockIdx.x * WAVES + wave) * ITEMS * rt;
+	const int wrow0 = (blockIdx.x * WAVES + wave) * ITEMS * rt;   // first launch row of the wave
 
 	// this wave's segment (Store / Add)
 	const int si = EPI == kEpiSwiGLU ? 0
@@ -289,19 +291,18 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 	const int srow0 = si == 0 ? segs.s[0].row0 : (si == 1 ? segs.s[1].row0 : segs.s[2].row0);
 	const int srows = si == 0 ? segs.s[0].rows : (si == 1 ? segs.s[1].rows : segs.s[2].rows);
 
-	// item it, this lane: row of its matrix, weight base, validity
+	// item it, this lane: row of its matrix and validity (SwiGLU: item it is
+	// gate (even) or up (odd) row wrow0/2 + rt*(it/2) + rsub)
 	auto item_row = [&](int it) -> int {
-		const int v = wrow0 + rt * it + rsub;
-		return EPI == kEpiSwiGLU ? (v >> 1) : v - srow0;
-	};
-	auto item_w = [&](int it) -> const uint8_t * {
-		if (EPI != kEpiSwiGLU) return sw;
-		return ((wrow0 + rt * it + rsub) & 1) ? segs.s[1].w : segs.s[0].w;
+		return EPI == kEpiSwiGLU ? (wrow0 >> 1) + rt * (it >> 1) + rsub : wrow0 + rt * it + rsub - srow0;
 	};
 	auto item_ok = [&](int it) -> bool {
-		const int v = wrow0 + rt * it + rsub;
-		return v < vrows && item_row(it) < srows;
+		return EPI == kEpiSwiGLU ? item_row(it) < segs.s[0].rows
+		                         : wrow0 + rt * it + rsub < vrows && item_row(it) < srows;
 	};
+	const uint32_t mbytes = (uint32_t)(rb * (EPI == kEpiSwiGLU ? segs.s[0].rows : srows));
+	const __amdgpu_buffer_rsrc_t wra = stream_rsrc(EPI == kEpiSwiGLU ? segs.s[0].w : sw, mbytes);
+	const __amdgpu_buffer_rsrc_t wrb = stream_rsrc(EPI == kEpiSwiGLU ? segs.s[1].w : sw, mbytes);
 
 	// 1. activation (and norm weight) loads, then residual / bias, then weights
 	float4 xv[XP], nv[XP];
@@ -325,10 +326,11 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 #pragma unroll
 	for (int j = 0; j < ITEMS; j++) {
 		const bool on = item_ok(j) && sub < C;
-		const uint8_t *p = item_w(j) + (on ? (size_t)item_row(j) * rb + (size_t)(sub >> 2) * kQ4Bytes : 0);
-		buf[j].h = *(const uint4 *)p;
-		buf[j].q0 = *(const uint4 *)(p + 16 + 32 * (sub & 3));
-		buf[j].q1 = *(const uint4 *)(p + 32 + 32 * (sub & 3));
+		const uint32_t blk = on ? (uint32_t)((size_t)item_row(j) * rb + (size_t)(sub >> 2) * kQ4Bytes) : kBufNone;
+		const __amdgpu_buffer_rsrc_t r = (EPI == kEpiSwiGLU && (j & 1)) ? wrb : wra;
+		buf[j].h = ld_b128(r, blk);
+		buf[j].q0 = ld_b128(r, blk + 16 + 32 * (sub & 3));
+		buf[j].q1 = ld_b128(r, blk + 32 + 32 * (sub & 3));
 		__builtin_amdgcn_sched_barrier(0);
 	}
 
@@ -390,10 +392,9 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		const int j = 4 * g + (sub & 3);
 		const bool writer = (sub >> 2) == 0 && j < ITEMS && item_ok(j);
 		if (EPI == kEpiSwiGLU) {
-			// partner holding the up row: the next segment (rt >= 2) or the next item (rt == 1)
-			const float other = rt >= 2 ? __shfl(tot, lane + seg) : dpp_f<kDppQuadSwap1>(tot);
-			const bool gate = rt >= 2 ? (rsub & 1) == 0 : (j & 1) == 0;
-			if (writer && gate) segs.s[0].out[item_row(j)] = silu(tot) * other;
+			// the up sum of the same row: item j + 1, in the neighbouring lane
+			const float other = dpp_f<kDppQuadSwap1>(tot);
+			if (writer && (j & 1) == 0) segs.s[0].out[item_row(j)] = silu(tot) * other;
 		} else if (writer) {
 			sout[item_row(j)] = EPI == kEpiAdd ? pre[g] + tot : (sbias ? tot + pre[g] : tot);
 		}
@@ -938,6 +939,9 @@ int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, 
 	const int C = n_in / kQK * 4;
 	const int rt = 64 / next_pow2(C);
 	const int rows_wg = 4 * kDecItems * rt;
+	for (int i = 0; i < segs.n; i++)   // weights are read through 32-bit buffer offsets
+		if ((size_t)segs.s[i].rows * (n_in / kQK) * kQ4Bytes >= kBufNone)
+			return set_error(HAKO_GPU_EINVAL, "fused Q4_K GEMV segment of %d x %d exceeds 2 GiB", segs.s[i].rows, n_in);
 	const int wgs = (vrows + rows_wg - 1) / rows_wg;
 	const size_t lds = (size_t)n_in + (size_t)(n_in / 32) * 4 + 16;
 	const int xp = (n_in + 1023) / 1024;
