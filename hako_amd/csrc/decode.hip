@@ -42,6 +42,7 @@ constexpr int kChunk = 64;   // cache positions per attention workgroup
 constexpr int kMaxG = 8;     // query heads per KV head
 constexpr int kArgBlocks = 64;
 constexpr int kDecItems = 4; // row items per wave of the fused GEMV
+constexpr int kDecItemsQkv = 2; // ... of the q/k/v launch (fewer rows: more workgroups)
 
 // ── embedding row (deq_row, reference src/nn.c:55-59) ──
 
@@ -934,11 +935,11 @@ int dalloc(hako_gpu_decoder *d, size_t bytes, void **p) {
 }
 
 // Launch helpers of the fused Q4_K GEMV: XP activation quads per thread.
-template <int PRO, int EPI>
+template <int PRO, int EPI, int IT = kDecItems>
 int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, int n_in, int vrows) {
 	const int C = n_in / kQK * 4;
 	const int rt = 64 / next_pow2(C);
-	const int rows_wg = 4 * kDecItems * rt;
+	const int rows_wg = 4 * IT * rt;
 	for (int i = 0; i < segs.n; i++)   // weights are read through 32-bit buffer offsets
 		if ((size_t)segs.s[i].rows * (n_in / kQK) * kQ4Bytes >= kBufNone)
 			return set_error(HAKO_GPU_EINVAL, "fused Q4_K GEMV segment of %d x %d exceeds 2 GiB", segs.s[i].rows, n_in);
@@ -946,7 +947,7 @@ int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, 
 	const size_t lds = (size_t)n_in + (size_t)(n_in / 32) * 4 + 16;
 	const int xp = (n_in + 1023) / 1024;
 #define HK_DEC(XP) \
-	hipLaunchKernelGGL((q4k_dec_kernel<PRO, EPI, XP, kDecItems>), dim3(wgs), dim3(256), lds, stream(), segs, x, nw, eps, \
+	hipLaunchKernelGGL((q4k_dec_kernel<PRO, EPI, XP, IT>), dim3(wgs), dim3(256), lds, stream(), segs, x, nw, eps, \
 	                   n_in, vrows)
 	if (xp <= 1) HK_DEC(1);
 	else if (xp <= 2) HK_DEC(2);
@@ -957,7 +958,7 @@ int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, 
 }
 
 // rows per wave of the fused GEMV at this n_in (segment starts must be multiples)
-int dec_rows_per_wave(int n_in) { return kDecItems * (64 / next_pow2(n_in / kQK * 4)); }
+int dec_rows_per_wave(int n_in, int items = kDecItems) { return items * (64 / next_pow2(n_in / kQK * 4)); }
 
 bool fusable_q4(int n_in) { return n_in % kQK == 0 && n_in / kQK * 4 <= 64; }
 
@@ -1128,7 +1129,7 @@ int enqueue_step(hako_gpu_decoder *d) {
 		const hako_gpu_block &B = d->blocks[l];
 		float *q = d->qkv, *k = d->qkv + D, *v = d->qkv + D + KV;
 		// 1. q, k, v
-		const int rpw = dec_rows_per_wave(D);
+		const int rpw = dec_rows_per_wave(D, kDecItemsQkv);
 		if (B.t_q == HAKO_TYPE_Q4_K && B.t_k == HAKO_TYPE_Q4_K && B.t_v == HAKO_TYPE_Q4_K && fusable_q4(D) &&
 		    D % rpw == 0 && KV % rpw == 0) {
 			DecSegs s{};
@@ -1136,7 +1137,8 @@ int enqueue_step(hako_gpu_decoder *d) {
 			s.s[0] = {(const uint8_t *)B.wq, B.bq, q, 0, D};
 			s.s[1] = {(const uint8_t *)B.wk, B.bk, k, D, KV};
 			s.s[2] = {(const uint8_t *)B.wv, B.bv, v, D + KV, KV};
-			if (int rc = launch_dec<kProNorm, kEpiStore>(s, d->x, B.attn_norm, m.rms_eps, D, D + 2 * KV)) return rc;
+			if (int rc = launch_dec<kProNorm, kEpiStore, kDecItemsQkv>(s, d->x, B.attn_norm, m.rms_eps, D, D + 2 * KV))
+				return rc;
 		} else {
 			if (int rc = rmsnorm(d->x, B.attn_norm, d->xn, D, m.rms_eps, 1)) return rc;
 			if (int rc = hako_gpu_matmul(q, d->xn, B.t_q, B.wq, B.bq, D, D)) return rc;
@@ -1158,7 +1160,7 @@ int enqueue_step(hako_gpu_decoder *d) {
 				                   (const uint8_t *)B.wo, d->x, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
 				                   D);
 			HK_LAUNCHED("attention merge + o");
-		} else if (B.t_o == HAKO_TYPE_Q4_K && fusable_q4(D) && D % rpw == 0) {
+		} else if (B.t_o == HAKO_TYPE_Q4_K && fusable_q4(D) && D % dec_rows_per_wave(D) == 0) {
 			DecSegs s{};
 			s.n = 1;
 			s.s[0] = {(const uint8_t *)B.wo, nullptr, d->x, 0, D};
