@@ -651,7 +651,7 @@ template <int HD>
 __device__ __forceinline__ float merge_head(const float *__restrict__ grp, int nact, int ht, int lane, int wave,
                                             int hw0, float (*r_s)[4], float *ws) {
 	constexpr int REC = HD + 2, NWH = HD / 64;
-	constexpr int OB = 16;                       // o rows in flight per thread
+	constexpr int OB = 32;                       // o rows in flight per thread
 	constexpr size_t CS = (size_t)kMaxG * REC;   // floats between two chunks' records of one head
 	// one round trip for the common case (nact <= HD chunks): every thread's
 	// (m, l) of chunk ht and its value dim of the first OB chunks, issued together
