@@ -26,6 +26,10 @@ SMALL_128 = mlf2.Qwen2Config(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, 
 # splits a group's heads 2 + 2 + 2 + 1 over four workgroups
 GQA7 = mlf2.Qwen2Config(n_layers=2, d_model=1792, n_heads=14, n_kv_heads=2, head_dim=128, ffn_dim=1536,
                         vocab=2000, ctx=256)
+# the 7-head grouping with ffn_dim 2304: the reference scores positions in its
+# ffn_dim-long gate buffer (src/model.c:125), so positions up to 2300 stay in it
+GQA7_LONG = mlf2.Qwen2Config(n_layers=2, d_model=1792, n_heads=14, n_kv_heads=2, head_dim=128, ffn_dim=2304,
+                             vocab=2000, ctx=4096)
 # one KV head per query head pair with head_dim 64 (two head parts of one head)
 GQA2 = mlf2.Qwen2Config(n_layers=2, d_model=512, n_heads=8, n_kv_heads=4, head_dim=64, ffn_dim=768,
                         vocab=1024, ctx=256)
@@ -67,14 +71,16 @@ def test_greedy_tokens_match_reference(gpu, ref, tmp_path, cfg, seed):
     assert maxabs_rel(np.stack(logits), want_logits) < 2e-2
 
 
-@pytest.mark.parametrize("cfg,seed,pos", [(TINY, 4, 100), (SMALL_128, 5, 300), (GQA7, 6, 250)])
+# position 2200: 35 chunks, more than the merge loads in its first round trip
+@pytest.mark.parametrize("cfg,seed,pos", [(TINY, 4, 100), (SMALL_128, 5, 300), (GQA7, 6, 250),
+                                          (GQA7_LONG, 7, 2200)])
 def test_prefilled_cache_matches_reference(gpu, ref, tmp_path, cfg, seed, pos):
     """KV cache filled with seeded N(0,1) keys and values at 0..pos-1, as the
     decode benchmarks start: the attention spans several 64-position chunks."""
     from dropin import prefilled_greedy
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, seed)
-    max_seq = 512
+    max_seq = max(512, pos + 64)
     kvd = cfg.n_kv_heads * cfg.head_dim
     rng = np.random.default_rng(seed)
     kv = rng.standard_normal((2, cfg.n_layers, pos, kvd)).astype(np.float32)
