@@ -1326,7 +1326,12 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 		// the merge also writes the q8 rows of its output for a fused o
 		int8_t *mxq = f_o ? d->pf_xq : nullptr;
 		float *mxs = f_o ? d->pf_xs : nullptr;
-		const dim3 ag(d->max_chunks, KVH, n), mg(G, KVH, n);
+		// chunks up to the pass's last position (not max_seq's: the rest would exit
+		// at once), rounded up to an odd count: workgroups go to the 8 XCDs in
+		// turn, and an even width would pin a chunk to a few of them (with 8,
+		// chunk c to XCD c, while the causal span gives chunk 0 every token)
+		const int pchunks = ((pos0 + n - 1) / kChunk + 1) | 1;
+		const dim3 ag(pchunks, KVH, n), mg(G, KVH, n);
 		if (HD == 128) {
 			hipLaunchKernelGGL((attn_kernel<128, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
 			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale,
