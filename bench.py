@@ -96,17 +96,19 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
             launch(k)
         g.sync()
         g.record(e0)
-        for k in range(steps):
+        for k in range(warmup, warmup + steps):
             launch(k)
         g.record(e1)
         ms = g.elapsed_ms(e0, e1)
     else:
-        def capture(n):
+        def capture(k0, n):
             g.capture_begin()
-            for k in range(n):
+            for k in range(k0, k0 + n):
                 launch(k)
             return g.capture_end()
-        warm, timed = capture(max(warmup, 1)), capture(steps)
+        # the timed launches start on the weight copy after the warm-up's last,
+        # so none of them finds its weights left in the last-level cache
+        warm, timed = capture(0, max(warmup, 1)), capture(max(warmup, 1), steps)
         g.graph_launch(warm)
         g.sync()
         g.record(e0)
@@ -124,29 +126,119 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
     return {"ms_total": ms, "us_per_launch": ms * 1e3 / steps, "single_launch_us": float(np.median(single)) * 1e3}
 
 
-def cpu_baseline(seconds: float, seed: int) -> dict:
-    """The reference's matmul (src/nn.c:179-210, compiled unmodified with its
-    Makefile flags) on the headline shape, rotating 8 weight copies."""
-    from oracle.hako_oracle import REF_LIB, RefLib
-    threads = min(os.cpu_count() or 1, 16)        # the reference caps at 16 (src/nn.c:61)
-    ref = RefLib(REF_LIB, threads=threads)
-    rng = np.random.default_rng(seed)
-    n_out, n_in = 11008, 2048
-    ws = [synth.q4k_weight(rng, n_out, n_in) for _ in range(8)]
-    x = synth.activation(rng, n_in)
-    for k in range(3):
-        ref.matmul(synth.TYPE_Q4_K, ws[k], x, n_out, n_in)
+def host_info() -> dict:
+    """The host the CPU baselines ran on, and how the reference was compiled."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    compiler = flags = ""
+    try:
+        with open(os.path.join(REPO, "oracle", "_ref", "build_info.txt")) as f:
+            lines = f.read().splitlines()
+        compiler, flags = (lines + ["", ""])[:2]
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": avail, "cpu_count": os.cpu_count(), "compiler": compiler,
+            "flags": flags}
+
+
+MAX_THREADS = 16                  # the reference caps its pool at 16 (src/nn.c:61,104)
+_REF = {}
+
+
+def ref_lib(threads: int):
+    """The reference's own C path (oracle/_ref, compiled unmodified from its
+    sources) with a pool of `threads` threads. Its thread count is read once
+    per loaded copy, at the first matmul (src/nn.c:99-107), so every count gets
+    its own copy of the library, and that first matmul happens here, with
+    n_out >= threads (a smaller first call starts the pool without workers and
+    later calls deadlock, src/nn.c:182-184)."""
+    if threads not in _REF:
+        import shutil
+        import tempfile
+        from oracle.hako_oracle import REF_LIB, RefLib
+        path = os.path.join(tempfile.mkdtemp(prefix="hakm_ref_"), f"libhakm_ref_t{threads}.so")
+        shutil.copy(REF_LIB, path)
+        ref = RefLib(path, threads=threads)
+        rng = np.random.default_rng(0)
+        ref.matmul(synth.TYPE_Q4_K, synth.q4k_weight(rng, 1024, 256), synth.activation(rng, 256), 1024, 256)
+        _REF[threads] = ref
+    return _REF[threads]
+
+
+def cpu_threads() -> int:
+    return min(host_info()["nproc"], MAX_THREADS)
+
+
+def time_ref_matmul(ref, qtype: int, ws: list, x: np.ndarray, n_out: int, n_in: int, seconds: float,
+                    min_calls: int) -> tuple[float, int]:
+    """Median wall time of the reference matmul (src/nn.c:179-210) over
+    rotating weight copies, for `seconds` and at least `min_calls` calls."""
+    ref.matmul(qtype, ws[0], x, n_out, n_in)
     times, t_end, k = [], time.perf_counter() + seconds, 0
-    while time.perf_counter() < t_end or len(times) < 20:
+    while time.perf_counter() < t_end or len(times) < min_calls:
         t0 = time.perf_counter()
-        ref.matmul(synth.TYPE_Q4_K, ws[k % 8], x, n_out, n_in)
+        ref.matmul(qtype, ws[k % len(ws)], x, n_out, n_in)
         times.append(time.perf_counter() - t0)
         k += 1
-    med = float(np.median(times))
-    return {"value": algo_bytes(synth.TYPE_Q4_K, n_out, n_in) / med / 1e9, "unit": "GB/s", "cores": threads,
-            "kind": "reference",
-            "sample": f"{len(times)} calls of the reference matmul on Q4_K 11008x2048 (8 rotating weight "
-                      f"copies), {threads} threads (HAKM_THREADS), median {med * 1e3:.3f} ms/call"}
+    return float(np.median(times)), len(times)
+
+
+def cpu_gemv_baseline(qtype: int, n_out: int, n_in: int, seconds: float, seed: int, copies: int = 8) -> dict:
+    """The reference's matmul on one GEMV shape at T = min(nproc, 16) threads
+    and at T = 1, rotating weight copies."""
+    rng = np.random.default_rng(seed)
+    ws = [synth.weight(rng, qtype, n_out, n_in) for _ in range(copies)]
+    x = synth.activation(rng, n_in)
+    nbytes = algo_bytes(qtype, n_out, n_in)
+    T = cpu_threads()
+    med, calls = time_ref_matmul(ref_lib(T), qtype, ws, x, n_out, n_in, seconds, 20)
+    med1, calls1 = time_ref_matmul(ref_lib(1), qtype, ws, x, n_out, n_in, seconds / 4, 3)
+    name = "Q4_K" if qtype == synth.TYPE_Q4_K else "Q6_K"
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": T, "kind": "reference",
+            "t1_value": round(nbytes / med1 / 1e9, 3),
+            "sample": f"{calls} calls (T={T}) and {calls1} calls (T=1) of the reference matmul on {name} "
+                      f"{n_out}x{n_in} ({copies} rotating weight copies); median {med * 1e3:.3f} ms/call at "
+                      f"T={T}, {med1 * 1e3:.3f} ms/call at T=1",
+            "host": host_info()}
+
+
+def cpu_baseline(seconds: float, seed: int) -> dict:
+    """The reference's matmul (src/nn.c:179-210, compiled unmodified with its
+    Makefile flags) on the headline shape."""
+    return cpu_gemv_baseline(synth.TYPE_Q4_K, 11008, 2048, seconds, seed)
+
+
+def cpu_prefill_baseline(qtype: int, m: int, n_out: int, n_in: int, seed: int) -> dict:
+    """The reference has no multi-token matmul: a prompt is one matmul call
+    per token (cli/main.c:56-60). Times m sequential calls at T = min(nproc,
+    16) over the m activation rows."""
+    rng = np.random.default_rng(seed)
+    w = synth.weight(rng, qtype, n_out, n_in)
+    xs = rng.standard_normal((m, n_in)).astype(np.float32)
+    T = cpu_threads()
+    ref = ref_lib(T)
+    ref.matmul(qtype, w, xs[0], n_out, n_in)
+    t0 = time.perf_counter()
+    for t in range(m):
+        ref.matmul(qtype, w, xs[t], n_out, n_in)
+    sec = time.perf_counter() - t0
+    ops = 2.0 * m * n_out * n_in
+    return {"value": round(ops / sec / 1e12, 4), "unit": "TOPS" if qtype == synth.TYPE_Q4_K else "TFLOP/s",
+            "cores": T, "kind": "reference", "tok_per_s": round(m / sec, 1),
+            "sample": f"{m} sequential calls of the reference matmul ({'Q4_K' if qtype == synth.TYPE_Q4_K else 'Q6_K'}"
+                      f" {n_out}x{n_in}), one per activation row, T={T}: {sec * 1e3:.1f} ms",
+            "host": host_info()}
 
 
 def bench_decode(g, steps: int, cpu_steps: int, seed: int = 30) -> dict:
@@ -194,17 +286,19 @@ def bench_decode(g, steps: int, cpu_steps: int, seed: int = 30) -> dict:
                "hbm_frac": round(per_tok / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                "timing": "HIP graph of one step replayed K times between two HIP events"}
         if cpu_steps > 0:
-            from oracle.hako_oracle import REF_LIB, RefLib, prefilled_greedy
-            threads = min(os.cpu_count() or 1, 16)
-            ref = RefLib(REF_LIB, threads=threads)
-            times = []
-            prefilled_greedy(ref.lib, path, kv, pos, 9, cpu_steps + 1, cfg.vocab, max_seq, times)
+            from oracle.hako_oracle import prefilled_greedy
+            threads = cpu_threads()
+            times, times1 = [], []
+            prefilled_greedy(ref_lib(threads).lib, path, kv, pos, 9, cpu_steps + 1, cfg.vocab, max_seq, times)
+            prefilled_greedy(ref_lib(1).lib, path, kv, pos, 9, 2, cfg.vocab, max_seq, times1)
             med = float(np.median(times[1:]))
             res["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads,
-                                   "kind": "reference",
+                                   "kind": "reference", "t1_value": round(1.0 / times1[1], 3),
                                    "sample": f"{cpu_steps} hakm_forward steps (after one warm-up) of the reference "
                                              f"on the same model file and cache, {threads} threads, median "
-                                             f"{med * 1e3:.1f} ms/token"}
+                                             f"{med * 1e3:.1f} ms/token; one step at T=1: "
+                                             f"{times1[1] * 1e3:.1f} ms",
+                                   "host": host_info()}
         return res
     finally:
         os.unlink(path)
@@ -262,19 +356,19 @@ def bench_decode_batched(g, steps: int, cpu_steps: int, seed: int = 40, n_seq: i
                "hbm_frac": round(per_step / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                "timing": "HIP graph of one 16-sequence step replayed K times between two HIP events"}
         if cpu_steps > 0:
-            from oracle.hako_oracle import REF_LIB, RefLib, prefilled_greedy
-            threads = min(os.cpu_count() or 1, 16)
-            ref = RefLib(REF_LIB, threads=threads)
+            from oracle.hako_oracle import prefilled_greedy
+            threads = cpu_threads()
             times = []
-            prefilled_greedy(ref.lib, path, kv, pos, int(starts[0]), cpu_steps + 1, cfg.vocab, pos + cpu_steps + 2,
-                             times)
+            prefilled_greedy(ref_lib(threads).lib, path, kv, pos, int(starts[0]), cpu_steps + 1, cfg.vocab,
+                             pos + cpu_steps + 2, times)
             med = float(np.median(times[1:]))
             res["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads,
                                    "kind": "reference",
                                    "sample": f"{cpu_steps} hakm_forward steps (after one warm-up) of the reference "
                                              f"on the same model file, one sequence with its cache at position "
                                              f"4095, {threads} threads, median {med * 1e3:.1f} ms/token (the "
-                                             f"reference steps its 16 contexts one after another)"}
+                                             f"reference steps its 16 contexts one after another)",
+                                   "host": host_info()}
         return res
     finally:
         os.unlink(path)
@@ -316,10 +410,8 @@ def bench_prompt(g, n_prompt: int, cpu_tokens: int, seed: int = 50) -> dict:
                "weight_gbps": round(weight_bytes * ((n_prompt + 511) // 512) / sec / 1e9, 1),
                "timing": "host wall clock around the synchronous call, median of 3 after one warm-up"}
         if cpu_tokens > 0:
-            from oracle.hako_oracle import REF_LIB, RefLib
-            threads = min(os.cpu_count() or 1, 16)
-            ref = RefLib(REF_LIB, threads=threads)
-            lib = ref.lib
+            threads = cpu_threads()
+            lib = ref_lib(threads).lib
             ctx = lib.hakm_ctx_new(path.encode(), n_prompt + 8)
             assert ctx
             try:
@@ -335,13 +427,14 @@ def bench_prompt(g, n_prompt: int, cpu_tokens: int, seed: int = 50) -> dict:
                                    "kind": "reference",
                                    "sample": f"the first {cpu_tokens} prompt tokens (after one warm-up) fed with the "
                                              f"reference's hakm_forward on the same model file, {threads} threads, "
-                                             f"median {med * 1e3:.1f} ms/token (its feed is one forward per token)"}
+                                             f"median {med * 1e3:.1f} ms/token (its feed is one forward per token)",
+                                   "host": host_info()}
         return res
     finally:
         os.unlink(path)
 
 
-def bench_prefill(g, launches: int, eager: bool = False) -> dict:
+def bench_prefill(g, launches: int, eager: bool = False, cpu: bool = False) -> dict:
     """The 7B prefill matmuls: Q4_K 18944x3584 x 512 tokens (q8_32 quantize +
     int8-MFMA GEMM) and Q6_K 3584x18944 x 512 tokens (fp16-MFMA GEMM).
     `eager` launches from Python (per-dispatch counter collection)."""
@@ -363,6 +456,8 @@ def bench_prefill(g, launches: int, eager: bool = False) -> dict:
         out[name] = {"us_per_launch": round(r["us_per_launch"], 2), "tops": round(tops, 1),
                      "peak": peak, "frac": round(tops / peak, 4),
                      "unit": "TOPS (int8)" if qt == synth.TYPE_Q4_K else "TFLOP/s (fp16 matrix cores)"}
+        if cpu:
+            out[name]["cpu_baseline"] = cpu_prefill_baseline(qt, m, n_out, n_in, n_out)
     return out
 
 
@@ -450,6 +545,11 @@ def main():
             extra[name] = {"us_per_launch": round(r["us_per_launch"], 3), "gbps": round(r["gbps"], 1),
                            "hbm_frac": round(r["gbps"] / HBM_PEAK_GBPS, 4),
                            "single_launch_us": round(r["single_launch_us"], 3)}
+            if not args.no_cpu:
+                # copies kept to about 1.3 GB of host memory for the vocab shape
+                extra[name]["cpu_baseline"] = cpu_gemv_baseline(qt, n_out, n_in, args.cpu_seconds / 4, seed=n_out,
+                                                                copies=8 if n_out < 100000 else 4)
+                log(f"  cpu: {extra[name]['cpu_baseline']['value']:.2f} GB/s")
     decode = None
     if not args.no_decode:
         decode = bench_decode(g, args.decode_steps, 0 if args.no_cpu else args.cpu_decode_steps)
@@ -469,7 +569,7 @@ def main():
             + (f"; cpu {prompt['cpu_baseline']['value']:.2f} tok/s" if 'cpu_baseline' in prompt else ""))
     prefill = None
     if not args.no_prefill:
-        prefill = bench_prefill(g, 30)
+        prefill = bench_prefill(g, 30, cpu=not args.no_cpu)
         for k, v in prefill.items():
             log(f"{k}: {v['us_per_launch']:.1f} us, {v['tops']:.1f} {v['unit']}")
     cpu = None

@@ -34,7 +34,7 @@
 
 namespace hako {
 
-int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n_out, int n_in, bool acc_out);
+int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n_out, int n_in, const float *res);
 
 namespace {
 
@@ -43,6 +43,23 @@ constexpr int kMaxG = 8;     // query heads per KV head
 constexpr int kArgBlocks = 64;
 constexpr int kDecItems = 4; // row items per wave of the fused GEMV
 constexpr int kDecItemsQkv = 2; // ... of the q/k/v launch (fewer rows: more workgroups)
+
+// One sequence's output projection adds its per-input-block row sums into a
+// residual accumulator of 64-bit fixed-point values (2^-32 units): integer
+// addition is associative, so the sum does not depend on the order in which
+// the blocks arrive and the step is bit-reproducible. |sum| stays below 2^31
+// for any activation a model produces (non-finite or larger sums saturate at
+// +-2^30). The value a block adds is its fp32 sum rounded to the 2^-32 grid;
+// the accumulated sum is converted back to fp32 once.
+constexpr double kFixScale = 4294967296.0;        // 2^32
+constexpr double kFixInv = 1.0 / 4294967296.0;    // 2^-32
+constexpr double kFixMax = 4611686018427387904.0; // 2^62
+__device__ __forceinline__ long long to_fixed(float f) {
+	double v = (double)f * kFixScale;
+	v = __builtin_fmin(__builtin_fmax(v, -kFixMax), kFixMax);   // NaN -> -2^62 (fmax takes the number)
+	return (long long)__builtin_rint(v);
+}
+__device__ __forceinline__ float from_fixed(long long a) { return (float)((double)a * kFixInv); }
 
 // ── embedding row (deq_row, reference src/nn.c:55-59) ──
 
@@ -91,9 +108,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 	for (int i = threadIdx.x; i < n; i += 256) y[(size_t)blockIdx.x * n + i] = xr[i] * scale * w[i];
 }
 
-__global__ __launch_bounds__(256) void add_kernel(float *__restrict__ x, const float *__restrict__ y, int n) {
+// x = a + y (a may be x)
+__global__ __launch_bounds__(256) void add_kernel(float *x, const float *a, const float *__restrict__ y, int n) {
 	const int i = blockIdx.x * 256 + threadIdx.x;
-	if (i < n) x[i] += y[i];
+	if (i < n) x[i] = a[i] + y[i];
 }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ h, const float *__restrict__ g,
@@ -264,10 +282,16 @@ enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2 };
 // its odd items the same up rows, so the two sums of a row meet in
 // neighbouring lanes. The activation x (n_in floats) is quantized with the
 // q8_32 scheme in the prologue, after rmsnorm with weight nw for kProNorm.
-template <int PRO, int EPI, int XP, int ITEMS>
+//
+// OACC: the activation is x plus the fixed-point residual accumulator oacc
+// (the output projection's sums, merge_o_kernel), added in the prologue;
+// workgroup 0 stores that sum to xmid (the residual the down projection adds
+// to) and clears the accumulator oacc_next for the next layer's projection.
+template <int PRO, int EPI, int XP, int ITEMS, bool OACC = false>
 __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float *__restrict__ x,
                                                       const float *__restrict__ nw, float eps, int n_in,
-                                                      int vrows) {
+                                                      int vrows, const long long *__restrict__ oacc,
+                                                      float *__restrict__ xmid, long long *__restrict__ oacc_next) {
 	extern __shared__ __align__(16) uint8_t smem[];
 	int8_t *xq_s = (int8_t *)smem;
 	float *xs_s = (float *)(smem + n_in);
@@ -307,11 +331,16 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 
 	// 1. activation (and norm weight) loads, then residual / bias, then weights
 	float4 xv[XP], nv[XP];
+	uint4 oa[XP][2];
 #pragma unroll
 	for (int k = 0; k < XP; k++) {
 		const int e = min((int)(threadIdx.x + k * T) * 4, n_in - 4);
 		xv[k] = *(const float4 *)(x + e);
 		if (PRO == kProNorm) nv[k] = *(const float4 *)(nw + e);
+		if (OACC) {
+			oa[k][0] = *(const uint4 *)(oacc + e);
+			oa[k][1] = *(const uint4 *)(oacc + e + 2);
+		}
 	}
 	float pre[NG];   // bias (Store) or the residual (Add) of the row this lane writes
 	if (EPI != kEpiSwiGLU) {
@@ -335,7 +364,19 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		__builtin_amdgcn_sched_barrier(0);
 	}
 
-	// 2. prologue: (rmsnorm and) q8_32 quantization into LDS
+	// 2. prologue: (residual accumulator,) (rmsnorm and) q8_32 quantization into LDS
+	if (OACC) {
+		auto fx = [](uint32_t lo, uint32_t hi) -> float {
+			return from_fixed((long long)(((unsigned long long)hi << 32) | lo));
+		};
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			xv[k].x += fx(oa[k][0].x, oa[k][0].y);
+			xv[k].y += fx(oa[k][0].z, oa[k][0].w);
+			xv[k].z += fx(oa[k][1].x, oa[k][1].y);
+			xv[k].w += fx(oa[k][1].z, oa[k][1].w);
+		}
+	}
 	float scale = 1.0f;
 	if (PRO == kProNorm) {
 		float ss = 0.0f;
@@ -369,6 +410,17 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		if (e < n_in) {
 			*(uint32_t *)(xq_s + e) = packed;
 			if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
+		}
+	}
+	if (OACC && blockIdx.x == 0) {
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			const int e = (threadIdx.x + k * T) * 4;
+			if (e < n_in) {
+				*(float4 *)(xmid + e) = xv[k];
+				*(uint4 *)(oacc_next + e) = make_uint4(0u, 0u, 0u, 0u);
+				*(uint4 *)(oacc_next + e + 2) = make_uint4(0u, 0u, 0u, 0u);
+			}
 		}
 	}
 	__syncthreads();
@@ -746,21 +798,20 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
 	}
 }
 
-// One sequence: the merge above, the output projection (Q4_K) and its
-// residual add in one launch. Grid (D/256 input blocks, D/64 row chunks),
-// 256 threads: workgroup (b, rc) merges the 256/HD query heads whose outputs
-// are input block b of the projection (thread t: head 256b/HD + t/HD, dim
-// t % HD, merge_head), quantizes them with q8_32 (a
-// block holds whole 32-blocks, so the codes and scales are those of the full
-// row), and adds block b's terms of q4k_vec_dot (its eight sub-blocks,
-// reference src/quant.c:150-232) for the 64 rows of chunk rc to x with a
-// float atomic add. The D/256 blocks' sums meet in x in the order their
-// atomics arrive: every term is computed as in the two-kernel path, the order
-// of the per-block additions varies from run to run.
+// One sequence: the merge above and the output projection (Q4_K) in one
+// launch. Grid (D/256 input blocks, D/64 row chunks), 256 threads: workgroup
+// (b, rc) merges the 256/HD query heads whose outputs are input block b of
+// the projection (thread t: head 256b/HD + t/HD, dim t % HD, merge_head),
+// quantizes them with q8_32 (a block holds whole 32-blocks, so the codes and
+// scales are those of the full row), and adds block b's terms of q4k_vec_dot
+// (its eight sub-blocks, reference src/quant.c:150-232) for the 64 rows of
+// chunk rc to the fixed-point accumulator oacc (zero before the launch) with
+// an integer atomic add: the D/256 block sums of a row meet in an order-free
+// sum, which the next kernel adds to the residual stream.
 template <int HD>
 __global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ part, const int *__restrict__ posv,
-                                                      const uint8_t *__restrict__ wo, float *__restrict__ x, int H,
-                                                      int KVH, int max_seq, int max_chunks, int D) {
+                                                      const uint8_t *__restrict__ wo, long long *__restrict__ oacc,
+                                                      int H, int KVH, int max_seq, int max_chunks, int D) {
 	__shared__ float w_s[256];
 	__shared__ float r_s[2][4];
 	__shared__ __align__(16) int8_t xq_s[256];
@@ -802,7 +853,21 @@ __global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ 
 	float f = q4_fold(wb, 16u * (g & 1), g >= 2 ? ~0u : 0u, ia, ib, col);
 	f += __shfl_xor(f, 1);
 	f += __shfl_xor(f, 2);
-	if (g == 0 && row < D) unsafeAtomicAdd(x + row, f);
+	if (g == 0 && row < D)
+		__hip_atomic_fetch_add(oacc + row, to_fixed(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// x = a + the fixed-point accumulator oacc, which is then cleared (the
+// merged output projection's residual add when no fused gate/up kernel
+// takes it), and oacc_next cleared for the next layer.
+__global__ __launch_bounds__(256) void oacc_apply_kernel(float *__restrict__ x, long long *__restrict__ oacc,
+                                                         long long *__restrict__ oacc_next, int n) {
+	const int i = blockIdx.x * 256 + threadIdx.x;
+	if (i < n) {
+		x[i] += from_fixed(oacc[i]);
+		oacc[i] = 0;
+		oacc_next[i] = 0;
+	}
 }
 
 // ── greedy pick (reference src/sample.c:28-32) ──
@@ -905,6 +970,11 @@ struct hako_gpu_decoder {
 	      *tmp = nullptr, *logits = nullptr, *part = nullptr, *kc = nullptr, *vc = nullptr;
 	float2 *rope = nullptr, *apart = nullptr;
 	int *tok = nullptr, *pos = nullptr, *ring = nullptr, *nout = nullptr;
+	// one sequence: the output projection's fixed-point residual accumulators
+	// (three: by layer parity, and the last layer of an odd count; then one
+	// scratch row) and the residual after it (x + o)
+	long long *oacc = nullptr;
+	float *xa = nullptr;
 	// batched steps (n_seq > 1): q8 and fp16 hi/lo activations, split-K state
 	int8_t *xq = nullptr;
 	float *xs = nullptr, *esc = nullptr, *escb = nullptr, *skpart = nullptr;
@@ -917,10 +987,13 @@ struct hako_gpu_decoder {
 	float *pf_xs = nullptr, *pf_esc = nullptr;  // fp16 split of the SwiGLU rows: hi, lo [chunk][ffn], esc[chunk]
 	_Float16 *pf_xh = nullptr, *pf_xl = nullptr;
 	int *pf_tok = nullptr, *pf_pos = nullptr;
-	int pf_chunk = 0;   // tokens per prefill pass
+	int pf_chunk = 0;   // most tokens per prefill pass
+	size_t pf_part_bytes = 0;   // capacity of pf_part
 	std::vector<void *> allocs;
 	hipGraphExec_t exec = nullptr;
 	hipGraph_t graph = nullptr;
+	void (*on_destroy)(void *) = nullptr;   // hako_gpu_decoder_on_destroy
+	void *on_destroy_arg = nullptr;
 };
 
 namespace {
@@ -935,8 +1008,10 @@ int dalloc(hako_gpu_decoder *d, size_t bytes, void **p) {
 }
 
 // Launch helpers of the fused Q4_K GEMV: XP activation quads per thread.
+// With oacc the activation is x + oacc (OACC prologue; see q4k_dec_kernel).
 template <int PRO, int EPI, int IT = kDecItems>
-int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, int n_in, int vrows) {
+int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, int n_in, int vrows,
+               const long long *oacc = nullptr, float *xmid = nullptr, long long *oacc_next = nullptr) {
 	const int C = n_in / kQK * 4;
 	const int rt = 64 / next_pow2(C);
 	const int rows_wg = 4 * IT * rt;
@@ -946,12 +1021,24 @@ int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, 
 	const int wgs = (vrows + rows_wg - 1) / rows_wg;
 	const size_t lds = (size_t)n_in + (size_t)(n_in / 32) * 4 + 16;
 	const int xp = (n_in + 1023) / 1024;
-#define HK_DEC(XP) \
-	hipLaunchKernelGGL((q4k_dec_kernel<PRO, EPI, XP, IT>), dim3(wgs), dim3(256), lds, stream(), segs, x, nw, eps, \
-	                   n_in, vrows)
-	if (xp <= 1) HK_DEC(1);
-	else if (xp <= 2) HK_DEC(2);
-	else HK_DEC(4);
+#define HK_DEC(XP, OA) \
+	hipLaunchKernelGGL((q4k_dec_kernel<PRO, EPI, XP, IT, OA>), dim3(wgs), dim3(256), lds, stream(), segs, x, nw, eps, \
+	                   n_in, vrows, oacc, xmid, oacc_next)
+	if constexpr (PRO == kProNorm && EPI == kEpiSwiGLU) {
+		if (oacc) {
+			if (xp <= 1) HK_DEC(1, true);
+			else if (xp <= 2) HK_DEC(2, true);
+			else HK_DEC(4, true);
+			HK_LAUNCHED("q4k_dec");
+			return HAKO_GPU_OK;
+		}
+	}
+	if (oacc) return set_error(HAKO_GPU_EINVAL, "the residual accumulator rides on the gate/up launch");
+	{
+		if (xp <= 1) HK_DEC(1, false);
+		else if (xp <= 2) HK_DEC(2, false);
+		else HK_DEC(4, false);
+	}
 #undef HK_DEC
 	HK_LAUNCHED("q4k_dec");
 	return HAKO_GPU_OK;
@@ -977,8 +1064,9 @@ int rmsnorm_q8_rows(const float *x, const float *w, float eps, int8_t *xq, float
 	return HAKO_GPU_OK;
 }
 
-int add(float *x, const float *y, int n) {
-	hipLaunchKernelGGL(add_kernel, dim3((n + 255) / 256), dim3(256), 0, stream(), x, y, n);
+// x = a + y (a may be x)
+int add(float *x, const float *a, const float *y, int n) {
+	hipLaunchKernelGGL(add_kernel, dim3((n + 255) / 256), dim3(256), 0, stream(), x, a, y, n);
 	HK_LAUNCHED("add");
 	return HAKO_GPU_OK;
 }
@@ -1146,20 +1234,38 @@ int enqueue_step(hako_gpu_decoder *d) {
 			if (int rc = hako_gpu_matmul(v, d->xn, B.t_v, B.wv, B.bv, KV, D)) return rc;
 		}
 		// 2. rope, cache append, attention; 3. output projection + residual
-		// (merged with the attention records in one launch for Q4_K)
+		// (merged with the attention records in one launch for Q4_K, its sums
+		// into the fixed-point accumulator of this layer, taken up by the
+		// gate/up kernel's prologue or by oacc_apply_kernel)
 		const bool merge_o = B.t_o == HAKO_TYPE_Q4_K && D % kQK == 0 && kQK % m.head_dim == 0;
+		const bool fused_gu = B.t_gate == HAKO_TYPE_Q4_K && B.t_up == HAKO_TYPE_Q4_K && fusable_q4(D);
+		// accumulators alternate by layer; with an odd layer count the last
+		// layer takes a third, so that it differs from the next step's layer 0
+		// (one layer: the same one, cleared by a launch of its own below)
+		auto acc_of = [&](int layer) -> long long * {
+			const int i = (m.n_layers & 1) && layer == m.n_layers - 1 && m.n_layers > 1 ? 2 : (layer & 1);
+			return d->oacc + (size_t)i * D;
+		};
+		long long *oacc = acc_of(l);
+		long long *oacc_next = acc_of(l + 1 == m.n_layers ? 0 : l + 1);
+		const bool self_next = oacc_next == oacc;
 		if (int rc = attention(d, l, nullptr, nullptr, !merge_o)) return rc;
 		if (merge_o) {
 			const dim3 grid(D / kQK, (D + 63) / 64);
 			if (m.head_dim == 128)
 				hipLaunchKernelGGL(merge_o_kernel<128>, grid, dim3(256), 0, stream(), d->part, d->pos,
-				                   (const uint8_t *)B.wo, d->x, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
+				                   (const uint8_t *)B.wo, oacc, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
 				                   D);
 			else
 				hipLaunchKernelGGL(merge_o_kernel<64>, grid, dim3(256), 0, stream(), d->part, d->pos,
-				                   (const uint8_t *)B.wo, d->x, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
+				                   (const uint8_t *)B.wo, oacc, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
 				                   D);
 			HK_LAUNCHED("attention merge + o");
+			if (!fused_gu) {
+				hipLaunchKernelGGL(oacc_apply_kernel, dim3((D + 255) / 256), dim3(256), 0, stream(), d->x, oacc,
+				                   oacc_next, D);
+				HK_LAUNCHED("residual accumulator");
+			}
 		} else if (B.t_o == HAKO_TYPE_Q4_K && fusable_q4(D) && D % dec_rows_per_wave(D) == 0) {
 			DecSegs s{};
 			s.n = 1;
@@ -1167,15 +1273,30 @@ int enqueue_step(hako_gpu_decoder *d) {
 			if (int rc = launch_dec<kProQ8, kEpiAdd>(s, d->att, nullptr, 0.0f, D, D)) return rc;
 		} else {
 			if (int rc = hako_gpu_matmul(d->tmp, d->att, B.t_o, B.wo, nullptr, D, D)) return rc;
-			if (int rc = add(d->x, d->tmp, D)) return rc;
+			if (int rc = add(d->x, d->x, d->tmp, D)) return rc;
 		}
-		// 4. gate, up, SwiGLU
-		if (B.t_gate == HAKO_TYPE_Q4_K && B.t_up == HAKO_TYPE_Q4_K && fusable_q4(D)) {
+		// 4. gate, up, SwiGLU (after merge_o: on x + the accumulator, that sum
+		// kept in xa as the residual of step 5)
+		const float *resid = d->x;
+		if (fused_gu) {
 			DecSegs s{};
 			s.n = 2;
 			s.s[0] = {(const uint8_t *)B.gate, nullptr, d->h, 0, F};
 			s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, 0, F};
-			if (int rc = launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)) return rc;
+			if (merge_o) {
+				// (a workgroup must not clear what the others still read)
+				if (int rc = launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F, oacc, d->xa,
+				                                              self_next ? d->oacc + (size_t)3 * D : oacc_next))
+					return rc;
+				if (self_next) {
+					hipLaunchKernelGGL(oacc_apply_kernel, dim3((D + 255) / 256), dim3(256), 0, stream(), d->tmp,
+					                   oacc, oacc, D);
+					HK_LAUNCHED("residual accumulator clear");
+				}
+				resid = d->xa;
+			} else if (int rc = launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)) {
+				return rc;
+			}
 		} else {
 			if (int rc = rmsnorm(d->x, B.ffn_norm, d->xn, D, m.rms_eps, 1)) return rc;
 			if (int rc = hako_gpu_matmul(d->g, d->xn, B.t_gate, B.gate, nullptr, F, D)) return rc;
@@ -1183,12 +1304,12 @@ int enqueue_step(hako_gpu_decoder *d) {
 			hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, stream(), d->h, d->g, d->u, F);
 			HK_LAUNCHED("silu_mul");
 		}
-		// 5. down projection + residual
+		// 5. down projection + residual: x = resid + W h
 		if (B.t_down == HAKO_TYPE_Q6_K) {
-			if (int rc = q6k_gemv(d->x, B.down, d->h, nullptr, D, F, true)) return rc;
+			if (int rc = q6k_gemv(d->x, B.down, d->h, nullptr, D, F, resid)) return rc;
 		} else {
 			if (int rc = hako_gpu_matmul(d->tmp, d->h, B.t_down, B.down, nullptr, D, F)) return rc;
-			if (int rc = add(d->x, d->tmp, D)) return rc;
+			if (int rc = add(d->x, resid, d->tmp, D)) return rc;
 		}
 	}
 	if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, 1)) return rc;
@@ -1237,19 +1358,30 @@ int check_room(hako_gpu_decoder *d, int n) {
 // hakm_forward per prompt token, as passes of up to pf_chunk tokens
 // through the multi-token matmuls ──
 
-// Tokens per pass: 512 (64-token GEMM tiles fill the chip and the weights
-// stream once per 512 tokens), halved while the attention records of a pass
-// (tokens x KV heads x max_seq/64 chunks x heads per KV head) exceed 1 GiB.
+// Tokens per pass: up to 512 (64-token GEMM tiles fill the chip and the
+// weights stream once per 512 tokens), halved while the pass's attention
+// records (tokens x KV heads x the chunks its last position reaches x heads
+// per KV head) exceed the record buffer, at most 1 GiB.
 constexpr int kPrefillMax = 512;
 constexpr size_t kPrefillRecordBytes = (size_t)1 << 30;
+
+// Attention chunks a pass ending at position `last` spans (the grid width and
+// the record stride of its launches): rounded up to an odd count, since
+// workgroups go to the 8 XCDs in turn and an even width would pin a chunk to
+// a few of them (with 8, chunk c to XCD c, while the causal span gives chunk
+// 0 every token).
+int prefill_chunks(int last) { return (last / kChunk + 1) | 1; }
+size_t prefill_rec_bytes(const hako_gpu_model &m, int tokens, int chunks) {
+	return (size_t)tokens * m.n_kv_heads * chunks * kMaxG * (m.head_dim + 2) * 4;
+}
 
 int prefill_alloc(hako_gpu_decoder *d) {
 	if (d->pf_x) return HAKO_GPU_OK;
 	const hako_gpu_model &m = d->m;
-	const size_t rec_per_token = (size_t)4 * m.n_kv_heads * d->max_chunks * kMaxG * (m.head_dim + 2);
-	size_t C = kPrefillMax;
-	while (C > 16 && C * rec_per_token > kPrefillRecordBytes) C /= 2;
+	const size_t C = kPrefillMax;
 	d->pf_chunk = (int)C;
+	size_t rec = prefill_rec_bytes(m, kPrefillMax, prefill_chunks(d->max_seq - 1));
+	d->pf_part_bytes = rec < kPrefillRecordBytes ? rec : kPrefillRecordBytes;
 	const size_t D = m.d_model, F = m.ffn_dim, KV = d->kv_dim;
 	int rc = 0;
 #define HK_ALLOC(ptr, bytes) \
@@ -1263,7 +1395,7 @@ int prefill_alloc(hako_gpu_decoder *d) {
 	HK_ALLOC(d->pf_tmp, 4 * C * D);
 	HK_ALLOC(d->pf_g, 4 * C * F);
 	HK_ALLOC(d->pf_u, 4 * C * F);
-	HK_ALLOC(d->pf_part, C * rec_per_token);
+	HK_ALLOC(d->pf_part, d->pf_part_bytes);
 	HK_ALLOC(d->pf_xq, C * (D > F ? D : F));
 	HK_ALLOC(d->pf_xs, 4 * C * (D > F ? D : F) / 32);
 	HK_ALLOC(d->pf_xh, 2 * C * F);
@@ -1326,26 +1458,24 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 		// the merge also writes the q8 rows of its output for a fused o
 		int8_t *mxq = f_o ? d->pf_xq : nullptr;
 		float *mxs = f_o ? d->pf_xs : nullptr;
-		// chunks up to the pass's last position (not max_seq's: the rest would exit
-		// at once), rounded up to an odd count: workgroups go to the 8 XCDs in
-		// turn, and an even width would pin a chunk to a few of them (with 8,
-		// chunk c to XCD c, while the causal span gives chunk 0 every token)
-		const int pchunks = ((pos0 + n - 1) / kChunk + 1) | 1;
+		// chunks up to the pass's last position (not max_seq's: the rest would
+		// exit at once), also the record stride of the pass
+		const int pchunks = prefill_chunks(pos0 + n - 1);
 		const dim3 ag(pchunks, KVH, n), mg(G, KVH, n);
 		if (HD == 128) {
 			hipLaunchKernelGGL((attn_kernel<128, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
-			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale,
+			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, pchunks, (size_t)0, D, scale,
 			                   1);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
-			                   mxq, mxs, m.n_heads, KVH, d->max_seq, d->max_chunks);
+			                   mxq, mxs, m.n_heads, KVH, d->max_seq, pchunks);
 		} else {
 			hipLaunchKernelGGL((attn_kernel<64, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
-			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, d->max_chunks, (size_t)0, D, scale,
+			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, pchunks, (size_t)0, D, scale,
 			                   1);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
-			                   mxq, mxs, m.n_heads, KVH, d->max_seq, d->max_chunks);
+			                   mxq, mxs, m.n_heads, KVH, d->max_seq, pchunks);
 		}
 		HK_LAUNCHED("attention merge");
 		if (f_o) {
@@ -1355,7 +1485,7 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 			if (int rc = q4k_gemm_segs(s, kSkAdd, d->pf_xq, d->pf_xs, n, D, D)) return rc;
 		} else {
 			if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_att, B.t_o, B.wo, nullptr, n, D, D)) return rc;
-			if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
+			if (int rc = add(d->pf_x, d->pf_x, d->pf_tmp, n * D)) return rc;
 		}
 		if (f_gu) {
 			if (int rc = rmsnorm_q8_rows(d->pf_x, B.ffn_norm, m.rms_eps, d->pf_xq, d->pf_xs, D, n)) return rc;
@@ -1385,7 +1515,7 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 			if (int rc = q4k_gemm_segs(s, kSkAdd, d->pf_xq, d->pf_xs, n, F, D)) return rc;
 		} else {
 			if (int rc = hako_gpu_matmul_batch(d->pf_tmp, d->pf_g, B.t_down, B.down, nullptr, n, D, F)) return rc;
-			if (int rc = add(d->pf_x, d->pf_tmp, n * D)) return rc;
+			if (int rc = add(d->pf_x, d->pf_x, d->pf_tmp, n * D)) return rc;
 		}
 	}
 	return HAKO_GPU_OK;
@@ -1463,6 +1593,8 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	HK_ALLOC(d->pos, sizeof(int) * n_seq);
 	HK_ALLOC(d->ring, sizeof(int) * n_seq * max_seq);
 	HK_ALLOC(d->nout, sizeof(int) * n_seq);
+	HK_ALLOC(d->oacc, sizeof(long long) * 4 * D);   // three accumulators and a scratch row
+	HK_ALLOC(d->xa, sizeof(float) * D);
 	const int DF = F > D ? F : D;
 	// split-K partials of the largest skinny matmul of a step
 	size_t skpart = 0;
@@ -1500,6 +1632,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	if (e == hipSuccess) e = hipMemset(d->vc, 0, sizeof(float) * kvn);
 	if (e == hipSuccess) e = hipMemset(d->pos, 0, sizeof(int) * n_seq);
 	if (e == hipSuccess) e = hipMemset(d->nout, 0, sizeof(int) * n_seq);
+	if (e == hipSuccess) e = hipMemset(d->oacc, 0, sizeof(long long) * 4 * D);
 	if (e == hipSuccess) e = hipDeviceSynchronize();
 	if (e != hipSuccess) {
 		hako_gpu_decoder_destroy(d);
@@ -1515,7 +1648,15 @@ int hako_gpu_decoder_destroy(hako_gpu_decoder *d) {
 	if (d->exec) (void)hipGraphExecDestroy(d->exec);
 	if (d->graph) (void)hipGraphDestroy(d->graph);
 	for (void *p : d->allocs) (void)hipFree(p);
+	if (d->on_destroy) d->on_destroy(d->on_destroy_arg);
 	delete d;
+	return ok();
+}
+
+int hako_gpu_decoder_on_destroy(hako_gpu_decoder *d, void (*fn)(void *), void *arg) {
+	if (!d) return set_error(HAKO_GPU_EINVAL, "null decoder");
+	d->on_destroy = fn;
+	d->on_destroy_arg = fn ? arg : nullptr;
 	return ok();
 }
 
@@ -1580,8 +1721,14 @@ int hako_gpu_decoder_prefill(hako_gpu_decoder *d, int seq, const int *tokens, in
 	if (int rc = prefill_alloc(d)) return rc;
 	const int D = m.d_model;
 	int last = 0;
-	for (int c0 = 0; c0 < n; c0 += d->pf_chunk) {
+	for (int c0 = 0; c0 < n; c0 += last) {
 		last = n - c0 < d->pf_chunk ? n - c0 : d->pf_chunk;
+		// halved while the pass's records exceed the buffer
+		while (last > 1 && prefill_rec_bytes(m, last, prefill_chunks(pos0 + c0 + last - 1)) > d->pf_part_bytes)
+			last /= 2;
+		if (prefill_rec_bytes(m, last, prefill_chunks(pos0 + c0 + last - 1)) > d->pf_part_bytes)
+			return set_error(HAKO_GPU_EINVAL, "attention records of one prompt token at position %d exceed %zu bytes",
+			                 pos0 + c0, d->pf_part_bytes);
 		if (int rc = prefill_chunk(d, seq, tokens + c0, last, pos0 + c0)) return rc;
 	}
 	// logits of the last prompt token (what feed returns), into the

@@ -133,8 +133,9 @@ __host__ __device__ inline Q6Geom q6_geom(int n_in, int target) {
 __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uint8_t *__restrict__ w,
                                                                        const float *__restrict__ x,
                                                                        const float *__restrict__ bias,
-                                                                       float *__restrict__ out, int n_out,
-                                                                       int n_in, int target, int acc_out) {
+                                                                       const float *res,
+                                                                       float *out, int n_out,
+                                                                       int n_in, int target) {
 	extern __shared__ float red_s[];   // [rows of this workgroup][parts]: partial row sums
 	const Q6Geom G = q6_geom(n_in, target);
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -173,7 +174,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 	// the end they would add a round trip after the weight stream.
 	float res0 = 0.0f, bias0 = 0.0f;
 	if (threadIdx.x < nrows) {
-		if (acc_out) res0 = out[r0 + threadIdx.x];
+		if (res) res0 = res[r0 + threadIdx.x];
 		if (bias) bias0 = bias[r0 + threadIdx.x];
 	}
 	// Keep every weight load below the activation loads (completion is in
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 		if (sub < kQ6Depth && base + j < nit && row < r1) {
 			if (G.tpr > 1)
 				red_s[(row - r0) * G.tpr + part] = tot;
-			else if (bias || acc_out)
+			else if (bias || res)
 				red_s[row - r0] = tot;
 			else
 				out[row] = tot;
@@ -221,14 +222,14 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 	}
 	// Rows with a bias or a residual to add, and split rows, finish here: a
 	// load of either inside the loop would wait for every weight load in flight.
-	if (G.tpr > 1 || bias || acc_out) {
+	if (G.tpr > 1 || bias || res) {
 		__syncthreads();
 		for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
 			float v = 0.0f;
 			for (int p = 0; p < G.tpr; p++) v += red_s[r * G.tpr + p];
 			const bool first = r == (int)threadIdx.x;
 			if (bias) v += first ? bias0 : bias[r0 + r];
-			out[r0 + r] = acc_out ? (first ? res0 : out[r0 + r]) + v : v;
+			out[r0 + r] = res ? (first ? res0 : res[r0 + r]) + v : v;
 		}
 	}
 }
@@ -245,8 +246,10 @@ void q6k_set_waves(int v) { g_q6_waves = v >= 8 ? 8 : 4; }
 
 namespace hako {
 
-// out = W x (+ bias), or out += W x (+ bias) when acc_out (a residual add).
-int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n_out, int n_in, bool acc_out) {
+// out = W x (+ bias), or out = res + W x (+ bias) when res is not null (a
+// residual add; res may equal out: each row is read before it is written, by
+// the same thread).
+int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n_out, int n_in, const float *res) {
 	if (int rc = require_device()) return rc;
 	if (n_out <= 0 || n_in <= 0 || n_in % kQK != 0)
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV needs n_out > 0 and n_in %% 256 == 0 (got %d x %d)",
@@ -268,7 +271,7 @@ int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n
 	const int rows_per_wg = (n_out + wgs - 1) / wgs;
 	const size_t lds = (size_t)rows_per_wg * G.tpr * sizeof(float);
 	hipLaunchKernelGGL(q6k_gemv_kernel, dim3(wgs), dim3(G.waves * kWave), lds, stream(), (const uint8_t *)w, x,
-	                   bias, out, n_out, n_in, g_q6_waves, acc_out ? 1 : 0);
+	                   bias, res, out, n_out, n_in, g_q6_waves);
 	HK_LAUNCHED("q6k_gemv");
 	return ok();
 }
@@ -277,5 +280,5 @@ int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n
 
 extern "C" int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, const float *bias,
                                  int n_out, int n_in) {
-	return hako::q6k_gemv(out, w, x, bias, n_out, n_in, false);
+	return hako::q6k_gemv(out, w, x, bias, n_out, n_in, nullptr);
 }

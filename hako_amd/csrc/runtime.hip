@@ -38,6 +38,9 @@ struct State {
 	std::vector<Mirror> mirrors;
 	void *ws[8] = {};
 	size_t ws_bytes[8] = {};
+	// workspaces outgrown by a later call: a graph captured earlier may still
+	// address them, so they live until hako_gpu_shutdown
+	std::vector<void *> ws_retired;
 };
 
 State &st() {
@@ -80,16 +83,19 @@ int workspace(int slot, size_t bytes, void **ptr) {
 	State &s = st();
 	if (slot < 0 || slot >= 8) return set_error(HAKO_GPU_EINVAL, "workspace slot %d", slot);
 	if (s.ws_bytes[slot] < bytes) {
-		// The stream may still read the old buffer.
-		HK_HIP(hipStreamSynchronize(s.stream));
-		if (s.ws[slot]) HK_HIP(hipFree(s.ws[slot]));
-		s.ws[slot] = nullptr;
-		s.ws_bytes[slot] = 0;
+		// Grow by at least half again, so the retired buffers of a slot stay
+		// below twice its size.
 		size_t want = bytes < 4096 ? 4096 : bytes;
-		if (hipMalloc(&s.ws[slot], want) != hipSuccess) {
+		if (want < s.ws_bytes[slot] + s.ws_bytes[slot] / 2) want = s.ws_bytes[slot] + s.ws_bytes[slot] / 2;
+		void *p = nullptr;
+		if (hipMalloc(&p, want) != hipSuccess) {
 			(void)hipGetLastError();
 			return set_error(HAKO_GPU_ENOMEM, "workspace of %zu bytes", want);
 		}
+		// The old buffer is retired, not freed: the stream, or a graph
+		// captured around an earlier call, may still address it.
+		if (s.ws[slot]) s.ws_retired.push_back(s.ws[slot]);
+		s.ws[slot] = p;
 		s.ws_bytes[slot] = want;
 	}
 	*ptr = s.ws[slot];
@@ -135,6 +141,8 @@ int hako_gpu_shutdown(void) {
 		s.ws[i] = nullptr;
 		s.ws_bytes[i] = 0;
 	}
+	for (void *p : s.ws_retired) HK_HIP(hipFree(p));
+	s.ws_retired.clear();
 	HK_HIP(hipStreamDestroy(s.stream));
 	s.stream = nullptr;
 	s.device = -1;

@@ -64,6 +64,7 @@ SIGNATURES = {
     "hako_gpu_decoder_generate": (_i, [_vp, _vp, _i, _vp]),
     "hako_gpu_decoder_replay": (_i, [_vp, _i]),
     "hako_gpu_decoder_prefill": (_i, [_vp, _i, _vp, _i, _vp, _vp]),
+    "hako_gpu_decoder_on_destroy": (_i, [_vp, _vp, _vp]),
 }
 
 

@@ -98,5 +98,15 @@ int hako_decoder_from_model(const hakm_model *m, int n_seq, int max_seq, hako_gp
 	}
 	if (!rc) rc = hako_gpu_decoder_create(&g, n_seq, max_seq, dec);
 	free(blocks);
+	/* the decoder reads the mirror in place: pinned until it is destroyed */
+	if (!rc) rc = hk_model_pin(m, 1);
+	if (!rc) {
+		rc = hako_gpu_decoder_on_destroy(*dec, hk_model_unpin_map, (void *)m->map);
+		if (rc) hk_model_pin(m, -1);
+	}
+	if (rc && *dec) {
+		hako_gpu_decoder_destroy(*dec);
+		*dec = NULL;
+	}
 	return rc;
 }

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "hako_gpu.h"
+#include "hako_mlf2.h"
 
 #pragma GCC visibility push(hidden)
 
@@ -32,5 +33,11 @@ const void *hk_dev_view(const void *p, size_t bytes, size_t align, int slot);
 void hk_die(const char *what) __attribute__((noreturn));
 
 size_t hk_row_nbytes(int type, int n_in);
+
+/* Pin count of model m's mirror entry (+1 / -1): a pinned mirror is never
+ * released, evicted or replaced. 0, or HAKO_GPU_ENOTFOUND without an entry. */
+int hk_model_pin(const hakm_model *m, int delta);
+/* Unpin the entry of the model mapped at `map` (a decoder's destroy hook). */
+void hk_model_unpin_map(void *map);
 
 #pragma GCC visibility pop

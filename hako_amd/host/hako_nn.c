@@ -12,6 +12,7 @@
 #include "hako_quant.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <string.h>
 
 /* ── host elementwise helpers (reference src/nn.c:13-42) ── */
@@ -62,6 +63,7 @@ typedef struct {
 	const unsigned char *data;
 	mlf2_header h;
 	uint64_t sig;
+	int pins;   /* live decoders reading this mirror (hako_decoder_from_model) */
 } model_entry;
 
 #define HK_MAX_MODELS 16
@@ -95,6 +97,13 @@ static void drop_model(int i) {
 	g_models[i] = g_models[--g_nmodels];
 }
 
+/* A pinned mirror is read by a live decoder: it is never dropped. */
+static int refuse_pinned(int i, const char *why) {
+	fprintf(stderr, "hako: model mirror at %p is read by %d live decoder(s): %s refused "
+	        "(destroy the decoders first)\n", g_models[i].map, g_models[i].pins, why);
+	return HAKO_GPU_EINVAL;
+}
+
 /* Lock held. */
 static int upload_locked(const hakm_model *m) {
 	if (!m->map || !m->data) return HAKO_GPU_EINVAL;
@@ -107,6 +116,7 @@ static int upload_locked(const hakm_model *m) {
 		if (e->map_size == m->map_size && e->data == m->data && e->sig == sig &&
 		    memcmp(&e->h, &m->h, sizeof e->h) == 0)
 			return 0;
+		if (e->pins) return refuse_pinned(i, "replacing it with a different model at that address");
 		drop_model(i);
 	}
 	/* an entry whose bytes overlap this live mapping belongs to a model
@@ -115,12 +125,23 @@ static int upload_locked(const hakm_model *m) {
 	for (int k = g_nmodels - 1; k >= 0; k--) {
 		const unsigned char *elo = g_models[k].data;
 		const unsigned char *ehi = (const unsigned char *)g_models[k].map + g_models[k].map_size;
-		if (elo < hi && lo < ehi) drop_model(k);
+		if (elo < hi && lo < ehi) {
+			if (g_models[k].pins) return refuse_pinned(k, "a new mapping over its range");
+			drop_model(k);
+		}
 	}
-	if (g_nmodels == HK_MAX_MODELS) drop_model(0);
+	if (g_nmodels == HK_MAX_MODELS) {   /* evict the oldest unpinned entry */
+		int k = 0;
+		while (k < g_nmodels && g_models[k].pins) k++;
+		if (k == g_nmodels) {
+			fprintf(stderr, "hako: %d model mirrors, all read by live decoders\n", g_nmodels);
+			return HAKO_GPU_ENOMEM;
+		}
+		drop_model(k);
+	}
 	rc = hako_gpu_mirror_upload(m->data, data_extent(m), NULL);
 	if (rc) return rc;
-	g_models[g_nmodels++] = (model_entry){ m->map, m->map_size, m->data, m->h, sig };
+	g_models[g_nmodels++] = (model_entry){ m->map, m->map_size, m->data, m->h, sig, 0 };
 	return 0;
 }
 
@@ -134,9 +155,30 @@ int hako_model_upload(const hakm_model *m) {
 int hako_model_release(const hakm_model *m) {
 	hk_lock();
 	int i = find_model(m);
-	if (i >= 0) drop_model(i);
+	int rc = i >= 0 ? 0 : HAKO_GPU_ENOTFOUND;
+	if (i >= 0 && g_models[i].pins) rc = refuse_pinned(i, "release");
+	else if (i >= 0) drop_model(i);
+	hk_unlock();
+	return rc;
+}
+
+int hk_model_pin(const hakm_model *m, int delta) {
+	hk_lock();
+	int i = find_model(m);
+	if (i >= 0) g_models[i].pins += delta;
 	hk_unlock();
 	return i >= 0 ? 0 : HAKO_GPU_ENOTFOUND;
+}
+
+/* the decoder's destroy hook: arg is the map address of its model entry */
+void hk_model_unpin_map(void *map) {
+	hk_lock();
+	for (int i = 0; i < g_nmodels; i++)
+		if (g_models[i].map == map && g_models[i].pins > 0) {
+			g_models[i].pins--;
+			break;
+		}
+	hk_unlock();
 }
 
 /* Device address of `bytes` at host address p of model m: the model mirror

@@ -59,11 +59,10 @@ typedef struct hako_gpu_decoder hako_gpu_decoder;
  * 1 <= n_seq <= 16. With n_seq > 1 every step advances all sequences
  * together, each matmul streaming its weights once for all of them (the
  * Q4_K_M mix: Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or Q6_K lm_head, and
- * d_model <= 4096); n_seq == 1 takes any F32/F16/Q4_K/Q6_K mix. With
- * n_seq == 1 and a Q4_K output projection, that projection's 256-input
- * blocks are added to the residual with float atomics: the order of those
- * additions, and so the last bits of the activations, may differ between
- * runs (every other sum has a fixed order). */
+ * d_model <= 4096); n_seq == 1 takes any F32/F16/Q4_K/Q6_K mix. Every sum
+ * of a step has a fixed order or is exact (with n_seq == 1 and a Q4_K output
+ * projection its 256-input block sums meet in a 64-bit fixed-point
+ * accumulator on the 2^-32 grid), so steps are bit-reproducible. */
 int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec);
 int hako_gpu_decoder_destroy(hako_gpu_decoder *dec);
 
@@ -102,6 +101,14 @@ int hako_gpu_decoder_prefill(hako_gpu_decoder *dec, int seq, const int *tokens, 
 /* Replays the captured step n times from the current device state (no host
  * transfer, no synchronization): the timed loop of a benchmark. */
 int hako_gpu_decoder_replay(hako_gpu_decoder *dec, int n);
+
+/* Registers fn(arg), run once by hako_gpu_decoder_destroy after the decoder's
+ * work has finished and before its memory is released: a decoder reads its
+ * weights in place, so whoever owns them (e.g. a model mirror) learns here
+ * when they are no longer read. A later call replaces the hook; fn NULL
+ * removes it. No reference counterpart (the reference's forward reads the
+ * mapping it holds, src/model.h:12-26). */
+int hako_gpu_decoder_on_destroy(hako_gpu_decoder *dec, void (*fn)(void *arg), void *arg);
 
 #pragma GCC visibility pop
 

@@ -98,7 +98,12 @@ int hako_gpu_event_destroy(void *ev);
 /* HIP graphs by stream capture: library calls made on this thread between
  * capture_begin and capture_end are recorded, not run; graph_launch replays
  * them on the library stream with one submission. Calls that copy from or to
- * host memory or allocate must stay outside a capture. */
+ * host memory or allocate must stay outside a capture: make one call of each
+ * shape before capturing it, so that the library workspaces it uses exist.
+ * A workspace outgrown by a later, larger call is kept (not freed) until
+ * hako_gpu_shutdown, so a graph captured earlier stays valid; graphs that
+ * run concurrently with each other or with eager calls share the workspaces
+ * and must not overlap in time. */
 int hako_gpu_capture_begin(void);
 int hako_gpu_capture_end(void **graph);
 int hako_gpu_graph_launch(void *graph);

@@ -42,7 +42,9 @@ void deq_row(const hakm_model *m, const mlf2_tensor *w, int r, int n_in, float *
  * Returns 0 or a negative hako_gpu error code. */
 int hako_model_upload(const hakm_model *m);
 /* Forget m's HBM mirror; call before unmapping a model whose address range
- * may be reused by another. */
+ * may be reused by another. Refused (HAKO_GPU_EINVAL, nothing released)
+ * while a decoder made by hako_decoder_from_model from m is alive: destroy
+ * the decoders first. */
 int hako_model_release(const hakm_model *m);
 
 /* A device decoder (hako_decode.h) for mapped model m: the tensors
@@ -51,6 +53,9 @@ int hako_model_release(const hakm_model *m);
  * hako_gpu_decoder_step / _generate call then replaces hakm_forward
  * (src/model.c:93-165) plus the greedy pick for every step. Returns 0 or a
  * negative hako_gpu error code. */
+/* The decoder reads m's mirror in place, so the mirror is pinned until
+ * hako_gpu_decoder_destroy(dec): release, eviction or replacement of it are
+ * refused until then. */
 int hako_decoder_from_model(const hakm_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec);
 
 #ifdef __cplusplus

@@ -212,11 +212,12 @@ assert C.sizeof(HakmCtx) == 344
 
 
 def prefilled_greedy(lib: C.CDLL, path: str, kv: np.ndarray, pos: int, start: int, steps: int, vocab: int,
-                     max_seq: int, times: list | None = None):
+                     max_seq: int, times: list | None = None, release=None):
     """Greedy decode through the reference's model.h API after writing the
     caches directly: kv[0] / kv[1] are [n_layers][pos][kv_dim] keys / values
     placed at positions 0..pos-1, and ctx.pos = pos. `times`, when given,
-    receives the wall time of each hakm_forward call (src/model.c:93)."""
+    receives the wall time of each hakm_forward call (src/model.c:93);
+    `release(ctx)`, when given, runs before hakm_ctx_free unmaps the model."""
     ctx = lib.hakm_ctx_new(path.encode(), max_seq)
     assert ctx, f"hakm_ctx_new({path}) failed"
     toks, logits = [start], []
@@ -236,5 +237,7 @@ def prefilled_greedy(lib: C.CDLL, path: str, kv: np.ndarray, pos: int, start: in
             logits.append(lg)
             toks.append(int(np.argmax(lg)))
     finally:
+        if release is not None:
+            release(ctx)
         lib.hakm_ctx_free(ctx)
     return toks[1:], np.stack(logits)

@@ -25,7 +25,7 @@ REF_ALL   := $(REF)/src/quant.c $(REF)/src/nn.c $(REF)/src/loader.c \
 # exporting the nn.h surface was loaded RTLD_GLOBAL first (the drop-in test).
 REF_MODEL := $(REF)/src/model.c $(REF)/src/loader.c
 
-all: $(OUT)/libhakm_ref.so $(OUT)/libhakm_ref_model.so
+all: $(OUT)/libhakm_ref.so $(OUT)/libhakm_ref_model.so $(OUT)/build_info.txt
 
 $(OUT):
 	mkdir -p $(OUT)
@@ -35,6 +35,10 @@ $(OUT)/libhakm_ref.so: $(REF_ALL) | $(OUT)
 
 $(OUT)/libhakm_ref_model.so: $(REF_MODEL) | $(OUT)
 	$(CC) $(REFFLAGS) -o $@ $(REF_MODEL) $(LDFLAGS)
+
+# compiler and flags of the build, for the CPU-baseline records
+$(OUT)/build_info.txt: $(OUT)/libhakm_ref.so | $(OUT)
+	{ $(CC) --version | head -n 1; echo "$(REFFLAGS)"; } > $@
 
 clean:
 	rm -rf $(OUT)

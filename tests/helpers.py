@@ -8,3 +8,12 @@ def maxabs_rel(got: np.ndarray, want: np.ndarray) -> float:
     want = np.asarray(want, np.float64)
     den = np.max(np.abs(want))
     return float(np.max(np.abs(got - want)) / (den if den > 0 else 1.0))
+
+
+def within(name: str, got: np.ndarray, want: np.ndarray, bar: float) -> float:
+    """Assert maxabs_rel(got, want) < bar, printing the measured value (the
+    bars of whole-model comparisons are set from these measurements)."""
+    err = maxabs_rel(got, want)
+    print(f"[bar] {name}: {err:.3e} (bar {bar:.0e})", flush=True)
+    assert err < bar, f"{name}: {err:.3e} >= {bar:.0e}"
+    return err

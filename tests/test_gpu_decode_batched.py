@@ -5,8 +5,10 @@ that streams the weights once for all of them.
 Each sequence is checked against the reference's own forward
 (src/model.c:93-165, compiled from its sources) run on that sequence alone
 with the same prefilled KV cache and start position: identical greedy tokens,
-logits within 2e-2 of their range (q8 re-quantization of activations that
-differ in the last bit flips single int8 values).
+and logits within a max-abs-normalised bar set per case at most 5x the value
+measured on MI355X (the q8 re-quantization of an activation that differs in
+its last bit can flip one int8 value, which moves logits by up to ~5e-4 of
+their range; the step is bit-reproducible, so each case's value is fixed).
 """
 import ctypes as C
 
@@ -14,7 +16,7 @@ import numpy as np
 import pytest
 
 from hako_amd import mlf2, synth
-from helpers import maxabs_rel
+from helpers import within
 
 pytestmark = pytest.mark.gpu
 
@@ -59,11 +61,14 @@ def seq_setup(cfg, n_seq, seed, max_pos):
     return pos.astype(np.int32), starts.astype(np.int32), kvs
 
 
-@pytest.mark.parametrize("cfg,n_seq,seed,max_seq,max_pos", [(TINY, 4, 1, 256, 200), (TINY, 16, 2, 256, 200),
-                                                             (SMALL_128, 16, 3, 256, 200),
-                                                             (UNTIED_Q4_OUT, 5, 4, 256, 200),
-                                                             (LONG, 6, 5, 2304, 2200)])
-def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, n_seq, seed, max_seq, max_pos):
+# logits bars: measured maxima 4.1e-7, 8.1e-5, 2.3e-5, 4.7e-4, 6.5e-7
+@pytest.mark.parametrize("cfg,n_seq,seed,max_seq,max_pos,bar", [(TINY, 4, 1, 256, 200, 2e-6),
+                                                                 (TINY, 16, 2, 256, 200, 4e-4),
+                                                                 (SMALL_128, 16, 3, 256, 200, 1.1e-4),
+                                                                 (UNTIED_Q4_OUT, 5, 4, 256, 200, 2.3e-3),
+                                                                 (LONG, 6, 5, 2304, 2200, 3.2e-6)])
+def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, n_seq, seed, max_seq, max_pos,
+                                                       bar):
     from dropin import prefilled_greedy
     from hako_amd.decoder import Decoder
     path = str(tmp_path / "m.mlf2")
@@ -88,7 +93,7 @@ def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, 
                                              vocab=cfg.vocab, max_seq=max_seq)
         assert np.all(np.isfinite(want_logits))
         assert got[:, s].tolist() == want, f"sequence {s} (position {pos[s]})"
-        assert maxabs_rel(logits[:, s], want_logits) < 2e-2, f"sequence {s}"
+        within(f"batched logits {cfg.d_model}/{seed} seq {s}", logits[:, s], want_logits, bar)
 
 
 def test_batched_graph_replays_equal_eager_steps(gpu, tmp_path):
@@ -154,33 +159,63 @@ def test_batched_rejects_other_weight_mixes(gpu, tmp_path):
     Decoder(gpu, path, n_seq=1, max_seq=64).close()   # one sequence takes any mix
 
 
-def test_qwen2_7b_sixteen_sequences(gpu, ref, tmp_path):
-    """The full Qwen2-7B shape (28 layers, d_model 3584, 28/4 heads, ffn
-    18944, untied Q6_K output 152064 x 3584) with 16 sequences at their own
-    prefilled positions: every sequence's greedy tokens equal the reference's
-    run of that sequence alone, and its logits are within 2e-3."""
+@pytest.mark.timeout(900)
+def test_qwen2_7b_sixteen_sequences_at_4095(gpu, ref, tmp_path):
+    """The decode benchmark's workload: the full Qwen2-7B shape (28 layers,
+    d_model 3584, 28/4 heads, ffn 18944, untied Q6_K output 152064 x 3584)
+    with 16 sequences, each with its own seeded N(0,1) cache of 4095
+    positions (64 attention chunks of 7 query heads per KV head at head_dim
+    128), stepped together three times. Every sequence's greedy tokens and
+    logits equal the reference's forward (src/model.c:93-165) run on that
+    sequence alone with the same cache; the captured step gives the eager
+    steps' tokens. Each sequence's cache is regenerated from its seed when
+    it is needed, so host memory holds one at a time."""
+    import time
     from dropin import prefilled_greedy
     from hako_amd.decoder import Decoder
     cfg = mlf2.QWEN2_7B
     path = str(tmp_path / "qwen2_7b.mlf2")
     mlf2.write_qwen2(path, cfg, 41)
-    n_seq, max_seq, steps = 16, 160, 3
-    pos, starts, kvs = seq_setup(cfg, n_seq, 41, 120)
+    n_seq, pos, steps = 16, 4095, 3
+    max_seq = pos + steps + 1
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    starts = np.random.default_rng(41).choice(cfg.vocab, n_seq, replace=False).astype(np.int32)
+
+    def cache(s):
+        return np.random.default_rng(1000 + s).standard_normal((2, cfg.n_layers, pos, kvd), dtype=np.float32)
+
+    t0 = time.time()
     dec = Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
     try:
-        fill_kv(gpu, dec, kvs, cfg.n_layers)
+        for s in range(n_seq):
+            kv = cache(s)
+            k, v = dec.kv()
+            for l in range(cfg.n_layers):
+                gpu.h2d(k + dec.kv_offset(s, l, 0), np.ascontiguousarray(kv[0, l]))
+                gpu.h2d(v + dec.kv_offset(s, l, 0), np.ascontiguousarray(kv[1, l]))
+            del kv
+        print(f"caches filled in {time.time() - t0:.0f} s", flush=True)
         dec.set_pos(pos)
-        first, lg = dec.step(starts, logits=True)
-        rest = dec.generate(first, steps - 1)
+        toks, got, logits = starts.copy(), [], []
+        for _ in range(steps):
+            toks, lg = dec.step(toks, logits=True)
+            assert np.array_equal(toks, np.argmax(lg, axis=1))
+            got.append(toks.copy())
+            logits.append(lg)
+        dec.set_pos(pos)
+        replayed = dec.generate(starts, steps)
     finally:
         dec.close()
-    got = np.concatenate([first[None], rest])
+    got, logits = np.stack(got), np.stack(logits)
+    assert np.array_equal(replayed, got)
     for s in range(n_seq):
-        want, want_logits = prefilled_greedy(ref, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=steps,
+        want, want_logits = prefilled_greedy(ref, path, cache(s), pos, start=int(starts[s]), steps=steps,
                                              vocab=cfg.vocab, max_seq=max_seq)
         assert np.all(np.isfinite(want_logits))
-        assert got[:, s].tolist() == want, f"sequence {s} (position {pos[s]})"
-        assert maxabs_rel(lg[s], want_logits[0]) < 2e-3, f"sequence {s}"
+        assert got[:, s].tolist() == want, f"sequence {s}"
+        # measured 1.8e-6 .. 1.2e-5 over the 16 sequences
+        within(f"7B x16 at 4095 logits seq {s}", logits[:, s], want_logits, 5.5e-5)
+        print(f"sequence {s} checked at {time.time() - t0:.0f} s", flush=True)
 
 
 def test_batched_sequences_reach_max_seq(gpu, ref, tmp_path):
@@ -212,4 +247,5 @@ def test_batched_sequences_reach_max_seq(gpu, ref, tmp_path):
         want, want_lg = prefilled_greedy(ref, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=1,
                                          vocab=cfg.vocab, max_seq=max_seq)
         assert int(toks[s]) == want[0]
-        assert maxabs_rel(lg[s], want_lg[0]) < 2e-2
+        # measured 1.9e-7, 8.0e-5, 5.6e-7
+        within(f"batched max_seq logits seq {s}", lg[s], want_lg[0], 4e-4)

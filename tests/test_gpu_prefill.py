@@ -2,10 +2,12 @@
 reference's feed (src/hakm_api.c:105-111: one hakm_forward per prompt token,
 src/model.c:93-165, compiled from its sources) followed by greedy decoding.
 
-Bars: the KV cache rows the prompt writes, and the last prompt token's
-logits, within 2e-2 of their range (q8 re-quantization of activations that
-differ in the last bit flips single int8 values); the greedy tokens after
-the prompt identical.
+Bars: the greedy tokens after the prompt identical; the KV cache rows the
+prompt writes and the last prompt token's logits within a max-abs-normalised
+bar set per case at most 5x the value measured on MI355X (logits 2e-7 ..
+4e-6; cache rows of the deeper layer up to 1e-3, where the q8
+re-quantization of an activation that differs in its last bit flips one int8
+value of a row).
 """
 import ctypes as C
 
@@ -13,7 +15,7 @@ import numpy as np
 import pytest
 
 from hako_amd import mlf2, synth
-from helpers import maxabs_rel
+from helpers import within
 
 pytestmark = pytest.mark.gpu
 
@@ -63,25 +65,40 @@ class RefSeq:
             lg = self.forward(out[-1])
         return out
 
-    def kv(self, upto):
+    def fill(self, kv, pos):
+        """Write kv[0] / kv[1] ([n_layers][pos][kv_dim]) at positions 0..pos-1 and set the position."""
         kvd = self.cfg.n_kv_heads * self.cfg.head_dim
         shape = (self.cfg.n_layers, self.max_seq, kvd)
-        k = np.ctypeslib.as_array(C.cast(self.c.k_cache, C.POINTER(C.c_float)), shape=shape)[:, :upto].copy()
-        v = np.ctypeslib.as_array(C.cast(self.c.v_cache, C.POINTER(C.c_float)), shape=shape)[:, :upto].copy()
+        for which, ptr in ((0, self.c.k_cache), (1, self.c.v_cache)):
+            np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_float)), shape=shape)[:, :pos] = kv[which]
+        self.c.pos = pos
+
+    def kv(self, upto, start=0):
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        shape = (self.cfg.n_layers, self.max_seq, kvd)
+        k = np.ctypeslib.as_array(C.cast(self.c.k_cache, C.POINTER(C.c_float)), shape=shape)[:, start:upto].copy()
+        v = np.ctypeslib.as_array(C.cast(self.c.v_cache, C.POINTER(C.c_float)), shape=shape)[:, start:upto].copy()
         return k, v
 
     def close(self):
         self.lib.hakm_ctx_free(self.ctx)
 
 
-def device_kv(gpu, dec, seq, upto):
+def device_kv(gpu, dec, seq, upto, start=0):
     k, v = dec.kv()
     kvd = dec.kv_dim
     out = []
     for base in (k, v):
-        out.append(np.stack([gpu.download(base + dec.kv_offset(seq, l, 0), np.float32, (upto, kvd))
+        out.append(np.stack([gpu.download(base + dec.kv_offset(seq, l, start), np.float32, (upto - start, kvd))
                              for l in range(dec.cfg["n_layers"])]))
     return out
+
+
+def fill_device_kv(gpu, dec, seq, kv, pos):
+    k, v = dec.kv()
+    for l in range(dec.cfg["n_layers"]):
+        gpu.h2d(k + dec.kv_offset(seq, l, 0), np.ascontiguousarray(kv[0, l, :pos]))
+        gpu.h2d(v + dec.kv_offset(seq, l, 0), np.ascontiguousarray(kv[1, l, :pos]))
 
 
 def make(gpu, path, n_seq, max_seq):
@@ -97,36 +114,54 @@ TINY_LONG = mlf2.Qwen2Config(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, h
                              vocab=1024, ctx=40000)
 
 
-# (cfg, seed, prompt length, max_seq): 600 tokens cross a 512-token pass;
-# max_seq 40000 makes the pass 256 tokens (records capped at 1 GiB), which
-# 300 tokens cross
-@pytest.mark.parametrize("cfg,seed,n_prompt,max_seq", [(TINY, 1, 37, 384), (TINY_UNTIED, 2, 50, 384),
-                                                       (SMALL_128, 3, 140, 384), (DENSE, 4, 21, 384),
-                                                       (TINY_LONG, 5, 600, 640), (TINY, 6, 300, 40000)])
-def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt, max_seq):
+# ffn_dim 40192 >= 40000 positions: a prompt fed at position 39000 of a
+# 40000-position context (the reference scores in its gate buffer)
+LONG_FFN = mlf2.Qwen2Config(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=40192,
+                            vocab=512, ctx=40000)
+
+
+# (cfg, seed, prompt length, max_seq, start position, K/V bar, logits bar):
+# 600 tokens cross a 512-token pass. The pass's attention records are sized
+# by the positions it reaches: from position 0 with max_seq 40000, 300 tokens
+# are one pass; from position 39000 a 512-token pass would need 1.3 GB of
+# records (more than the 1 GiB buffer), so the 600 tokens go as 256 + 256 +
+# 88. Measured K/V: 2.7e-7, 3.0e-7, 7.5e-5, 2.4e-7, 1.1e-3, 4.4e-4; logits
+# 4.6e-7, 5.1e-7, 6.0e-7, 3.5e-7, 2.6e-7, 4.2e-7.
+@pytest.mark.parametrize("cfg,seed,n_prompt,max_seq,pos0,kv_bar,lg_bar", [
+    (TINY, 1, 37, 384, 0, 1.4e-6, 2.3e-6), (TINY_UNTIED, 2, 50, 384, 0, 1.5e-6, 2.6e-6),
+    (SMALL_128, 3, 140, 384, 0, 3.8e-4, 3e-6), (DENSE, 4, 21, 384, 0, 1.2e-6, 1.8e-6),
+    (TINY_LONG, 5, 600, 640, 0, 5.3e-3, 1.3e-6), (TINY, 6, 300, 40000, 0, 2.2e-3, 2.1e-6),
+    (LONG_FFN, 12, 600, 40000, 39000, 2e-2, 2e-2)])
+def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt, max_seq, pos0, kv_bar, lg_bar):
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, seed)
     steps = 8
-    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    kv = rng.standard_normal((2, cfg.n_layers, pos0, kvd), dtype=np.float32)
+    end = pos0 + n_prompt
     r = RefSeq(ref, path, max_seq, cfg)
     try:
+        r.fill(kv, pos0)
         want_lg = r.feed(prompt)
-        want_k, want_v = r.kv(n_prompt)
+        want_k, want_v = r.kv(end, pos0)
         want = r.greedy(want_lg, steps)
     finally:
         r.close()
     dec = make(gpu, path, 1, max_seq)
     try:
-        dec.set_pos(0)
+        fill_device_kv(gpu, dec, 0, kv, pos0)
+        dec.set_pos(pos0)
         first, lg = dec.prefill(prompt, logits=True)
-        got_k, got_v = device_kv(gpu, dec, 0, n_prompt)
+        got_k, got_v = device_kv(gpu, dec, 0, end, pos0)
         got = [first] + dec.generate(first, steps - 1)[:, 0].tolist()
     finally:
         dec.close()
     assert first == int(np.argmax(lg))
-    assert maxabs_rel(got_k, want_k) < 2e-2
-    assert maxabs_rel(got_v, want_v) < 2e-2
-    assert maxabs_rel(lg, want_lg) < 2e-2
+    within(f"prefill K {cfg.d_model}/{n_prompt}/{max_seq}/{pos0}", got_k, want_k, kv_bar)
+    within(f"prefill V {cfg.d_model}/{n_prompt}/{max_seq}/{pos0}", got_v, want_v, kv_bar)
+    within(f"prefill logits {cfg.d_model}/{n_prompt}/{max_seq}/{pos0}", lg, want_lg, lg_bar)
     assert got == want
 
 
@@ -207,7 +242,7 @@ def test_prefill_qwen2_3b_prompt(gpu, ref, tmp_path):
         got = [first] + dec.generate(first, 2)[:, 0].tolist()
     finally:
         dec.close()
-    assert maxabs_rel(lg, want_lg) < 2e-3
+    within("prefill 3B logits", lg, want_lg, 1.7e-5)   # measured 3.5e-6
     assert got == want
 
 
@@ -244,7 +279,8 @@ def test_prefill_of_one_token_equals_a_step(gpu, tmp_path):
         _, b = dec.step(t, logits=True)
     finally:
         dec.close()
-    assert maxabs_rel(a, b[0]) < 2e-3
+    # the pass's single-token matmuls against the step's fused kernels: measured 4.2e-7
+    within("one-token prefill vs step logits", a, b[0], 2e-6)
 
 
 def test_prefill_fills_the_cache_to_max_seq(gpu, ref, tmp_path):
@@ -269,4 +305,4 @@ def test_prefill_fills_the_cache_to_max_seq(gpu, ref, tmp_path):
             dec.step(1)
     finally:
         dec.close()
-    assert maxabs_rel(lg, want_lg) < 2e-2
+    within("prefill to max_seq logits", lg, want_lg, 1.6e-6)   # measured 3.2e-7
