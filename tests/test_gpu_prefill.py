@@ -114,24 +114,26 @@ TINY_LONG = mlf2.Qwen2Config(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, h
                              vocab=1024, ctx=40000)
 
 
-# ffn_dim 40192 >= 40000 positions: a prompt fed at position 39000 of a
-# 40000-position context (the reference scores in its gate buffer)
-LONG_FFN = mlf2.Qwen2Config(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=40192,
-                            vocab=512, ctx=40000)
+# a prompt fed at position 9000 of a 10000-position context: four KV heads of
+# head_dim 128 make a 512-token pass's attention records 1.3 GB there (more
+# than the 1 GiB record buffer); ffn_dim 9728 covers the positions (the
+# reference scores in its gate buffer)
+LONG_CTX = mlf2.Qwen2Config(n_layers=1, d_model=512, n_heads=4, n_kv_heads=4, head_dim=128, ffn_dim=9728,
+                            vocab=512, ctx=10000)
 
 
 # (cfg, seed, prompt length, max_seq, start position, K/V bar, logits bar):
 # 600 tokens cross a 512-token pass. The pass's attention records are sized
 # by the positions it reaches: from position 0 with max_seq 40000, 300 tokens
-# are one pass; from position 39000 a 512-token pass would need 1.3 GB of
-# records (more than the 1 GiB buffer), so the 600 tokens go as 256 + 256 +
-# 88. Measured K/V: 2.7e-7, 3.0e-7, 7.5e-5, 2.4e-7, 1.1e-3, 4.4e-4; logits
-# 4.6e-7, 5.1e-7, 6.0e-7, 3.5e-7, 2.6e-7, 4.2e-7.
+# are one pass; from position 9000 of LONG_CTX a 512-token pass would need
+# 1.3 GB of records (more than the 1 GiB buffer), so the 600 tokens go as
+# 256 + 256 + 88. Measured K/V: 2.7e-7, 3.0e-7, 7.5e-5, 2.4e-7, 1.1e-3, 4.4e-4,
+# 3.2e-7; logits 4.6e-7, 5.1e-7, 6.0e-7, 3.5e-7, 2.6e-7, 4.2e-7, 5.8e-7.
 @pytest.mark.parametrize("cfg,seed,n_prompt,max_seq,pos0,kv_bar,lg_bar", [
     (TINY, 1, 37, 384, 0, 1.4e-6, 2.3e-6), (TINY_UNTIED, 2, 50, 384, 0, 1.5e-6, 2.6e-6),
     (SMALL_128, 3, 140, 384, 0, 3.8e-4, 3e-6), (DENSE, 4, 21, 384, 0, 1.2e-6, 1.8e-6),
     (TINY_LONG, 5, 600, 640, 0, 5.3e-3, 1.3e-6), (TINY, 6, 300, 40000, 0, 2.2e-3, 2.1e-6),
-    (LONG_FFN, 12, 600, 40000, 39000, 2e-2, 2e-2)])
+    (LONG_CTX, 12, 600, 10000, 9000, 1.6e-6, 2.9e-6)])
 def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt, max_seq, pos0, kv_bar, lg_bar):
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, seed)
