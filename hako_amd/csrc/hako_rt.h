@@ -32,6 +32,9 @@ void q4k_skinny_set_target_wgs(int wgs);
 void q6k_skinny_set_target_wgs(int wgs);
 // Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
 int workspace(int slot, size_t bytes, void **ptr);
+// Look up this device's address of the no-allocation scratch array (with
+// the device current; once per device).
+int noalloc_setup(int device);
 
 }  // namespace hako
 

@@ -124,6 +124,7 @@ int hako_gpu_init(int device) {
 	if (strncmp(s.prop.gcnArchName, "gfx950", 6) != 0)
 		return set_error(HAKO_GPU_ENODEV, "device %d is %s; this library is built for gfx950",
 		                 device, s.prop.gcnArchName);
+	if (int rc = noalloc_setup(device)) return rc;
 	HK_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
 	s.device = device;
 	return ok();

@@ -56,6 +56,7 @@ SIGNATURES = {
     "hako_gpu_q4k_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
     "hako_gpu_q6k_gemm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "hako_gpu_matmul_batch": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _i]),
+    "hako_gpu_matmul_batch_noalloc": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _i]),
     "hako_gpu_decoder_create": (_i, [_vp, _i, _i, C.POINTER(_vp)]),
     "hako_gpu_decoder_destroy": (_i, [_vp]),
     "hako_gpu_decoder_kv": (_i, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),

@@ -182,6 +182,19 @@ int hako_gpu_q6k_gemm(float *y, const void *w, const float *x, const float *bias
 int hako_gpu_matmul_batch(float *y, const float *x, int type, const void *w,
                           const float *bias, int m, int n_out, int n_in);
 
+/* hako_gpu_matmul_batch that allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results (bit for bit) as hako_gpu_matmul_batch;
+ * its scratch (activation rows in q8_32 or fp16 hi/lo form, split-K partials)
+ * is a 48 MiB array that each device holds until the process ends, enough
+ * for 512 tokens x 18944 inputs of either type. A call that needs more is
+ * refused with HAKO_GPU_EINVAL and a message. Calls on one device share the
+ * array: calls that overlap in time on one device (several streams, or
+ * graphs replayed concurrently) race. */
+int hako_gpu_matmul_batch_noalloc(float *y, const float *x, int type, const void *w,
+                                  const float *bias, int m, int n_out, int n_in);
+
 /* matmul (reference src/nn.c:179-210) on device pointers: out[n_out] =
  * W x (+bias) for a weight of any supported type. For Q4_K the activation is
  * quantized with the q8_32 scheme inside the GEMV's workgroups (in LDS), so
