@@ -234,13 +234,128 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 	}
 }
 
+// Flat grid: every weight load of a wave issued at once, right after the
+// activation (and bias / residual) loads, as the Q4_K flat GEMV does; latency
+// is hidden by the many workgroups resident on each CU instead of a software
+// pipeline. Rows of C <= 64 chunks: a workgroup of 4 waves, a wave owns ITEMS
+// consecutive row tiles of rt = 64/seg rows. Wider rows: a workgroup of P =
+// ceil(C/64) waves, wave p the chunks [64p, 64p + 64) of ITEMS consecutive
+// rows; the P partial sums of a row meet in LDS.
+template <int ITEMS>
+__global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(const uint8_t *__restrict__ w,
+                                                                            const float *__restrict__ x,
+                                                                            const float *__restrict__ bias,
+                                                                            const float *res, float *out,
+                                                                            int n_out, int n_in) {
+	constexpr int NG = (ITEMS + 3) / 4;   // groups of four items reduced together
+	__shared__ float red_s[kQ6MaxWaves][4 * NG];
+	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int NB = n_in >> 8, C = NB * 8;
+	const bool wide = C > 64;
+	const int seg = wide ? 64 : next_pow2(C), rt = 64 / seg;
+	const int sub = lane & (seg - 1), rsub = lane / seg;
+	const int part = wide ? wave : 0;
+	const int c = 64 * part + sub;
+	const bool lane_on = c < C;
+	// first row of this wave's items; a wide workgroup's waves share rows
+	const int wrow0 = wide ? blockIdx.x * ITEMS : (blockIdx.x * 4 + wave) * ITEMS * rt;
+	auto item_row = [&](int it) -> int { return wide ? wrow0 + it : wrow0 + rt * it + rsub; };
+	const size_t rb = (size_t)NB * kQ6Bytes;
+
+	const int cc = min(c, C - 1);
+	const int i = cc >> 3, s = cc & 7, hn = s >> 2, kp = (s >> 1) & 1, lh = s & 1, sel = 2 * kp + lh;
+
+	// 1. activation, then bias / residual of the row this lane writes
+	Q6Col col;
+	q6_col_load(x, cc, col);
+	float rv[NG], bv[NG];
+#pragma unroll
+	for (int g = 0; g < NG; g++) {
+		const int r = min(item_row(4 * g + (sub & 3)), n_out - 1);
+		rv[g] = res ? res[r] : 0.0f;
+		bv[g] = bias ? bias[r] : 0.0f;
+	}
+	// out = res + (sum + bias), the persistent kernel's order of additions
+	auto finish = [&](float v, int g) -> float {
+		v = bias ? v + bv[g] : v;
+		return res ? rv[g] + v : v;
+	};
+	__builtin_amdgcn_sched_barrier(0);
+	// 2. every weight load of the wave, in consumption order
+	const __amdgpu_buffer_rsrc_t wr = stream_rsrc(w, (uint32_t)(rb * n_out));
+	Q6Buf buf[ITEMS];
+#pragma unroll
+	for (int j = 0; j < ITEMS; j++) {
+		const int row = item_row(j);
+		const bool on = row < n_out && lane_on;
+		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + (size_t)i * kQ6Bytes) : kBufNone;
+		buf[j].ql = ld_b128(wr, blk + 64 * hn + 32 * kp + 16 * lh);
+		buf[j].qh = ld_b128(wr, blk + 128 + 32 * hn + 16 * lh);
+		buf[j].s = ld_b64(wr, blk + 192 + 8 * hn);
+		buf[j].d = ld_b16(wr, blk + 208);
+		__builtin_amdgcn_sched_barrier(0);
+	}
+	q6_col_sums(col);   // waits for x only: it was loaded first
+
+	// 3. the row sums
+	float rsum[4 * NG];
+#pragma unroll
+	for (int j = 0; j < 4 * NG; j++) {
+		rsum[j] = 0.0f;
+		if (j >= ITEMS) continue;
+		const float d = q6_dot(buf[j], col, kp, sel);
+		rsum[j] = (lane_on && item_row(j) < n_out) ? d : 0.0f;
+	}
+	// 4. lane sub = j (< 4) of each segment holds item 4g + j
+	if (!wide) {
+#pragma unroll
+		for (int g = 0; g < NG; g++) {
+			const float tot = seg_sum4(rsum + 4 * g, seg, lane);
+			const int j = 4 * g + (sub & 3);
+			const int row = item_row(j);
+			if ((sub >> 2) == 0 && j < ITEMS && row < n_out) out[row] = finish(tot, g);
+		}
+		return;
+	}
+#pragma unroll
+	for (int g = 0; g < NG; g++) {
+		const float tot = seg_sum4(rsum + 4 * g, 64, lane);
+		if (lane < 4) red_s[part][4 * g + lane] = tot;
+	}
+	__syncthreads();
+	if (wave == 0 && lane < 4 * NG && lane < ITEMS) {
+		const int row = wrow0 + lane;
+		if (row < n_out) {
+			float v = 0.0f;
+			for (int p = 0; p < (int)(blockDim.x >> 6); p++) v += red_s[p][lane];
+			out[row] = finish(v, lane >> 2);
+		}
+	}
+}
+
 int g_q6_wgs_per_cu = 1;
 int g_q6_waves = 4;
+// -1: by shape (below); 0: persistent grid; 1, 2, 4, 8: flat grid with that many items per wave
+int g_q6_flat_items = -1;
+
+// Measured on MI355X (us per launch, persistent / flat with 1, 2, 4 items):
+// 2048x11008 9.18 / 12.0 / 9.38 / 8.06; 1000x4608 4.76 / 4.45 / 4.15 / 3.91;
+// 256x2048 3.75 / 2.99 / 3.38 / 3.92; 151936x2048 65.8 / 104 / 78.8 / 68.4;
+// 3584x18944 19.2 / 30.0 / 27.1 / 21.9. Rows of 2..6 parts take the flat grid
+// with 4 items; short matrices of one part the flat grid with one item;
+// wider rows and tall matrices the persistent grid.
+int q6_flat_items_for(int n_out, const Q6Geom &G) {
+	if (g_q6_flat_items >= 0) return g_q6_flat_items;
+	if (G.C > 64 && G.tpr <= 6) return 4;
+	if (G.C <= 64 && n_out <= 4096) return 1;
+	return 0;
+}
 
 }  // namespace
 
 void q6k_set_wgs_per_cu(int v) { g_q6_wgs_per_cu = v < 1 ? 1 : (v > 8 ? 8 : v); }
 void q6k_set_waves(int v) { g_q6_waves = v >= 8 ? 8 : 4; }
+void q6k_set_flat_items(int v) { g_q6_flat_items = v < 0 ? -1 : (v == 0 ? 0 : (v <= 1 ? 1 : (v <= 2 ? 2 : (v <= 4 ? 4 : 8)))); }
 
 }  // namespace hako
 
@@ -259,8 +374,24 @@ int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n
 	const Q6Geom G = q6_geom(n_in, g_q6_waves);
 	if ((size_t)n_out * (n_in / kQK) * kQ6Bytes >= kBufNone)
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV weight of %d x %d exceeds 2 GiB", n_out, n_in);
-	if (G.waves > kQ6MaxWaves)
+	if (G.waves > kQ6MaxWaves || G.tpr > kQ6MaxWaves)
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV n_in %d exceeds %d", n_in, kQ6MaxWaves * 64 * 32);
+	if (const int items = q6_flat_items_for(n_out, G)) {
+		const bool wide = G.C > 64;
+		const int rows_wg = wide ? items : 4 * items * G.rt;
+		const int wgs = (n_out + rows_wg - 1) / rows_wg;
+		const dim3 block(wide ? G.tpr * kWave : 4 * kWave);
+#define HK_Q6F(IT) \
+	hipLaunchKernelGGL(q6k_gemv_flat_kernel<IT>, dim3(wgs), block, 0, stream(), (const uint8_t *)w, x, bias, res, out, \
+	                   n_out, n_in)
+		if (items <= 1) HK_Q6F(1);
+		else if (items <= 2) HK_Q6F(2);
+		else if (items <= 4) HK_Q6F(4);
+		else HK_Q6F(8);
+#undef HK_Q6F
+		HK_LAUNCHED("q6k_gemv_flat");
+		return ok();
+	}
 	const int min_rows = G.rt * G.rw;
 	int wgs = (n_out + min_rows - 1) / min_rows;
 	const int max_wgs = g_q6_wgs_per_cu * cu_count();

@@ -158,6 +158,7 @@ int hako_gpu_tune(int knob, int value) {
 	case HAKO_TUNE_Q6K_WGS_PER_CU: q6k_set_wgs_per_cu(value); return ok();
 	case HAKO_TUNE_Q4K_WAVES: q4k_set_waves(value); return ok();
 	case HAKO_TUNE_Q6K_WAVES: q6k_set_waves(value); return ok();
+	case HAKO_TUNE_Q6K_FLAT_ITEMS: q6k_set_flat_items(value); return ok();
 	case HAKO_TUNE_Q4K_FLAT_ITEMS: q4k_set_flat_items(value); return ok();
 	case HAKO_TUNE_SKINNY_Q4K_WGS: q4k_skinny_set_target_wgs(value); return ok();
 	case HAKO_TUNE_SKINNY_Q6K_WGS: q6k_skinny_set_target_wgs(value); return ok();

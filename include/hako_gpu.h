@@ -65,6 +65,7 @@ const char *hako_gpu_last_error(void);
  * EINVAL. */
 #define HAKO_TUNE_SKINNY_Q4K_WGS 6
 #define HAKO_TUNE_SKINNY_Q6K_WGS 7
+#define HAKO_TUNE_Q6K_FLAT_ITEMS 8   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
 int hako_gpu_tune(int knob, int value);
 
 typedef struct {

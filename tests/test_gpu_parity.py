@@ -216,6 +216,44 @@ def test_q6k_gemv_vs_oracle(gpu, oracle, n_out, n_in):
     assert maxabs_rel(got, want) < TOL
 
 
+HAKO_TUNE_Q6K_WGS_PER_CU, HAKO_TUNE_Q6K_WAVES, HAKO_TUNE_Q6K_FLAT_ITEMS = 2, 4, 8
+
+
+@pytest.mark.parametrize("n_out,n_in", [(2048, 11008), (300, 2048), (77, 18944), (100, 1792), (64, 512)])
+def test_q6k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
+    """Persistent grid (4 or 8 waves, 1 or 2 workgroups per CU) and flat grid
+    (1..8 row items per wave), with and without a bias: the lane work and the
+    order of every addition are the same, so outputs are identical."""
+    rng = np.random.default_rng(n_out + 5 * n_in)
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    bias = synth.activation(rng, n_out)
+    dw, dx, db, do = gpu.upload(w), gpu.upload(x), gpu.upload(bias), gpu.alloc(n_out * 4)
+    seen = {}
+    try:
+        for items, waves, wgs in ((-1, 4, 1), (0, 4, 1), (0, 8, 1), (0, 4, 2), (1, 4, 1), (2, 4, 1), (4, 4, 1),
+                                  (8, 4, 1)):
+            gpu.tune(HAKO_TUNE_Q6K_FLAT_ITEMS, items)
+            gpu.tune(HAKO_TUNE_Q6K_WAVES, waves)
+            gpu.tune(HAKO_TUNE_Q6K_WGS_PER_CU, wgs)
+            for b in (None, db):
+                gpu.q6k_gemv(do, dw, dx, b, n_out, n_in)
+                v = gpu.download(do, np.float32, (n_out,))
+                key = b is None
+                if key in seen:
+                    assert np.array_equal(seen[key].view(np.uint32), v.view(np.uint32)), (items, waves, wgs, key)
+                else:
+                    seen[key] = v
+    finally:
+        gpu.tune(HAKO_TUNE_Q6K_FLAT_ITEMS, -1)
+        gpu.tune(HAKO_TUNE_Q6K_WAVES, 4)
+        gpu.tune(HAKO_TUNE_Q6K_WGS_PER_CU, 1)
+        for b in (dw, dx, db, do):
+            b.free()
+    want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True, threads=16)
+    assert maxabs_rel(seen[False], want) < TOL
+
+
 def test_q6k_full_int8_scales(gpu, oracle):
     rng = np.random.default_rng(11)
     w = synth.q6k_blocks(rng, 300 * 8, scale_range=(-128, 127)).reshape(300, -1)
