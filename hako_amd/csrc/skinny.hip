@@ -8,13 +8,13 @@
 // rows (B operand), so every lane owns one row (l % 16) and keeps that row's
 // scales to itself, and holds four tokens (4*(l/16) + v) of the output.
 //
-// A workgroup (4 waves, 64 rows) takes a range of at most a few
-// super-blocks of K: its activations fit a small LDS stage and its weight
-// loads a few registers per lane, so several workgroups share a CU and keep
-// enough bytes in flight. When K is split over several workgroups their
-// partial results go to a buffer that skinny_reduce_kernel sums in split
-// order, applying the epilogue (a kernel boundary, not a device-scope fence
-// per workgroup, makes the partials visible).
+// Q4_K runs a persistent grid whose workgroups share one 16-row group at a
+// time (its waves split the group's K range) and reduce their sums in LDS;
+// Q6_K runs a workgroup (4 waves, 64 rows) per tile and range of K. When K is
+// split over several workgroups their partial results go to a buffer that
+// skinny_reduce_kernel sums in split order, applying the epilogue (a kernel
+// boundary, not a device-scope fence per workgroup, makes the partials
+// visible).
 //
 // Q4_K x q8 (src/quant.c:150-232 per token and row): one
 // v_mfma_i32_16x16x32_i8 per 32-wide sub-block gives the exact per-sub-block
@@ -91,147 +91,229 @@ __device__ __forceinline__ void skinny_epilogue(int epi, const SegView &S, int v
 }
 
 // ── Q4_K x q8 ──
-
-// (7 blocks: occupancy 3, the 7B gate/up matmul 4% faster but the 16-sequence
-// step 1.4% slower)
-constexpr int kQ4SkBlocks = 4;                       // super-blocks of K per workgroup at most
-constexpr int kQ4SkRow = kQ4SkBlocks * kQK + kAPadQ4; // bytes per staged token row
+//
+// Persistent grid of G workgroups over the launch's 16-row groups: workgroup
+// b takes groups b, b + G, b + 2G, ...; its W waves split the group's K range
+// so that the whole group (16 rows of consecutive bytes) is requested at
+// once, and every wave loads its share of the next group while it folds the
+// current one. HBM serves such whole-region bursts at about 5 TB/s; waves
+// that each walk their own rows one super-block at a time (a wave per row
+// group over all of K) open every DRAM page once per super-block and stream
+// 30% slower. The 16 tokens' q8 rows of the K range sit in LDS, staged once
+// per workgroup. The waves' sums of a group meet in LDS and are added in wave
+// order, so the K range needs no partial sums in memory unless K is split
+// over launches (more than kQ4SkMaxBlocks super-blocks).
+constexpr int kQ4SkMaxBlocks = 16;   // super-blocks of K per launch split (K <= 4096: one split)
+constexpr int kQ4SkWaves = 16;       // waves per workgroup: four per SIMD
+constexpr int kQ4SkWgs = 256;        // workgroups of the persistent grid: one per CU
 
 struct Q4SkBuf {
 	uint4 h;        // block header of the lane's row
 	uint2 q[4];     // qs bytes 32g + 8(l/16) .. +8 of each 64-weight group g
 };
 
-// Workgroup (64-row tile, K split): wave w takes rows 16w.. of the tile over
-// super-blocks [kb_beg, kb_end) (at most kQ4SkBlocks). EPI kSkStore / kSkAdd
-// apply the epilogue directly (one split); kSkPart writes the partial sums
-// to part[split][t][vrow].
-template <int EPI>
-__global__ __launch_bounds__(kT) void q4k_skinny_kernel(SkSegs segs, const int8_t *__restrict__ xq,
-                                                        const float *__restrict__ xs, int M, int K, int vrows,
-                                                        int nsplit, float *__restrict__ part) {
-	__shared__ __align__(16) int8_t a_s[16 * kQ4SkRow];          // xq of the range, token rows
-	__shared__ __align__(16) float xs_s[kQ4SkBlocks * 8][16];    // xs per (sub-block, token)
-	__shared__ __align__(16) float nu_s[kQ4SkBlocks * 8][16];    // -xs * sum xq
-	__shared__ __align__(16) float ex_s[4][16][8];               // d*s per (wave, row, sub-block)
+// LDS of a workgroup over nbk super-blocks: the q8 rows [16][nbk*256 + 16],
+// xs and -xs*sum(xq) per (sub-block, token), d*s per (wave, row, sub-block),
+// and three slots of the waves' sums of a group.
+__host__ __device__ constexpr size_t q4sk_arow(int nbk) { return (size_t)nbk * kQK + 16; }
+__host__ __device__ constexpr size_t q4sk_lds(int nbk, int W) {
+	return ((16 * q4sk_arow(nbk) + 15) & ~(size_t)15) + 2 * (size_t)nbk * 8 * 16 * 4 + (size_t)W * 16 * 8 * 4 +
+	       3 * (size_t)W * 64 * 16;
+}
+
+template <int EPI, int W>
+__global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const int8_t *__restrict__ xq,
+                                                            const float *__restrict__ xs, int M, int K, int vrows,
+                                                            int nsplit, float *__restrict__ part) {
+	constexpr int T = 64 * W;
+	constexpr int NBW = (kQ4SkMaxBlocks + W - 1) / W;   // super-blocks per wave at most
+	extern __shared__ __align__(16) uint8_t smem[];
 	const int tid = threadIdx.x, lane = tid & 63;
-	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: segment and descriptors in SGPRs
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 	const int j = lane & 15, kq = lane >> 4;
 	const int NB = K >> 8, NS = K >> 5;
-	const int tile = blockIdx.x / nsplit, split = blockIdx.x - tile * nsplit;
+	const int split = blockIdx.y;
 	const int kb_beg = (int)((int64_t)split * NB / nsplit), kb_end = (int)((int64_t)(split + 1) * NB / nsplit);
 	const int nbk = kb_end - kb_beg;
-	const int wrow0 = (tile * 4 + wave) * kRowsWave;
-	const SegView S = seg_of(segs, wrow0, false);
-	const int vrow = wrow0 + j, wr = vrow - S.row0;
-	const bool ok = vrow < vrows && wr < S.rows;
+	const int arow = (int)q4sk_arow(nbk);
+	int8_t *a_s = (int8_t *)smem;
+	float *xs_s = (float *)(smem + ((16 * (size_t)arow + 15) & ~(size_t)15));   // [nbk*8][16]
+	float *nu_s = xs_s + nbk * 8 * 16;                                          // [nbk*8][16]
+	float *ex = nu_s + nbk * 8 * 16 + wave * 128 + j * 8;                       // [W][16][8]: this lane's row
+	float4 *red_s = (float4 *)(nu_s + nbk * 8 * 16 + W * 128);                  // [3][W][64]
+	// the wave's super-blocks of the group
+	const int wb_beg = kb_beg + wave * nbk / W, wb_end = kb_beg + (wave + 1) * nbk / W;
+	const int ngroups = (vrows + 15) >> 4, G = gridDim.x;
 	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
-	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, (uint32_t)S.rows * rb);
-	const uint32_t row_off = ok ? (uint32_t)wr * rb : kBufNone;
 
-	// 1. every weight load of the range, then the activation staging
-	Q4SkBuf buf[kQ4SkBlocks];
+	// Loads take the lane's fixed offset in the vector operand and the
+	// block's in the scalar one. A row outside the segment (or a group past
+	// the last) starts at the stream's end; a block past the wave's range
+	// loads through a descriptor of zero bytes. Either way the load returns
+	// zeros without touching memory.
+	auto wload = [&](Q4SkBuf (&b)[NBW], int g) {
+		const int r0 = g * 16;
+		const SegView S = seg_of(segs, r0, false);
+		const int wr = r0 + j - S.row0;
+		const bool ok = g < ngroups && r0 + j < vrows && wr < S.rows;
+		const uint32_t wbytes = (uint32_t)S.rows * rb;
+		const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, wbytes), none = stream_rsrc(S.w, 0);
+		const uint32_t row_off = ok ? (uint32_t)wr * rb : wbytes;
 #pragma unroll
-	for (int d = 0; d < kQ4SkBlocks; d++) {
-		const uint32_t o = d < nbk ? row_off + (uint32_t)(kb_beg + d) * kQ4Bytes : kBufNone;
-		buf[d].h = ld_b128(wrs, o);
+		for (int d = 0; d < NBW; d++) {
+			const int kb = wb_beg + d;
+			const __amdgpu_buffer_rsrc_t r = kb < wb_end ? wrs : none;
+			const int so = kb * kQ4Bytes;
+			b[d].h = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)row_off, so, 0));
 #pragma unroll
-		for (int g = 0; g < 4; g++) buf[d].q[g] = ld_b64(wrs, o + 16 + 32 * g + 8 * kq);
-	}
-	__builtin_amdgcn_sched_barrier(0);
-	// 16 tokens x (16 per block) pieces of 16 bytes, zeros past M or the range
-	constexpr int QP = 16 * kQ4SkBlocks, QU = (16 * QP + kT - 1) / kT;       // pieces per token, per thread
-	constexpr int SP = 8 * kQ4SkBlocks, SU = (16 * SP + kT - 1) / kT;        // sub-blocks per token, per thread
-	const __amdgpu_buffer_rsrc_t qrs = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
-	const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
-	uint4 qv[QU];
-	float sv[SU];
-#pragma unroll
-	for (int u = 0; u < QU; u++) {
-		const int c = tid + kT * u, t = c / QP, p = c - t * QP;
-		qv[u] = ld_b128(qrs, (p < 16 * nbk && t < M) ? (uint32_t)t * K + 256u * kb_beg + 16u * p : kBufNone);
-	}
-#pragma unroll
-	for (int u = 0; u < SU; u++) {
-		const int c = tid + kT * u, t = c / SP, sb = c - t * SP;
-		sv[u] = __builtin_bit_cast(float, ld_b32(srs, (sb < 8 * nbk && t < M)
-		                                                  ? 4u * ((uint32_t)t * NS + 8u * kb_beg + sb)
-		                                                  : kBufNone));
-	}
-#pragma unroll
-	for (int u = 0; u < QU; u++) {
-		const int c = tid + kT * u, t = c / QP, p = c - t * QP;
-		if (t < 16) *(uint4 *)(a_s + t * kQ4SkRow + 16 * p) = qv[u];
-	}
-	__syncthreads();
-#pragma unroll
-	for (int u = 0; u < SU; u++) {
-		const int c = tid + kT * u, t = c / SP, sb = c - t * SP;
-		if (t >= 16) continue;
-		const int4 *p = (const int4 *)(a_s + t * kQ4SkRow + 32 * sb);
-		const int4 p0 = p[0], p1 = p[1];
-		int ix = 0;
-		ix = sdot4(p0.x, 0x01010101, ix); ix = sdot4(p0.y, 0x01010101, ix);
-		ix = sdot4(p0.z, 0x01010101, ix); ix = sdot4(p0.w, 0x01010101, ix);
-		ix = sdot4(p1.x, 0x01010101, ix); ix = sdot4(p1.y, 0x01010101, ix);
-		ix = sdot4(p1.z, 0x01010101, ix); ix = sdot4(p1.w, 0x01010101, ix);
-		xs_s[sb][t] = sv[u];
-		nu_s[sb][t] = -sv[u] * (float)ix;
-	}
-	__syncthreads();
+			for (int q = 0; q < 4; q++)
+				b[d].q[q] = __builtin_bit_cast(
+				    uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(row_off + 16 + 32 * q + 8 * kq), so, 0));
+		}
+	};
 
-	// 2. per block: (s, m) of sub-blocks kq, kq+4 of the lane's row; d*s to
-	//    the row's other lanes through LDS, dmin*m into the min-term MFMA
-	v4f acc = {0.0f, 0.0f, 0.0f, 0.0f}, accm = {0.0f, 0.0f, 0.0f, 0.0f};
-	const v4i zero = {0, 0, 0, 0};
-	float *ex = &ex_s[wave][j][0];
-	const int8_t *arow = a_s + j * kQ4SkRow + 8 * kq;   // A operand: token j, K-slice 8kq
+	// per block: (s, m) of sub-blocks kq, kq+4 of the lane's row; d*s to the
+	// row's other lanes through LDS, dmin*m into the min-term MFMA
+	auto fold = [&](const Q4SkBuf (&b)[NBW], float (&y)[4]) {
+		v4f acc = {0.0f, 0.0f, 0.0f, 0.0f}, accm = {0.0f, 0.0f, 0.0f, 0.0f};
+		const v4i zero = {0, 0, 0, 0};
 #pragma unroll
-	for (int d = 0; d < kQ4SkBlocks; d++) {
-		if (d < nbk) {
-			const Q4SkBuf &b = buf[d];
-			uint32_t s0, m0, s1, m1;
-			scale_min_k4((uint32_t)kq, b.h.y, b.h.z, b.h.w, s0, m0);
-			scale_min_k4((uint32_t)kq + 4u, b.h.y, b.h.z, b.h.w, s1, m1);
-			const float dd = f16_to_f32(b.h.x & 0xFFFFu), dmin = f16_to_f32(b.h.x >> 16);
-			ex[kq] = dd * (float)s0;
-			ex[kq + 4] = dd * (float)s1;
-			const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
-			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[8 * d + kq][j], dm0, accm, 0, 0, 0);
-			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[8 * d + kq + 4][j], dm1, accm, 0, 0, 0);
-			__builtin_amdgcn_wave_barrier();
-			const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
-			const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
+		for (int d = 0; d < NBW; d++) {
+			const int kl = wb_beg + d - kb_beg;   // block within the staged range
+			if (wb_beg + d < wb_end) {
+				uint32_t s0, m0, s1, m1;
+				scale_min_k4((uint32_t)kq, b[d].h.y, b[d].h.z, b[d].h.w, s0, m0);
+				scale_min_k4((uint32_t)kq + 4u, b[d].h.y, b[d].h.z, b[d].h.w, s1, m1);
+				const float dd = f16_to_f32(b[d].h.x & 0xFFFFu), dmin = f16_to_f32(b[d].h.x >> 16);
+				ex[kq] = dd * (float)s0;
+				ex[kq + 4] = dd * (float)s1;
+				const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
+				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kl + kq) * 16 + j], dm0, accm, 0, 0, 0);
+				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kl + kq + 4) * 16 + j], dm1, accm, 0, 0, 0);
+				__builtin_amdgcn_wave_barrier();
+				const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
+				const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
+				const int8_t *arow_p = a_s + j * arow + kl * kQK + 8 * kq;   // A operand: token j, K-slice 8kq
+				// the block's eight integer products first, then their folds
+				v4i di[8];
 #pragma unroll
-			for (int g = 0; g < 4; g++) {
-				const uint2 q = b.q[g];
+				for (int g = 0; g < 4; g++) {
+					const uint2 q = b[d].q[g];
 #pragma unroll
-				for (int h = 0; h < 2; h++) {
-					const int sb = 2 * g + h;
-					const uint32_t w0 = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
-					const uint32_t w1 = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
-					const long wv = (long)(((uint64_t)w1 << 32) | w0);
-					const long av = *(const long *)(arow + 256 * d + 32 * sb);
-					const v4i di = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zero, 0, 0, 0);
-					const float4 x4 = *(const float4 *)&xs_s[8 * d + sb][4 * kq];
-					acc[0] = __builtin_fmaf((float)di[0], x4.x * ds[sb], acc[0]);
-					acc[1] = __builtin_fmaf((float)di[1], x4.y * ds[sb], acc[1]);
-					acc[2] = __builtin_fmaf((float)di[2], x4.z * ds[sb], acc[2]);
-					acc[3] = __builtin_fmaf((float)di[3], x4.w * ds[sb], acc[3]);
+					for (int h = 0; h < 2; h++) {
+						const int sb = 2 * g + h;
+						const uint32_t w0 = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+						const uint32_t w1 = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+						const long wv = (long)(((uint64_t)w1 << 32) | w0);
+						const long av = *(const long *)(arow_p + 32 * sb);
+						di[sb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zero, 0, 0, 0);
+					}
+				}
+#pragma unroll
+				for (int sb = 0; sb < 8; sb++) {
+					const float4 x4 = *(const float4 *)&xs_s[(8 * kl + sb) * 16 + 4 * kq];
+					acc[0] = __builtin_fmaf((float)di[sb][0], x4.x * ds[sb], acc[0]);
+					acc[1] = __builtin_fmaf((float)di[sb][1], x4.y * ds[sb], acc[1]);
+					acc[2] = __builtin_fmaf((float)di[sb][2], x4.z * ds[sb], acc[2]);
+					acc[3] = __builtin_fmaf((float)di[sb][3], x4.w * ds[sb], acc[3]);
+				}
+				__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next block
+			}
+		}
+#pragma unroll
+		for (int v = 0; v < 4; v++) y[v] = acc[v] + accm[v];
+	};
+
+	// the waves' sums of group g (lane: tokens 4(l/16) + v of row l%16) to
+	// LDS slot p, then thread (t, r) < 256 adds them in wave order and
+	// applies the epilogue to token t of row r of the group
+	auto finish = [&](const float (&y)[4], int g, int p) {
+		red_s[(p * W + wave) * 64 + lane] = make_float4(y[0], y[1], y[2], y[3]);
+		__syncthreads();
+		if (tid < 256) {
+			const int t = tid >> 4, r = tid & 15;
+			const float *src = (const float *)&red_s[p * W * 64 + 16 * (t >> 2) + r] + (t & 3);
+			float sum = 0.0f;
+#pragma unroll
+			for (int w = 0; w < W; w++) sum += src[w * 64 * 4];
+			const int r0 = g * 16;
+			const SegView S = seg_of(segs, r0, false);
+			const int vrow = r0 + r, wr = vrow - S.row0;
+			if (vrow < vrows && wr < S.rows) {
+				if (EPI == kSkPart) {
+					part[((size_t)split * 16 + t) * vrows + vrow] = sum;   // tokens past M: zeros
+				} else if (t < M) {
+					float *o = S.out + (size_t)t * S.ld + wr;
+					*o = EPI == kSkAdd ? *o + sum : sum + (S.bias ? S.bias[wr] : 0.0f);
 				}
 			}
-			__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next block
+		}
+	};
+
+	// weights of three groups in flight: the one being folded and the next two
+	Q4SkBuf wb0[NBW], wb1[NBW], wb2[NBW];
+	int g = blockIdx.x;
+	wload(wb0, g);
+
+	// stage the q8 rows of the K range: piece c = (t, p) holds bytes 16p..
+	// of token t's range and, for even p, the scale of its sub-block p/2
+	// (zeros past M); a sub-block's two pieces sit in neighbouring lanes
+	{
+		const int PT = 16 * nbk;   // pieces per token
+		const __amdgpu_buffer_rsrc_t qrs = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
+		const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
+		constexpr int U = (16 * 16 * kQ4SkMaxBlocks + T - 1) / T;
+		uint4 qv[U];
+		float sv[U];
+#pragma unroll
+		for (int u = 0; u < U; u++) {
+			const int c = tid + T * u, t = c / PT, p = c - t * PT;
+			const bool in = c < 16 * PT && t < M;
+			qv[u] = ld_b128(qrs, in ? (uint32_t)t * K + 256u * kb_beg + 16u * p : kBufNone);
+			sv[u] = __builtin_bit_cast(float, ld_b32(srs, in && !(p & 1) ? 4u * ((uint32_t)t * NS + 8u * kb_beg + (p >> 1))
+			                                                            : kBufNone));
+		}
+#pragma unroll
+		for (int u = 0; u < U; u++) {
+			const int c = tid + T * u, t = c / PT, p = c - t * PT;
+			int ix = 0;
+			ix = sdot4((int)qv[u].x, 0x01010101, ix);
+			ix = sdot4((int)qv[u].y, 0x01010101, ix);
+			ix = sdot4((int)qv[u].z, 0x01010101, ix);
+			ix = sdot4((int)qv[u].w, 0x01010101, ix);
+			ix += dpp_i<kDppQuadSwap1>(ix);   // the sub-block's other 16 bytes
+			if (c < 16 * PT) {
+				*(uint4 *)(a_s + t * arow + 16 * p) = qv[u];
+				if (!(p & 1)) {
+					xs_s[(p >> 1) * 16 + t] = sv[u];
+					nu_s[(p >> 1) * 16 + t] = -sv[u] * (float)ix;
+				}
+			}
 		}
 	}
-	const float y[4] = {acc[0] + accm[0], acc[1] + accm[1], acc[2] + accm[2], acc[3] + accm[3]};
-	if (EPI == kSkPart) {
-		// tokens past M hold zeros (zero activations)
-		if (ok)
-#pragma unroll
-			for (int v = 0; v < 4; v++) part[((size_t)split * 16 + 4 * kq + v) * vrows + vrow] = y[v];
-		return;
+	// every load so far complete (the staging's waits sit on a branch that
+	// the wait-count pass would otherwise carry into the loop as pending
+	// loads, waiting out the whole prefetch at every use of their registers)
+	__builtin_amdgcn_s_waitcnt(0);
+	__syncthreads();
+	wload(wb1, g + G);
+
+	for (; g < ngroups; g += 3 * G) {
+		float y[4];
+		wload(wb2, g + 2 * G);
+		fold(wb0, y);
+		finish(y, g, 0);
+		wload(wb0, g + 3 * G);
+		if (g + G < ngroups) {
+			fold(wb1, y);
+			finish(y, g + G, 1);
+		}
+		wload(wb1, g + 4 * G);
+		if (g + 2 * G < ngroups) {
+			fold(wb2, y);
+			finish(y, g + 2 * G, 2);
+		}
 	}
-	skinny_epilogue(EPI, S, vrow, ok, y, M, lane);
 }
 
 // ── Q6_K x fp32 (fp16 hi/lo) ──
@@ -509,18 +591,16 @@ int reduce(const SkSegs &segs, int epi, const float *part, int nsplit, int m, in
 }  // namespace
 
 namespace {
-int g_q4_target = kSkTargetWgs, g_q6_target = kSkTargetWgsQ6;
+int g_q4_target = kQ4SkWgs, g_q6_target = kSkTargetWgsQ6;
 }
 
-void q4k_skinny_set_target_wgs(int wgs) { g_q4_target = wgs > 0 ? wgs : kSkTargetWgs; }
+void q4k_skinny_set_target_wgs(int wgs) { g_q4_target = wgs > 0 ? wgs : kQ4SkWgs; }
 void q6k_skinny_set_target_wgs(int wgs) { g_q6_target = wgs > 0 ? wgs : kSkTargetWgsQ6; }
 
 int q4k_skinny_splits(int n_in, int vrows) {
-	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
-	int ns = (g_q4_target + tiles - 1) / tiles;            // enough workgroups to fill the chip
-	const int need = (nb + kQ4SkBlocks - 1) / kQ4SkBlocks;  // at most kQ4SkBlocks per workgroup
-	ns = ns < need ? need : ns;
-	return ns > nb ? nb : ns;
+	(void)vrows;
+	const int nb = n_in / kQK;
+	return (nb + kQ4SkMaxBlocks - 1) / kQ4SkMaxBlocks;
 }
 
 size_t q4k_skinny_part_floats(int n_in, int vrows, int epi) {
@@ -530,22 +610,38 @@ size_t q4k_skinny_part_floats(int n_in, int vrows, int epi) {
 
 int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
                float *part, size_t part_cap) {
-	const int tiles = (vrows + kRowsWg - 1) / kRowsWg;
-	const int ns = q4k_skinny_splits(n_in, vrows);
+	const int ns = q4k_skinny_splits(n_in, vrows), nb = n_in / kQK;
 	const bool direct = ns == 1 && epi != kSkSwiGLU && epi != kSkPart;
 	if (!direct && (!part || part_cap < q4k_skinny_part_floats(n_in, vrows, epi)))
 		return set_error(HAKO_GPU_EINVAL, "Q4_K skinny split needs a workspace of %zu floats (has %zu)",
 		                 q4k_skinny_part_floats(n_in, vrows, epi), part ? part_cap : (size_t)0);
-	const dim3 grid(tiles * ns);
+	const int ngroups = (vrows + 15) / 16;
+	const dim3 grid(ngroups < g_q4_target ? ngroups : g_q4_target, ns);
+	const size_t lds = q4sk_lds((nb + ns - 1) / ns, kQ4SkWaves);
+	static bool attr_set[64];   // per device
+	int dev = 0;
+	HK_HIP(hipGetDevice(&dev));
+	if (dev < 0 || dev >= 64) return set_error(HAKO_GPU_ENODEV, "device %d beyond the 64 the skinny launch tracks", dev);
+	if (!attr_set[dev]) {   // more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU)
+		const size_t max_lds = q4sk_lds(kQ4SkMaxBlocks, kQ4SkWaves);
+		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkPart, kQ4SkWaves>,
+		                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds));
+		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkStore, kQ4SkWaves>,
+		                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds));
+		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkAdd, kQ4SkWaves>,
+		                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds));
+		attr_set[dev] = true;
+	}
+	const dim3 block(64 * kQ4SkWaves);
 	if (!direct)
-		hipLaunchKernelGGL(q4k_skinny_kernel<kSkPart>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, ns,
-		                   part);
+		hipLaunchKernelGGL((q4k_skinny_kernel<kSkPart, kQ4SkWaves>), grid, block, lds, stream(), segs, xq, xs, m, n_in,
+		                   vrows, ns, part);
 	else if (epi == kSkStore)
-		hipLaunchKernelGGL(q4k_skinny_kernel<kSkStore>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, 1,
-		                   part);
+		hipLaunchKernelGGL((q4k_skinny_kernel<kSkStore, kQ4SkWaves>), grid, block, lds, stream(), segs, xq, xs, m,
+		                   n_in, vrows, 1, part);
 	else
-		hipLaunchKernelGGL(q4k_skinny_kernel<kSkAdd>, grid, dim3(kT), 0, stream(), segs, xq, xs, m, n_in, vrows, 1,
-		                   part);
+		hipLaunchKernelGGL((q4k_skinny_kernel<kSkAdd, kQ4SkWaves>), grid, block, lds, stream(), segs, xq, xs, m, n_in,
+		                   vrows, 1, part);
 	HK_LAUNCHED("q4k_skinny");
 	return (direct || epi == kSkPart) ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
 }

@@ -58,10 +58,11 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_Q4K_WAVES      3
 #define HAKO_TUNE_Q6K_WAVES      4
 #define HAKO_TUNE_Q4K_FLAT_ITEMS 5   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
-/* Workgroups a skinny (2..16 token) Q4_K / Q6_K launch aims for through its
- * K split (0: the defaults, 512 and 1024); the split count sets the order in
- * which the fp32 partial sums are added. A decoder sizes its split workspace
- * when it is created; a later, larger target makes its steps fail with
+/* Skinny (2..16 token) launches: the Q4_K persistent grid's workgroups (0:
+ * the default, 256), and the workgroups a Q6_K launch aims for through its K
+ * split (0: the default, 1024); the Q6_K split count sets the order in which
+ * its fp32 partial sums are added. A decoder sizes its split workspace when
+ * it is created; a later, larger Q6_K target makes its steps fail with
  * EINVAL. */
 #define HAKO_TUNE_SKINNY_Q4K_WGS 6
 #define HAKO_TUNE_SKINNY_Q6K_WGS 7

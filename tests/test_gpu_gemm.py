@@ -42,7 +42,9 @@ def run_q4k_gemm(gpu, w, xq, xs, n_out, n_in):
 GEMM_SHAPES = [(64, 64, 256), (130, 200, 2048), (17, 100, 3584), (64, 512, 3584), (200, 37, 1280),
                (96, 300, 11008),
                # up to 16 tokens: the skinny kernels (batched decode)
-               (2, 64, 256), (5, 100, 2048), (16, 512, 3584), (16, 1000, 1280), (1 + 15, 37, 2048), (3, 18944, 3584)]
+               (2, 64, 256), (5, 100, 2048), (16, 512, 3584), (16, 1000, 1280), (1 + 15, 37, 2048), (3, 18944, 3584),
+               # one split per 64-row tile, two passes of the weight prefetch ring
+               (16, 32832, 2048)]
 
 
 @pytest.mark.parametrize("m,n_out,n_in", GEMM_SHAPES)
