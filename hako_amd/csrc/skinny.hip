@@ -93,40 +93,67 @@ __device__ __forceinline__ void skinny_epilogue(int epi, const SegView &S, int v
 // ── Q4_K x q8 ──
 //
 // Persistent grid of G workgroups over the launch's 16-row groups: workgroup
-// b takes groups b, b + G, b + 2G, ...; its W waves split the group's K range
-// so that the whole group (16 rows of consecutive bytes) is requested at
-// once, and every wave loads its share of the next group while it folds the
-// current one. HBM serves such whole-region bursts at about 5 TB/s; waves
-// that each walk their own rows one super-block at a time (a wave per row
-// group over all of K) open every DRAM page once per super-block and stream
-// 30% slower. The 16 tokens' q8 rows of the K range sit in LDS, staged once
-// per workgroup. The waves' sums of a group meet in LDS and are added in wave
+// b takes groups b, b + G, b + 2G, ... Its threads load a group's weights
+// (16 rows of consecutive bytes over the K range) as consecutive 16-byte
+// pieces and park them in an LDS slot, from which each wave reads its
+// super-block of the 16 rows in the matrix-core lane layout: the waves split
+// the group's K range one super-block each. Whole-region loads stream at
+// about 6 TB/s; loads in the lane layout (16 rows x 32 bytes per
+// instruction) reach 4 TB/s at the same grid. Two groups are in flight in
+// registers while a third is folded from LDS. A wave's super-block is the
+// same for every group, so its activation operands (the 16 tokens' q8 bytes,
+// scales and -xs*sum(xq) of that block) are read from LDS into registers
+// once. The waves' sums of a group meet in LDS and are added in a fixed
 // order, so the K range needs no partial sums in memory unless K is split
 // over launches (more than kQ4SkMaxBlocks super-blocks).
 constexpr int kQ4SkMaxBlocks = 16;   // super-blocks of K per launch split (K <= 4096: one split)
-constexpr int kQ4SkWaves = 16;       // waves per workgroup: four per SIMD
 constexpr int kQ4SkWgs = 256;        // workgroups of the persistent grid: one per CU
+constexpr int kQ4SkPieces = 3;       // 16-byte pieces per thread and group: 16 rows x 9 x nbk <= 2.25 T
 
-struct Q4SkBuf {
-	uint4 h;        // block header of the lane's row
-	uint2 q[4];     // qs bytes 32g + 8(l/16) .. +8 of each 64-weight group g
-};
-
-// LDS of a workgroup over nbk super-blocks: the q8 rows [16][nbk*256 + 16],
-// xs and -xs*sum(xq) per (sub-block, token), d*s per (wave, row, sub-block),
-// and three slots of the waves' sums of a group.
+// LDS of a workgroup over nbk super-blocks (W waves, nbk <= W). Region A
+// holds first the staged q8 rows [16][nbk*256 + 16], then two slots of a
+// group's weights [16][nbk*144 + 16]; then xs and -xs*sum(xq) per
+// (sub-block, token), d*s per (wave, row, sub-block) and two slots of the
+// waves' sums of a group.
 __host__ __device__ constexpr size_t q4sk_arow(int nbk) { return (size_t)nbk * kQK + 16; }
+__host__ __device__ constexpr size_t q4sk_rstride(int nbk) { return (size_t)nbk * kQ4Bytes + 16; }
+__host__ __device__ constexpr size_t q4sk_region(int nbk) {
+	return 16 * q4sk_arow(nbk) > 2 * 16 * q4sk_rstride(nbk) ? 16 * q4sk_arow(nbk) : 2 * 16 * q4sk_rstride(nbk);
+}
 __host__ __device__ constexpr size_t q4sk_lds(int nbk, int W) {
-	return ((16 * q4sk_arow(nbk) + 15) & ~(size_t)15) + 2 * (size_t)nbk * 8 * 16 * 4 + (size_t)W * 16 * 8 * 4 +
-	       3 * (size_t)W * 64 * 16;
+	return q4sk_region(nbk) + 2 * (size_t)nbk * 8 * 16 * 4 + (size_t)W * 16 * 8 * 4 + 2 * (size_t)W * 64 * 16;
 }
 
+// A pointer the compiler cannot prove wave-uniform (it is) in scalar
+// registers, so that a descriptor built on it needs no per-lane loop.
+template <class P>
+__device__ __forceinline__ P *uniform_ptr(P *p) {
+	const uint64_t v = (uint64_t)(uintptr_t)p;
+	const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+	return (P *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// The segment of launch row r0 (uniform) with plain selects of its fields:
+// scalar selects, no copy of the argument block.
+__device__ __forceinline__ SegView seg_at(const SkSegs &s, int r0) {
+	const bool in1 = s.n > 1 && r0 >= s.s[1].row0, in2 = s.n > 2 && r0 >= s.s[2].row0;
+	SegView v;
+	v.w = in2 ? s.s[2].w : in1 ? s.s[1].w : s.s[0].w;
+	v.bias = in2 ? s.s[2].bias : in1 ? s.s[1].bias : s.s[0].bias;
+	v.out = in2 ? s.s[2].out : in1 ? s.s[1].out : s.s[0].out;
+	v.row0 = in2 ? s.s[2].row0 : in1 ? s.s[1].row0 : s.s[0].row0;
+	v.rows = in2 ? s.s[2].rows : in1 ? s.s[1].rows : s.s[0].rows;
+	v.ld = in2 ? s.s[2].ld : in1 ? s.s[1].ld : s.s[0].ld;
+	return v;
+}
+
+// W waves, one super-block of the launch split's K range each (nbk <= W).
 template <int EPI, int W>
 __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const int8_t *__restrict__ xq,
                                                             const float *__restrict__ xs, int M, int K, int vrows,
                                                             int nsplit, float *__restrict__ part) {
 	constexpr int T = 64 * W;
-	constexpr int NBW = (kQ4SkMaxBlocks + W - 1) / W;   // super-blocks per wave at most
+	constexpr int PP = kQ4SkPieces;
 	extern __shared__ __align__(16) uint8_t smem[];
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -135,125 +162,171 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 	const int split = blockIdx.y;
 	const int kb_beg = (int)((int64_t)split * NB / nsplit), kb_end = (int)((int64_t)(split + 1) * NB / nsplit);
 	const int nbk = kb_end - kb_beg;
-	const int arow = (int)q4sk_arow(nbk);
-	int8_t *a_s = (int8_t *)smem;
-	float *xs_s = (float *)(smem + ((16 * (size_t)arow + 15) & ~(size_t)15));   // [nbk*8][16]
-	float *nu_s = xs_s + nbk * 8 * 16;                                          // [nbk*8][16]
-	float *ex = nu_s + nbk * 8 * 16 + wave * 128 + j * 8;                       // [W][16][8]: this lane's row
-	float4 *red_s = (float4 *)(nu_s + nbk * 8 * 16 + W * 128);                  // [3][W][64]
-	// the wave's super-blocks of the group
-	const int wb_beg = kb_beg + wave * nbk / W, wb_end = kb_beg + (wave + 1) * nbk / W;
+	const int arow = (int)q4sk_arow(nbk), rstride = (int)q4sk_rstride(nbk);
+	const size_t region = q4sk_region(nbk);
+	int8_t *a_s = (int8_t *)smem;                         // staging: [16][arow]
+	uint8_t *w_s = smem;                                  // then: [2][16][rstride]
+	float *xs_s = (float *)(smem + region);               // [nbk*8][16]
+	float *nu_s = xs_s + nbk * 8 * 16;                    // [nbk*8][16]
+	float *ex = nu_s + nbk * 8 * 16 + wave * 128 + j * 8;   // [W][16][8]: this lane's row
+	float4 *red_s = (float4 *)(nu_s + nbk * 8 * 16 + W * 128);   // [2][W][64]
+	const bool live = wave < nbk;   // this wave's super-block: kb_beg + wave
 	const int ngroups = (vrows + 15) >> 4, G = gridDim.x;
 	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
 
-	// Loads take the lane's fixed offset in the vector operand and the
-	// block's in the scalar one. A row outside the segment (or a group past
-	// the last) starts at the stream's end; a block past the wave's range
-	// loads through a descriptor of zero bytes. Either way the load returns
-	// zeros without touching memory.
-	auto wload = [&](Q4SkBuf (&b)[NBW], int g) {
+	// the group's pieces of this thread: piece p = tid + T*i is bytes 16c..
+	// of row r of the group's K range (PR pieces per row)
+	const int PR = 9 * nbk, PG = 16 * PR;
+	uint32_t goff[PP], loff[PP];
+	int prow[PP];
+#pragma unroll
+	for (int i = 0; i < PP; i++) {
+		const int p = tid + T * i, r = p / PR, c = p - r * PR;
+		prow[i] = p < PG ? r : 1 << 20;   // pieces past the group: a row no group has
+		goff[i] = (uint32_t)r * rb + (uint32_t)kb_beg * kQ4Bytes + 16u * c;
+		loff[i] = (uint32_t)(r * rstride + 16 * c);
+	}
+	// A row outside the segment or the launch, a piece past the group and a
+	// group past the last read nothing (zeros, no memory access).
+	// the output this thread writes in the epilogue: token et of row er
+	constexpr int Q = T / 256;   // threads per output: 2 (8 waves) or 4 (16 waves)
+	const int eo = tid / Q, et = eo >> 4, er = eo & 15;
+	const bool eq = tid % Q == 0 && et < M;
+	auto gload = [&](uint4 (&v)[PP], float &ev, SegView &S, int g) {
 		const int r0 = g * 16;
-		const SegView S = seg_of(segs, r0, false);
-		const int wr = r0 + j - S.row0;
-		const bool ok = g < ngroups && r0 + j < vrows && wr < S.rows;
+		S = seg_at(segs, r0);
+		const int wr0 = r0 - S.row0;   // the group's first row in its segment
 		const uint32_t wbytes = (uint32_t)S.rows * rb;
-		const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, wbytes), none = stream_rsrc(S.w, 0);
-		const uint32_t row_off = ok ? (uint32_t)wr * rb : wbytes;
+		const __amdgpu_buffer_rsrc_t r = stream_rsrc(S.w, g < ngroups ? wbytes : 0u);
+		const int rmax = min(S.rows - wr0, vrows - r0);   // rows of the group in the segment and launch
 #pragma unroll
-		for (int d = 0; d < NBW; d++) {
-			const int kb = wb_beg + d;
-			const __amdgpu_buffer_rsrc_t r = kb < wb_end ? wrs : none;
-			const int so = kb * kQ4Bytes;
-			b[d].h = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)row_off, so, 0));
+		for (int i = 0; i < PP; i++)
+			v[i] = ld_b128(r, prow[i] < rmax ? (uint32_t)wr0 * rb + goff[i] : wbytes);
+		// the epilogue's operand, loaded with the weights so that the
+		// epilogue waits on nothing: the bias (Store) or the output (Add)
+		ev = 0.0f;
+		if (EPI == kSkStore || EPI == kSkAdd) {
+			const bool ok = eq && er < rmax;
+			const float *src = uniform_ptr(EPI == kSkStore ? S.bias : (const float *)S.out);
+			const uint32_t n = src ? (EPI == kSkStore ? (uint32_t)S.rows : (uint32_t)M * (uint32_t)S.ld) * 4u : 0u;
+			const __amdgpu_buffer_rsrc_t er_rs = stream_rsrc(src ? (const void *)src : (const void *)xs, n);
+			const uint32_t off = EPI == kSkStore ? 4u * (uint32_t)(wr0 + er) : 4u * ((uint32_t)et * S.ld + wr0 + er);
+			ev = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(er_rs, ok ? (int)off : (int)kBufNone, 0, 0));
+		}
+	};
+	// Parks a register set in a weight slot. Pieces past the group go to
+	// this thread's own entry of reduction slot p, which the next finish
+	// (slot p) overwrites before anyone reads it: no branch around the
+	// stores (the wait-count pass turns one into waits on every load).
+	const uint32_t red_off = (uint32_t)((uint8_t *)red_s - smem);
+	auto gstore = [&](const uint4 (&v)[PP], int slot, int p) {
+		const uint32_t ws = (uint32_t)slot * 16 * rstride, dummy = red_off + 16u * (p * W * 64 + tid);
 #pragma unroll
-			for (int q = 0; q < 4; q++)
-				b[d].q[q] = __builtin_bit_cast(
-				    uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(row_off + 16 + 32 * q + 8 * kq), so, 0));
+		for (int i = 0; i < PP; i++) {
+			const uint32_t a = prow[i] < 16 ? ws + loff[i] : dummy;   // a select, not a branch
+			*(uint4 *)(smem + a) = v[i];
 		}
 	};
 
+	// the wave's activation operands (registers, filled once): A operand
+	// (token j, bytes 32sb + 8kq.. of the block) and -xs*sum(xq) of (token j,
+	// sub-blocks kq, kq+4); xs of the lane's four tokens stays in LDS
+	long av[8];
+	float nu0 = 0.0f, nu1 = 0.0f;
+	const float *xsw = xs_s + (8 * wave) * 16 + 4 * kq;
+
 	// per block: (s, m) of sub-blocks kq, kq+4 of the lane's row; d*s to the
 	// row's other lanes through LDS, dmin*m into the min-term MFMA
-	auto fold = [&](const Q4SkBuf (&b)[NBW], float (&y)[4]) {
+	auto fold = [&](int slot, float (&y)[4]) {
 		v4f acc = {0.0f, 0.0f, 0.0f, 0.0f}, accm = {0.0f, 0.0f, 0.0f, 0.0f};
-		const v4i zero = {0, 0, 0, 0};
+		if (live) {
+			const uint8_t *rowp = w_s + ((size_t)slot * 16 + j) * rstride + wave * kQ4Bytes;
+			const uint4 hd = *(const uint4 *)rowp;
+			uint2 qv[4];
 #pragma unroll
-		for (int d = 0; d < NBW; d++) {
-			const int kl = wb_beg + d - kb_beg;   // block within the staged range
-			if (wb_beg + d < wb_end) {
-				uint32_t s0, m0, s1, m1;
-				scale_min_k4((uint32_t)kq, b[d].h.y, b[d].h.z, b[d].h.w, s0, m0);
-				scale_min_k4((uint32_t)kq + 4u, b[d].h.y, b[d].h.z, b[d].h.w, s1, m1);
-				const float dd = f16_to_f32(b[d].h.x & 0xFFFFu), dmin = f16_to_f32(b[d].h.x >> 16);
-				ex[kq] = dd * (float)s0;
-				ex[kq + 4] = dd * (float)s1;
-				const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
-				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kl + kq) * 16 + j], dm0, accm, 0, 0, 0);
-				accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu_s[(8 * kl + kq + 4) * 16 + j], dm1, accm, 0, 0, 0);
-				__builtin_amdgcn_wave_barrier();
-				const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
-				const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
-				const int8_t *arow_p = a_s + j * arow + kl * kQK + 8 * kq;   // A operand: token j, K-slice 8kq
-				// the block's eight integer products first, then their folds
-				v4i di[8];
+			for (int g = 0; g < 4; g++) qv[g] = *(const uint2 *)(rowp + 16 + 32 * g + 8 * kq);
+			const v4i zero = {0, 0, 0, 0};
+			uint32_t s0, m0, s1, m1;
+			scale_min_k4((uint32_t)kq, hd.y, hd.z, hd.w, s0, m0);
+			scale_min_k4((uint32_t)kq + 4u, hd.y, hd.z, hd.w, s1, m1);
+			const float dd = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+			ex[kq] = dd * (float)s0;
+			ex[kq + 4] = dd * (float)s1;
+			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu0, dmin * (float)m0, accm, 0, 0, 0);
+			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu1, dmin * (float)m1, accm, 0, 0, 0);
+			__builtin_amdgcn_wave_barrier();
+			const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
+			const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
+			// four integer products at a time, then their folds
 #pragma unroll
-				for (int g = 0; g < 4; g++) {
-					const uint2 q = b[d].q[g];
+			for (int half = 0; half < 2; half++) {
+				v4i di[4];
 #pragma unroll
-					for (int h = 0; h < 2; h++) {
-						const int sb = 2 * g + h;
-						const uint32_t w0 = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
-						const uint32_t w1 = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
-						const long wv = (long)(((uint64_t)w1 << 32) | w0);
-						const long av = *(const long *)(arow_p + 32 * sb);
-						di[sb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zero, 0, 0, 0);
-					}
+				for (int i = 0; i < 4; i++) {
+					const int sb = 4 * half + i, g4 = sb >> 1, h = sb & 1;
+					const uint2 q = qv[g4];
+					const uint32_t w0 = h ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+					const uint32_t w1 = h ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+					di[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[sb], (long)(((uint64_t)w1 << 32) | w0), zero, 0,
+					                                              0, 0);
 				}
 #pragma unroll
-				for (int sb = 0; sb < 8; sb++) {
-					const float4 x4 = *(const float4 *)&xs_s[(8 * kl + sb) * 16 + 4 * kq];
-					acc[0] = __builtin_fmaf((float)di[sb][0], x4.x * ds[sb], acc[0]);
-					acc[1] = __builtin_fmaf((float)di[sb][1], x4.y * ds[sb], acc[1]);
-					acc[2] = __builtin_fmaf((float)di[sb][2], x4.z * ds[sb], acc[2]);
-					acc[3] = __builtin_fmaf((float)di[sb][3], x4.w * ds[sb], acc[3]);
+				for (int i = 0; i < 4; i++) {
+					const int sb = 4 * half + i;
+					const float4 x4 = *(const float4 *)(xsw + sb * 16);
+					acc[0] = __builtin_fmaf((float)di[i][0], x4.x * ds[sb], acc[0]);
+					acc[1] = __builtin_fmaf((float)di[i][1], x4.y * ds[sb], acc[1]);
+					acc[2] = __builtin_fmaf((float)di[i][2], x4.z * ds[sb], acc[2]);
+					acc[3] = __builtin_fmaf((float)di[i][3], x4.w * ds[sb], acc[3]);
 				}
-				__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next block
 			}
+			__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next group
 		}
 #pragma unroll
 		for (int v = 0; v < 4; v++) y[v] = acc[v] + accm[v];
 	};
 
 	// the waves' sums of group g (lane: tokens 4(l/16) + v of row l%16) to
-	// LDS slot p, then thread (t, r) < 256 adds them in wave order and
-	// applies the epilogue to token t of row r of the group
-	auto finish = [&](const float (&y)[4], int g, int p) {
+	// LDS slot p; then every thread takes a quarter of the waves of output
+	// (t, r) = tid/(T/256) (W/4 waves each, in order), the quarters meet in
+	// neighbouring lanes, and the first applies the epilogue to token t of
+	// row r of the group: the same order of additions at every call
+	auto finish = [&](const float (&y)[4], const SegView &S, float ev, int g, int p) {
 		red_s[(p * W + wave) * 64 + lane] = make_float4(y[0], y[1], y[2], y[3]);
 		__syncthreads();
-		if (tid < 256) {
-			const int t = tid >> 4, r = tid & 15;
-			const float *src = (const float *)&red_s[p * W * 64 + 16 * (t >> 2) + r] + (t & 3);
-			float sum = 0.0f;
+		constexpr int WQ = W / Q;     // waves per thread: 4
+		const int qq = tid % Q, t = et, r = er;
+		const float *src = (const float *)&red_s[(p * W + qq * WQ) * 64 + 16 * (t >> 2) + r] + (t & 3);
+		float sum = 0.0f;
 #pragma unroll
-			for (int w = 0; w < W; w++) sum += src[w * 64 * 4];
-			const int r0 = g * 16;
-			const SegView S = seg_of(segs, r0, false);
-			const int vrow = r0 + r, wr = vrow - S.row0;
-			if (vrow < vrows && wr < S.rows) {
-				if (EPI == kSkPart) {
-					part[((size_t)split * 16 + t) * vrows + vrow] = sum;   // tokens past M: zeros
-				} else if (t < M) {
-					float *o = S.out + (size_t)t * S.ld + wr;
-					*o = EPI == kSkAdd ? *o + sum : sum + (S.bias ? S.bias[wr] : 0.0f);
-				}
-			}
+		for (int w = 0; w < WQ; w++) sum += src[w * 64 * 4];
+		sum += dpp_f<kDppQuadSwap1>(sum);   // quarters 0+1, 2+3
+		if (Q == 4) sum += dpp_f<kDppQuadSwap2>(sum);
+		// through descriptors, with an offset past the stream for the lanes
+		// that write nothing: no branch around memory operations
+		const int vrow = g * 16 + r, wr = vrow - S.row0;
+		const bool ok = qq == 0 && vrow < vrows && wr < S.rows;
+		if (EPI == kSkPart) {   // tokens past M: zeros
+			const __amdgpu_buffer_rsrc_t pr = stream_rsrc(part, (uint32_t)nsplit * 16u * (uint32_t)vrows * 4u);
+			__builtin_amdgcn_raw_buffer_store_b32(
+			    __builtin_bit_cast(uint32_t, sum), pr,
+			    ok ? (int)(4u * (((uint32_t)split * 16u + t) * (uint32_t)vrows + vrow)) : (int)kBufNone, 0, 0);
+		} else {
+			const int ld = __builtin_amdgcn_readfirstlane(S.ld);
+			const __amdgpu_buffer_rsrc_t orr = stream_rsrc(uniform_ptr(S.out), (uint32_t)M * (uint32_t)ld * 4u);
+			const int off = ok && t < M ? (int)(4u * ((uint32_t)t * ld + wr)) : (int)kBufNone;
+			const float v = EPI == kSkAdd ? ev + sum : sum + ev;
+			__builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), orr, off, 0, 0);
 		}
 	};
 
-	// weights of three groups in flight: the one being folded and the next two
-	Q4SkBuf wb0[NBW], wb1[NBW], wb2[NBW];
-	int g = blockIdx.x;
-	wload(wb0, g);
+	// groups in flight: two in registers (X, Y), one in an LDS slot
+	uint4 X[PP], Y[PP];
+	float eX, eY, e0, e1;         // the epilogue operands of the groups in X, Y and the two LDS slots
+	SegView svX, svY, sv0, sv1;   // their segments
+	const int g0 = blockIdx.x;
+	gload(X, eX, svX, g0);
+	gload(Y, eY, svY, g0 + G);
 
 	// stage the q8 rows of the K range: piece c = (t, p) holds bytes 16p..
 	// of token t's range and, for even p, the scale of its sub-block p/2
@@ -262,7 +335,7 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 		const int PT = 16 * nbk;   // pieces per token
 		const __amdgpu_buffer_rsrc_t qrs = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
 		const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
-		constexpr int U = (16 * 16 * kQ4SkMaxBlocks + T - 1) / T;
+		constexpr int U = (16 * 16 * W + T - 1) / T;   // nbk <= W
 		uint4 qv[U];
 		float sv[U];
 #pragma unroll
@@ -296,23 +369,37 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 	// loads, waiting out the whole prefetch at every use of their registers)
 	__builtin_amdgcn_s_waitcnt(0);
 	__syncthreads();
-	wload(wb1, g + G);
+	if (live) {
+		const int8_t *arow_p = a_s + j * arow + wave * kQK + 8 * kq;   // token j, K-slice 8kq of each sub-block
+#pragma unroll
+		for (int sb = 0; sb < 8; sb++) av[sb] = *(const long *)(arow_p + 32 * sb);
+		nu0 = nu_s[(8 * wave + kq) * 16 + j];
+		nu1 = nu_s[(8 * wave + kq + 4) * 16 + j];
+	}
+	__syncthreads();   // the staging area becomes the weight slots
+	gstore(X, 0, 0);
+	sv0 = svX;
+	e0 = eX;
+	gload(X, eX, svX, g0 + 2 * G);
+	__syncthreads();
 
-	for (; g < ngroups; g += 3 * G) {
+	// iteration: fold the group in an LDS slot, park the older register set
+	// in the other slot, reload that set with the group three ahead, reduce
+	for (int g = g0; g < ngroups; g += 2 * G) {
 		float y[4];
-		wload(wb2, g + 2 * G);
-		fold(wb0, y);
-		finish(y, g, 0);
-		wload(wb0, g + 3 * G);
-		if (g + G < ngroups) {
-			fold(wb1, y);
-			finish(y, g + G, 1);
-		}
-		wload(wb1, g + 4 * G);
-		if (g + 2 * G < ngroups) {
-			fold(wb2, y);
-			finish(y, g + 2 * G, 2);
-		}
+		fold(0, y);
+		gstore(Y, 1, 0);
+		sv1 = svY;
+		e1 = eY;
+		gload(Y, eY, svY, g + 3 * G);
+		finish(y, sv0, e0, g, 0);
+		if (g + G >= ngroups) break;
+		fold(1, y);
+		gstore(X, 0, 1);
+		sv0 = svX;
+		e0 = eX;
+		gload(X, eX, svX, g + 4 * G);
+		finish(y, sv1, e1, g + G, 1);
 	}
 }
 
@@ -608,6 +695,44 @@ size_t q4k_skinny_part_floats(int n_in, int vrows, int epi) {
 	return (ns > 1 || epi == kSkSwiGLU || epi == kSkPart) ? (size_t)ns * 16 * vrows : 0;
 }
 
+namespace {
+
+template <int W>
+int q4k_skinny_launch(const SkSegs &segs, bool direct, int epi, const int8_t *xq, const float *xs, int m, int n_in,
+                      int vrows, int ns, float *part) {
+	const int nb = n_in / kQK, ngroups = (vrows + 15) / 16;
+	const dim3 grid(ngroups < g_q4_target ? ngroups : g_q4_target, ns);
+	const size_t lds = q4sk_lds((nb + ns - 1) / ns, W);
+	static bool attr_set[64];   // per device
+	int dev = 0;
+	HK_HIP(hipGetDevice(&dev));
+	if (dev < 0 || dev >= 64) return set_error(HAKO_GPU_ENODEV, "device %d beyond the 64 the skinny launch tracks", dev);
+	if (!attr_set[dev]) {   // more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU)
+		const int max_lds = (int)q4sk_lds(W, W);
+		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkPart, W>,
+		                           hipFuncAttributeMaxDynamicSharedMemorySize, max_lds));
+		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkStore, W>,
+		                           hipFuncAttributeMaxDynamicSharedMemorySize, max_lds));
+		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkAdd, W>,
+		                           hipFuncAttributeMaxDynamicSharedMemorySize, max_lds));
+		attr_set[dev] = true;
+	}
+	const dim3 block(64 * W);
+	if (!direct)
+		hipLaunchKernelGGL((q4k_skinny_kernel<kSkPart, W>), grid, block, lds, stream(), segs, xq, xs, m, n_in, vrows,
+		                   ns, part);
+	else if (epi == kSkStore)
+		hipLaunchKernelGGL((q4k_skinny_kernel<kSkStore, W>), grid, block, lds, stream(), segs, xq, xs, m, n_in, vrows,
+		                   1, part);
+	else
+		hipLaunchKernelGGL((q4k_skinny_kernel<kSkAdd, W>), grid, block, lds, stream(), segs, xq, xs, m, n_in, vrows, 1,
+		                   part);
+	HK_LAUNCHED("q4k_skinny");
+	return HAKO_GPU_OK;
+}
+
+}  // namespace
+
 int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows,
                float *part, size_t part_cap) {
 	const int ns = q4k_skinny_splits(n_in, vrows), nb = n_in / kQK;
@@ -615,34 +740,11 @@ int q4k_skinny(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, i
 	if (!direct && (!part || part_cap < q4k_skinny_part_floats(n_in, vrows, epi)))
 		return set_error(HAKO_GPU_EINVAL, "Q4_K skinny split needs a workspace of %zu floats (has %zu)",
 		                 q4k_skinny_part_floats(n_in, vrows, epi), part ? part_cap : (size_t)0);
-	const int ngroups = (vrows + 15) / 16;
-	const dim3 grid(ngroups < g_q4_target ? ngroups : g_q4_target, ns);
-	const size_t lds = q4sk_lds((nb + ns - 1) / ns, kQ4SkWaves);
-	static bool attr_set[64];   // per device
-	int dev = 0;
-	HK_HIP(hipGetDevice(&dev));
-	if (dev < 0 || dev >= 64) return set_error(HAKO_GPU_ENODEV, "device %d beyond the 64 the skinny launch tracks", dev);
-	if (!attr_set[dev]) {   // more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU)
-		const size_t max_lds = q4sk_lds(kQ4SkMaxBlocks, kQ4SkWaves);
-		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkPart, kQ4SkWaves>,
-		                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds));
-		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkStore, kQ4SkWaves>,
-		                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds));
-		HK_HIP(hipFuncSetAttribute((const void *)q4k_skinny_kernel<kSkAdd, kQ4SkWaves>,
-		                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds));
-		attr_set[dev] = true;
-	}
-	const dim3 block(64 * kQ4SkWaves);
-	if (!direct)
-		hipLaunchKernelGGL((q4k_skinny_kernel<kSkPart, kQ4SkWaves>), grid, block, lds, stream(), segs, xq, xs, m, n_in,
-		                   vrows, ns, part);
-	else if (epi == kSkStore)
-		hipLaunchKernelGGL((q4k_skinny_kernel<kSkStore, kQ4SkWaves>), grid, block, lds, stream(), segs, xq, xs, m,
-		                   n_in, vrows, 1, part);
-	else
-		hipLaunchKernelGGL((q4k_skinny_kernel<kSkAdd, kQ4SkWaves>), grid, block, lds, stream(), segs, xq, xs, m, n_in,
-		                   vrows, 1, part);
-	HK_LAUNCHED("q4k_skinny");
+	// a wave per super-block of the split: 8 waves up to 8 blocks, else 16
+	const int nbk = (nb + ns - 1) / ns;
+	const int rc = nbk <= 8 ? q4k_skinny_launch<8>(segs, direct, epi, xq, xs, m, n_in, vrows, ns, part)
+	                        : q4k_skinny_launch<16>(segs, direct, epi, xq, xs, m, n_in, vrows, ns, part);
+	if (rc) return rc;
 	return (direct || epi == kSkPart) ? HAKO_GPU_OK : reduce(segs, epi, part, ns, m, vrows);
 }
 
