@@ -449,10 +449,13 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 	const int vrow = wrow0 + j, wr = vrow - S.row0;
 	const bool ok = vrow < vrows && wr < S.rows;
 	const uint32_t rb = (uint32_t)NB * kQ6Bytes;
-	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, (uint32_t)S.rows * rb);   // the wave's segment
-	// staging loads: piece lp of row 4i + lr (i = 0..3), and d of row `lane`;
-	// rows outside the segment or the launch, pieces 13..15 and lanes 16..63
-	// of the d load read nothing
+	// Every load and LDS store below is issued unconditionally: a lane with
+	// nothing to load has an offset past its stream, a block past the range
+	// loads through a descriptor of zero bytes (zeros, no memory access), and
+	// a lane with nothing to store writes a pad. A branch around them makes
+	// the wait-count pass wait for every load in flight.
+	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(S.w, (uint32_t)S.rows * rb), wnone = stream_rsrc(S.w, 0);
+	// staging loads: piece lp of row 4i + lr (i = 0..3), and d of row `lane`
 	const int lp = lane & 15, lr = lane >> 4;
 	uint32_t srow_off[4];
 #pragma unroll
@@ -466,24 +469,34 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 		d_off = (lane < 16 && r < vrows && rr < S.rows) ? (uint32_t)rr * rb + 208u : kBufNone;
 	}
 	uint8_t *wt = w_s[wave];
-	const __amdgpu_buffer_rsrc_t hrs = stream_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
-	const __amdgpu_buffer_rsrc_t lrs = stream_rsrc(xl, (uint32_t)M * (uint32_t)K * 2u);
+	// LDS targets of the staged pieces (pieces 13..15: the row's pad at 224)
+	// and of d (lanes 16..63: pad bytes 210..215 of row lane%16)
+	const int pcol = lp < kQ6Pieces ? 16 * lp : 224;
+	const int dpos = lane < 16 ? lane * kQ6TileRow + 208 : (lane & 15) * kQ6TileRow + 210 + 2 * ((lane >> 4) - 1);
+	const uint32_t hbytes = (uint32_t)M * (uint32_t)K * 2u;
+	const __amdgpu_buffer_rsrc_t hrs = stream_rsrc(xh, hbytes), lrs = stream_rsrc(xl, hbytes);
+	const __amdgpu_buffer_rsrc_t hnone = stream_rsrc(xh, 0), lnone = stream_rsrc(xl, 0);
+	const __amdgpu_buffer_rsrc_t ers = stream_rsrc(esc, BLK ? (uint32_t)M * (uint32_t)NB * 4u : 0u);
+	const __amdgpu_buffer_rsrc_t enone = stream_rsrc(esc, 0);
 	const int t0 = 4 * kq;
 
-	auto issue = [&](uint4 (&wv)[4], uint32_t &dv, int kb) {
+	struct WBuf {
+		uint4 v[4];
+		uint32_t d;
+	};
+	auto issue = [&](WBuf &w, int kb) {
+		const __amdgpu_buffer_rsrc_t r = kb < kb_end ? wrs : wnone;
+		const int so = kb * kQ6Bytes;
 #pragma unroll
 		for (int i = 0; i < 4; i++)
-			wv[i] = ld_b128(wrs, kb < kb_end && srow_off[i] != kBufNone ? srow_off[i] + (uint32_t)kb * kQ6Bytes
-			                                                             : kBufNone);
-		dv = ld_b16(wrs, kb < kb_end && d_off != kBufNone ? d_off + (uint32_t)kb * kQ6Bytes : kBufNone);
+			w.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)srow_off[i], so, 0));
+		w.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)d_off, so, 0);
 	};
 	// the staged pieces to the wave's tile, then this lane's fields of row j
-	auto unstage = [&](const uint4 (&wv)[4], uint32_t dv, Q6SkBuf &b) {
-		if (lp < kQ6Pieces) {
+	auto unstage = [&](const WBuf &w, Q6SkBuf &b) {
 #pragma unroll
-			for (int i = 0; i < 4; i++) *(uint4 *)(wt + (4 * i + lr) * kQ6TileRow + 16 * lp) = wv[i];
-		}
-		if (lane < 16) *(uint16_t *)(wt + lane * kQ6TileRow + 208) = (uint16_t)dv;
+		for (int i = 0; i < 4; i++) *(uint4 *)(wt + (4 * i + lr) * kQ6TileRow + pcol) = w.v[i];
+		*(uint16_t *)(wt + dpos) = (uint16_t)w.d;
 		__builtin_amdgcn_wave_barrier();
 		const uint8_t *row = wt + j * kQ6TileRow;
 #pragma unroll
@@ -497,37 +510,51 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 		b.d = *(const uint16_t *)(row + 208);
 		__builtin_amdgcn_wave_barrier();   // read before the next block's pieces land
 	};
-	// activation stage of block kb: 16 tokens x 256 K of hi and lo (zeros past M)
-	uint4 hreg[2], lreg[2];
-	float ereg = 0.0f;
-	const __amdgpu_buffer_rsrc_t ers = stream_rsrc(esc, BLK ? (uint32_t)M * (uint32_t)NB * 4u : 0u);
-	auto load_stage = [&](int kb) {
+	// activation stage of block kb: 16 tokens x 256 K of hi and lo (zeros
+	// past M) and, BLK, esc[t][kb] of token tid%16 (every thread: the same
+	// value lands in es_s from sixteen threads)
+	struct Stage {
+		uint4 h[2], l[2];
+		float e;
+	};
+	auto load_stage = [&](Stage &a, int kb) {
+		const bool in = kb < kb_end;
 #pragma unroll
 		for (int u = 0; u < 2; u++) {
 			const int c = tid + kT * u, t = c >> 5, p = c & 31;   // 16 tokens x 32 pieces of 8 fp16
-			const uint32_t off = t < M ? 2u * ((uint32_t)t * K + kQK * kb + 8 * p) : kBufNone;
-			hreg[u] = ld_b128(hrs, off);
-			lreg[u] = ld_b128(lrs, off);
+			const int off = t < M ? (int)(2u * ((uint32_t)t * K + 8 * p)) : (int)kBufNone;
+			a.h[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(in ? hrs : hnone, off, kb * 512, 0));
+			a.l[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(in ? lrs : lnone, off, kb * 512, 0));
 		}
-		if (BLK)   // tokens past M: zero (their activations are zero too)
-			ereg = __builtin_bit_cast(float, ld_b32(ers, tid < M ? 4u * ((uint32_t)tid * NB + kb) : kBufNone));
+		a.e = 0.0f;
+		if (BLK) {
+			const int t = tid & 15;
+			a.e = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+			                                    in ? ers : enone, t < M ? (int)(4u * ((uint32_t)t * NB)) : (int)kBufNone,
+			                                    kb * 4, 0));
+		}
 	};
-	auto store_stage = [&](int slot) {
+	auto store_stage = [&](const Stage &a, int slot) {
 #pragma unroll
 		for (int u = 0; u < 2; u++) {
 			const int c = tid + kT * u, t = c >> 5, p = c & 31;
-			*(uint4 *)(ah_s[slot] + t * kHPadSk + 8 * p) = hreg[u];
-			*(uint4 *)(al_s[slot] + t * kHPadSk + 8 * p) = lreg[u];
+			*(uint4 *)(ah_s[slot] + t * kHPadSk + 8 * p) = a.h[u];
+			*(uint4 *)(al_s[slot] + t * kHPadSk + 8 * p) = a.l[u];
 		}
-		if (BLK && tid < 16) es_s[slot][tid] = ereg;
+		if (BLK) es_s[slot][tid & 15] = a.e;
 	};
 
-	uint4 wv0[4], wv1[4];
-	uint32_t dv0, dv1;
-	issue(wv0, dv0, kb_beg);
-	issue(wv1, dv1, kb_beg + 1);
-	load_stage(kb_beg);
-	store_stage(0);
+	// in flight: the weights of the next two blocks (W0, W1) and the stages
+	// of the next two (S0, S1); weights of block kb + 2 and the stage of
+	// kb + 3 are issued while block kb is folded
+	WBuf W0, W1;
+	Stage A0, A1;
+	issue(W0, kb_beg);
+	load_stage(A0, kb_beg);
+	issue(W1, kb_beg + 1);
+	load_stage(A1, kb_beg + 1);
+	store_stage(A0, 0);
+	load_stage(A0, kb_beg + 2);
 	__syncthreads();
 	v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 	const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -535,12 +562,12 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 #pragma unroll
 		for (int half = 0; half < 2; half++) {
 			const int kb = kb0 + half;
+			WBuf &W = half ? W1 : W0;
+			Stage &A = half ? A0 : A1;   // the stage of kb + 1
+			Q6SkBuf b;
+			unstage(W, b);
+			issue(W, kb + 2);
 			if (kb < kb_end) {
-				const bool more = kb + 1 < kb_end;
-				if (more) load_stage(kb + 1);
-				Q6SkBuf b;
-				unstage(half ? wv1 : wv0, half ? dv1 : dv0, b);
-				issue(half ? wv1 : wv0, half ? dv1 : dv0, kb + 2);
 				const _Float16 *ah = ah_s[half] + j * kHPadSk + 4 * kq;
 				const _Float16 *al = al_s[half] + j * kHPadSk + 4 * kq;
 				const float dd = f16_to_f32(b.d);
@@ -560,17 +587,17 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 					const v4h wv = {w01[0], w01[1], w23[0], w23[1]};
 					v4f pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(ah + 16 * gg), wv, zero, 0, 0, 0);
 					pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(al + 16 * gg), wv, pr, 0, 0, 0);
-					const float s = dd * (float)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 0xFFu);
+					const float sgg = dd * (float)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 0xFFu);
 					if (BLK) {
-						accb[0] = __builtin_fmaf(pr[0], s, accb[0]);
-						accb[1] = __builtin_fmaf(pr[1], s, accb[1]);
-						accb[2] = __builtin_fmaf(pr[2], s, accb[2]);
-						accb[3] = __builtin_fmaf(pr[3], s, accb[3]);
+						accb[0] = __builtin_fmaf(pr[0], sgg, accb[0]);
+						accb[1] = __builtin_fmaf(pr[1], sgg, accb[1]);
+						accb[2] = __builtin_fmaf(pr[2], sgg, accb[2]);
+						accb[3] = __builtin_fmaf(pr[3], sgg, accb[3]);
 					} else {
-						acc[0] = __builtin_fmaf(pr[0], s, acc[0]);
-						acc[1] = __builtin_fmaf(pr[1], s, acc[1]);
-						acc[2] = __builtin_fmaf(pr[2], s, acc[2]);
-						acc[3] = __builtin_fmaf(pr[3], s, acc[3]);
+						acc[0] = __builtin_fmaf(pr[0], sgg, acc[0]);
+						acc[1] = __builtin_fmaf(pr[1], sgg, acc[1]);
+						acc[2] = __builtin_fmaf(pr[2], sgg, acc[2]);
+						acc[3] = __builtin_fmaf(pr[3], sgg, acc[3]);
 					}
 				}
 				if (BLK) {
@@ -582,11 +609,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 					acc[2] = __builtin_fmaf(accb[2], eb.z, acc[2]);
 					acc[3] = __builtin_fmaf(accb[3], eb.w, acc[3]);
 				}
-				if (more) {
-					store_stage(half ^ 1);
-					__syncthreads();
-				}
 			}
+			store_stage(A, half ^ 1);
+			load_stage(A, kb + 3);
+			__syncthreads();
 		}
 	}
 	float y[4];
@@ -757,8 +783,8 @@ int swiglu_split(const float *part, int nsplit, int F, int m, _Float16 *xh, _Flo
 
 int q6k_skinny_splits(int n_in, int vrows) {
 	const int tiles = (vrows + kRowsWg - 1) / kRowsWg, nb = n_in / kQK;
-	int ns = (g_q6_target + tiles - 1) / tiles;        // enough workgroups to fill the chip
-	ns = ns > nb / 4 ? nb / 4 : ns;                    // at least four super-blocks per split
+	int ns = g_q6_target / tiles;   // workgroups to fill the chip, all resident at once
+	ns = ns > nb / 4 ? nb / 4 : ns;  // at least four super-blocks per split
 	return ns < 1 ? 1 : ns;
 }
 
