@@ -37,7 +37,7 @@ HBM_PEAK_GBPS = 8000.0            # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0           # MI355X dense int8 matrix cores
 FP16_PEAK_TFLOPS = 2500.0         # MI355X dense fp16 matrix cores
 ROTATION_BYTES = 512 << 20        # > 256 MB Infinity Cache
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "q4k_gemv_11008x2048_traffic.json")
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "matmul_traffic.json")
 
 
 def log(*a):
@@ -109,7 +109,14 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
         # the timed launches start on the weight copy after the warm-up's last,
         # so none of them finds its weights left in the last-level cache
         warm, timed = capture(0, max(warmup, 1)), capture(max(warmup, 1), steps)
+        # the warm-up graph replayed for at least 30 ms: a GPU idle during the
+        # host-side set-up runs its first milliseconds at lower clocks
+        g.record(e0)
         g.graph_launch(warm)
+        g.record(e1)
+        reps = int(math.ceil(30.0 / max(g.elapsed_ms(e0, e1), 1e-3)))
+        for _ in range(min(reps, 1000)):
+            g.graph_launch(warm)
         g.sync()
         g.record(e0)
         g.graph_launch(timed)
@@ -453,21 +460,28 @@ def bench_prefill(g, launches: int, eager: bool = False, cpu: bool = False) -> d
         ops = 2.0 * m * n_out * n_in
         tops = ops / (r["us_per_launch"] * 1e-6) / 1e12
         peak = INT8_PEAK_TOPS if qt == synth.TYPE_Q4_K else FP16_PEAK_TFLOPS
+        traffic, ratio = read_traffic(("q4k_gemm_7b_ffn_up_512x18944x3584" if qt == synth.TYPE_Q4_K
+                                       else "q6k_gemm_7b_ffn_down_512x3584x18944"))
         out[name] = {"us_per_launch": round(r["us_per_launch"], 2), "tops": round(tops, 1),
                      "peak": peak, "frac": round(tops / peak, 4),
-                     "unit": "TOPS (int8)" if qt == synth.TYPE_Q4_K else "TFLOP/s (fp16 matrix cores)"}
+                     "unit": "TOPS (int8)" if qt == synth.TYPE_Q4_K else "TFLOP/s (fp16 matrix cores)",
+                     "traffic": traffic, "traffic_over_algorithmic": ratio}
         if cpu:
             out[name]["cpu_baseline"] = cpu_prefill_baseline(qt, m, n_out, n_in, n_out)
     return out
 
 
-def read_traffic():
+def read_traffic(name: str):
+    """HBM bytes per launch (fetched + written) of workload `name` from the
+    calibrated rocprofv3 counter summary, and their ratio to the algorithmic
+    bytes; (None, None) when the summary has no entry."""
     try:
         with open(TRAFFIC_FILE) as f:
-            t = json.load(f)
-        return float(t["fetch_bytes_per_launch"]) + float(t["write_bytes_per_launch"])
+            t = json.load(f)["workloads"][name]
+        total = float(t["fetch_bytes_per_launch"]) + float(t["write_bytes_per_launch"])
+        return total, round(total / float(t["algorithmic_bytes_per_launch"]), 3)
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
 
 
 # name -> (type, n_out, n_in, default steps); the first is the headline.
@@ -542,9 +556,11 @@ def main():
                 continue
             r = bench_gemv(g, qt, n_out, n_in, steps, 20, seed=n_out)
             log(f"{name}: {r['us_per_launch']:.2f} us/launch, {r['gbps']:.0f} GB/s")
+            traffic, ratio = read_traffic(name)
             extra[name] = {"us_per_launch": round(r["us_per_launch"], 3), "gbps": round(r["gbps"], 1),
                            "hbm_frac": round(r["gbps"] / HBM_PEAK_GBPS, 4),
-                           "single_launch_us": round(r["single_launch_us"], 3)}
+                           "single_launch_us": round(r["single_launch_us"], 3),
+                           "traffic": traffic, "traffic_over_algorithmic": ratio}
             if not args.no_cpu:
                 # copies kept to about 1.3 GB of host memory for the vocab shape
                 extra[name]["cpu_baseline"] = cpu_gemv_baseline(qt, n_out, n_in, args.cpu_seconds / 4, seed=n_out,
@@ -589,7 +605,7 @@ def main():
                    "timing": "HIP graph of K launches between two HIP events on the library stream"},
         "hbm_frac": round(value / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": read_traffic()},
+                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": read_traffic(HEADLINE)[0]},
         "cpu_baseline": cpu,
         "single_launch_us": round(head["single_launch_us"], 3),
         "extra": extra,

@@ -55,6 +55,17 @@ __device__ __forceinline__ int xcd_tile(int b, int ntiles) {
 	return (b % kXcds) * per + b / kXcds;
 }
 
+// Tile t of an XCD-contiguous order to its (token tile, row tile): groups of
+// gm token tiles, row tiles major and token tiles minor within a group. An
+// XCD's range of tiles then covers gm token tiles x (its share of) the row
+// tiles, and the tiles that share a row tile's weights (or a token tile's
+// activations) run on one XCD at the same time, sharing its L2.
+__device__ __forceinline__ void tile_mn(int t, int ntiles, int gm, int &mt, int &nt) {
+	const int span = gm * ntiles, g = t / span, r = t - g * span;
+	nt = r / gm;
+	mt = g * gm + (r - nt * gm);
+}
+
 __device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 	return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
@@ -71,7 +82,7 @@ constexpr int kAPad = 272;   // bytes per staged token row: 256 + 16 (conflict-f
 // the same up rows (segment 1); out (segment 0's) = silu(gate)*up.
 template <int EPI>
 __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const int8_t *__restrict__ xq,
-                                                       const float *__restrict__ xs, int M, int N, int K) {
+                                                       const float *__restrict__ xs, int M, int N, int K, int gm) {
 	__shared__ __align__(16) uint8_t w_s[kTN * kQ4Bytes];   // this stage's block of each row
 	__shared__ __align__(16) int8_t a_s[kTM * kAPad];       // this stage's 256 xq of each token
 	__shared__ __align__(16) float ds_s[8][kTN];            // d*s   [sub-block][row]
@@ -81,7 +92,9 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const 
 	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
 	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
 	if (tile >= mtiles * ntiles) return;
-	const int m0 = (tile / ntiles) * kTM, n0 = (tile % ntiles) * kTN;
+	int mt, nt;
+	tile_mn(tile, ntiles, gm, mt, nt);
+	const int m0 = mt * kTM, n0 = nt * kTN;
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 	const int wr = wave & 1, wt = wave >> 1, li = lane & 31, kh = lane >> 5;
@@ -333,7 +346,7 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
                                                        const _Float16 *__restrict__ xl,
                                                        const float *__restrict__ esc,
                                                        const float *__restrict__ bias,
-                                                       float *__restrict__ y, int M, int N, int K, int add) {
+                                                       float *__restrict__ y, int M, int N, int K, int add, int gm) {
 	__shared__ __align__(16) _Float16 ah_s[kTM * kHPad];   // activation hi [token][k]
 	__shared__ __align__(16) _Float16 al_s[kTM * kHPad];   // activation lo
 	__shared__ __align__(16) _Float16 wq_s[kTN * kHPad];   // q - 32 [row][k]
@@ -342,7 +355,9 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
 	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
 	if (tile >= mtiles * ntiles) return;
-	const int m0 = (tile / ntiles) * kTM, n0 = (tile % ntiles) * kTN;
+	int mt, nt;
+	tile_mn(tile, ntiles, gm, mt, nt);
+	const int m0 = mt * kTM, n0 = nt * kTN;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int wr = wave & 1, wt = wave >> 1, li = lane & 31, kh = lane >> 5;
 	const int NB = K >> 8;
@@ -461,6 +476,26 @@ int skinny_split_workspace(size_t floats, float **part) {
 	return HAKO_GPU_OK;
 }
 
+// Token tiles per XCD group (tile_mn): the divisor of the token tiles that
+// minimizes what one XCD reads, gm token tiles of act_tile bytes each plus
+// its share of the row tiles of w_tile bytes each.
+int gemm_gm(int M, int N, double act_tile, double w_tile) {
+	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
+	const double per = (double)mtiles * ntiles / kXcds;
+	int best = 1;
+	double best_bytes = 1e300;
+	for (int gm = 1; gm <= mtiles; gm++) {
+		if (mtiles % gm) continue;
+		const double rows = per / gm < 1.0 ? 1.0 : per / gm;
+		const double bytes = gm * act_tile + rows * w_tile;
+		if (bytes < best_bytes) {
+			best_bytes = bytes;
+			best = gm;
+		}
+	}
+	return best;
+}
+
 int gemm_grid(int M, int N) {
 	const int tiles = ((M + kTM - 1) / kTM) * ((N + kTN - 1) / kTN);
 	return kXcds * ((tiles + kXcds - 1) / kXcds);
@@ -512,10 +547,11 @@ int q4k_gemm_segs(const SkSegs &segs, int epi, const int8_t *xq, const float *xs
 	}
 	const int N = epi == kSkSwiGLU ? 2 * segs.s[0].rows : vrows;
 	const dim3 grid(gemm_grid(m, N));
+	const int gm = gemm_gm(m, N, (double)kTM * (n_in + n_in / 32 * 4), (double)kTN * (n_in / kQK) * kQ4Bytes);
 	switch (epi) {
-	case kSkStore: hipLaunchKernelGGL(q4k_gemm_kernel<kSkStore>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in); break;
-	case kSkAdd: hipLaunchKernelGGL(q4k_gemm_kernel<kSkAdd>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in); break;
-	case kSkSwiGLU: hipLaunchKernelGGL(q4k_gemm_kernel<kSkSwiGLU>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in); break;
+	case kSkStore: hipLaunchKernelGGL(q4k_gemm_kernel<kSkStore>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in, gm); break;
+	case kSkAdd: hipLaunchKernelGGL(q4k_gemm_kernel<kSkAdd>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in, gm); break;
+	case kSkSwiGLU: hipLaunchKernelGGL(q4k_gemm_kernel<kSkSwiGLU>, grid, dim3(kGT), 0, stream(), segs, xq, xs, m, N, n_in, gm); break;
 	default: return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM epilogue %d", epi);
 	}
 	HK_LAUNCHED("q4k_gemm");
@@ -556,8 +592,9 @@ int q6k_gemm_split(float *y, const void *w, const _Float16 *xh, const _Float16 *
                    const float *bias, int m, int n_out, int n_in, bool add) {
 	if (int rc = check_gemm("Q6_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ6Bytes, w)) return rc;
 	if (m <= kSkMaxTokens) return set_error(HAKO_GPU_EINVAL, "Q6_K GEMM on split rows needs m > %d", kSkMaxTokens);
+	const int gm = gemm_gm(m, n_out, (double)kTM * n_in * 4, (double)kTN * (n_in / kQK) * kQ6Bytes);
 	hipLaunchKernelGGL(q6k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
-	                   xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0);
+	                   xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0, gm);
 	HK_LAUNCHED("q6k_gemm");
 	return ok();
 }

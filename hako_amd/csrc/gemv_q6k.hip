@@ -346,7 +346,7 @@ int g_q6_flat_items = -1;
 // wider rows and tall matrices the persistent grid.
 int q6_flat_items_for(int n_out, const Q6Geom &G) {
 	if (g_q6_flat_items >= 0) return g_q6_flat_items;
-	if (G.C > 64 && G.tpr <= 6) return 4;
+	if (G.C > 64 && G.tpr <= 6 && n_out <= 8192) return 4;   // past ~8K rows the persistent grid streams faster
 	if (G.C <= 64 && n_out <= 4096) return 1;
 	return 0;
 }
