@@ -66,9 +66,6 @@ __device__ __forceinline__ void tile_mn(int t, int ntiles, int gm, int &mt, int 
 	mt = g * gm + (r - nt * gm);
 }
 
-__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-	return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
-}
 
 // ── Q4_K x q8 ──
 
@@ -250,19 +247,30 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const 
 		}
 		return;
 	}
-	if (tok >= M) return;
-	float *yr = S.out + (size_t)tok * S.ld;
+	// Store / Add: every operand load (the bias, or the output the sums are
+	// added to) first, then the stores; lanes past the rows or tokens use an
+	// offset past the stream (no access), so no branch separates the loads
+	// and each does not wait for the one before
+	const int ld = __builtin_amdgcn_readfirstlane(S.ld), srows = __builtin_amdgcn_readfirstlane(S.rows);
+	float *out = uniform_ptr(S.out);
+	const float *bias = uniform_ptr(S.bias);
+	const __amdgpu_buffer_rsrc_t ors = stream_rsrc(out, (uint32_t)M * (uint32_t)ld * 4u);
+	const __amdgpu_buffer_rsrc_t brs =
+	    stream_rsrc(bias ? (const void *)bias : (const void *)out, (EPI == kSkStore && bias) ? (uint32_t)srows * 4u : 0u);
+	uint32_t off[16];
+	float ev[16];
 #pragma unroll
 	for (int q4 = 0; q4 < 4; q4++) {
 		const int row = r0 + 32 * wr + 8 * q4 + 4 * kh;
 #pragma unroll
-		for (int r = 0; r < 4; r++)
-			if (row + r < S.rows) {
-				const float v = acc[4 * q4 + r] + accm[4 * q4 + r];
-				if (EPI == kSkAdd) yr[row + r] += v;
-				else yr[row + r] = S.bias ? v + S.bias[row + r] : v;
-			}
+		for (int r = 0; r < 4; r++) {
+			const bool ok = tok < M && row + r < srows;
+			off[4 * q4 + r] = ok ? 4u * ((uint32_t)tok * ld + row + r) : kBufNone;
+			ev[4 * q4 + r] = EPI == kSkAdd ? ld_f32(ors, off[4 * q4 + r]) : ld_f32(brs, ok ? 4u * (row + r) : kBufNone);
+		}
 	}
+#pragma unroll
+	for (int v = 0; v < 16; v++) st_f32(ors, off[v], EPI == kSkAdd ? ev[v] + (acc[v] + accm[v]) : (acc[v] + accm[v]) + ev[v]);
 }
 
 // ── Q6_K x fp32 ──
@@ -451,18 +459,30 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 		}
 		__syncthreads();
 	}
-	// lane: row n0+32wr+li, tokens m0+32wt+8q4+4kh+r
+	// lane: row n0+32wr+li, tokens m0+32wt+8q4+4kh+r. Every operand load
+	// (token scales, bias, the output added to) first, then the stores;
+	// lanes past the rows or tokens use an offset past the stream
 	const int row = n0 + 32 * wr + li;
-	if (row >= N) return;
-	const float bv = bias ? bias[row] : 0.0f;
+	const bool rok = row < N;
+	const __amdgpu_buffer_rsrc_t yrs = stream_rsrc(y, (uint32_t)M * (uint32_t)N * 4u);
+	const __amdgpu_buffer_rsrc_t ars = stream_rsrc(y, add ? (uint32_t)M * (uint32_t)N * 4u : 0u);
+	const __amdgpu_buffer_rsrc_t ers = stream_rsrc(esc, (uint32_t)M * 4u);
+	const __amdgpu_buffer_rsrc_t brs = stream_rsrc(bias ? (const void *)bias : (const void *)esc, bias ? (uint32_t)N * 4u : 0u);
+	const float bv = ld_f32(brs, rok ? 4u * row : kBufNone);
+	uint32_t off[16];
+	float ev[16], ov[16];
 #pragma unroll
 	for (int v = 0; v < 16; v++) {
 		const int tok = m0 + 32 * wt + 8 * (v >> 2) + 4 * kh + (v & 3);
-		if (tok < M) {
-			float *o = y + (size_t)tok * N + row;
-			const float r = acc[v] * esc[tok] + bv;
-			*o = add ? *o + r : r;
-		}
+		const bool ok = rok && tok < M;
+		off[v] = ok ? 4u * ((uint32_t)tok * N + row) : kBufNone;
+		ev[v] = ld_f32(ers, ok ? 4u * tok : kBufNone);
+		ov[v] = ld_f32(ars, off[v]);
+	}
+#pragma unroll
+	for (int v = 0; v < 16; v++) {
+		const float r = acc[v] * ev[v] + bv;
+		st_f32(yrs, off[v], add ? ov[v] + r : r);
 	}
 }
 

@@ -120,6 +120,20 @@ constexpr uint32_t kBufNone = 0x80000000u; // an offset past every stream (strea
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const void *base, uint32_t bytes) {
 	return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufFlags);
 }
+// A pointer the compiler cannot prove wave-uniform (it is) in scalar
+// registers, so that a descriptor built on it needs no per-lane loop.
+template <class P>
+__device__ __forceinline__ P *uniform_ptr(P *p) {
+	const uint64_t v = (uint64_t)(uintptr_t)p;
+	const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+	return (P *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+	return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ void st_f32(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+	__builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)off, 0, 0);
+}
 __device__ __forceinline__ uint4 ld_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 	return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }

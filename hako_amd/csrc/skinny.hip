@@ -124,15 +124,6 @@ __host__ __device__ constexpr size_t q4sk_lds(int nbk, int W) {
 	return q4sk_region(nbk) + 2 * (size_t)nbk * 8 * 16 * 4 + (size_t)W * 16 * 8 * 4 + 2 * (size_t)W * 64 * 16;
 }
 
-// A pointer the compiler cannot prove wave-uniform (it is) in scalar
-// registers, so that a descriptor built on it needs no per-lane loop.
-template <class P>
-__device__ __forceinline__ P *uniform_ptr(P *p) {
-	const uint64_t v = (uint64_t)(uintptr_t)p;
-	const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-	return (P *)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
 // The segment of launch row r0 (uniform) with plain selects of its fields:
 // scalar selects, no copy of the argument block.
 __device__ __forceinline__ SegView seg_at(const SkSegs &s, int r0) {
