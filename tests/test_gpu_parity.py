@@ -203,7 +203,8 @@ def test_q4k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
     assert maxabs_rel(seen["fused"], want) < TOL
 
 
-Q6_SHAPES = [(2048, 11008), (151936, 2048), (3584, 18944), (256, 2048), (1, 256), (9, 768), (33, 11008)]
+Q6_SHAPES = [(2048, 11008), (151936, 2048), (3584, 18944), (256, 2048), (1, 256), (9, 768), (33, 11008),
+             (40000, 512), (5, 20480), (5, 32000)]
 
 
 @pytest.mark.parametrize("n_out,n_in", Q6_SHAPES)
@@ -214,6 +215,47 @@ def test_q6k_gemv_vs_oracle(gpu, oracle, n_out, n_in):
     got = gpu_matmul(gpu, Q6, w, x, n_out, n_in)
     want = oracle.matmul(Q6, w, x, n_out, n_in, f64=True, threads=16)
     assert maxabs_rel(got, want) < TOL
+
+
+@pytest.mark.parametrize("n_out,n_in", [(300, 2048), (40000, 768), (33, 11008)])
+def test_q6k_block_magnitudes(gpu, oracle, n_out, n_in):
+    """Activation blocks 1e-30 .. 1e30 apart, an all-zero block and a block of
+    subnormals, with a bias; then single blocks alone, each against the
+    oracle's float64 sums (not the subnormal one: the reference's fast-math
+    build flushes it to zero)."""
+    rng = np.random.default_rng(n_out + 3 * n_in)
+    nb = n_in // 256
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    mags = np.float32(10.0) ** rng.integers(-30, 31, nb).astype(np.float32)
+    x = (x.reshape(nb, 256) * mags[:, None]).astype(np.float32)
+    x[0] = 0.0
+    if nb > 2:
+        x[2] = (rng.standard_normal(256) * 1e-39).astype(np.float32)   # subnormal
+    x = x.reshape(-1)
+    bias = synth.activation(rng, n_out)
+    got = gpu_matmul(gpu, Q6, w, x, n_out, n_in, bias=bias)
+    want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True, threads=16)
+    assert maxabs_rel(got, want) < TOL
+    alone = [b for b in range(nb) if not (nb > 2 and b == 2)]
+    for b in rng.choice(alone, size=min(len(alone), 3), replace=False):
+        xb = np.zeros_like(x)
+        xb[256 * b:256 * b + 256] = x[256 * b:256 * b + 256]
+        got = gpu_matmul(gpu, Q6, w, xb, n_out, n_in)
+        want = oracle.matmul(Q6, w, xb, n_out, n_in, f64=True, threads=16)
+        assert maxabs_rel(got, want) < TOL, b
+
+
+@pytest.mark.parametrize("n_out,n_in", [(300, 2048), (40000, 512), (2048, 11008)])
+def test_q6k_nan_propagates(gpu, n_out, n_in):
+    """A NaN anywhere in the activation makes every output NaN, as the
+    reference's fp32 dot does (every weight multiplies it)."""
+    rng = np.random.default_rng(7)
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    x[n_in - 3] = np.nan
+    got = gpu_matmul(gpu, Q6, w, x, n_out, n_in)
+    assert np.all(np.isnan(got))
 
 
 HAKO_TUNE_Q6K_WGS_PER_CU, HAKO_TUNE_Q6K_WAVES, HAKO_TUNE_Q6K_FLAT_ITEMS = 2, 4, 8
