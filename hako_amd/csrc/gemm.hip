@@ -37,6 +37,7 @@
 #include "hako_dev.h"
 #include "hako_rt.h"
 #include "skinny.h"
+#include "q4k_dev.h"
 
 namespace hako {
 namespace {
@@ -44,6 +45,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 constexpr int kTM = 64, kTN = 64;   // tokens, weight rows per workgroup tile
@@ -78,7 +80,7 @@ constexpr int kAPad = 272;   // bytes per staged token row: 256 + 16 (conflict-f
 // residual), SwiGLU: N = 2F rows, tile j holds gate rows 32j.. (segment 0) and
 // the same up rows (segment 1); out (segment 0's) = silu(gate)*up.
 template <int EPI>
-__global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const int8_t *__restrict__ xq,
+__global__ __launch_bounds__(kGT, 3) void q4k_gemm_kernel(const SkSegs segs, const int8_t *__restrict__ xq,
                                                        const float *__restrict__ xs, int M, int N, int K, int gm) {
 	__shared__ __align__(16) uint8_t w_s[kTN * kQ4Bytes];   // this stage's block of each row
 	__shared__ __align__(16) int8_t a_s[kTM * kAPad];       // this stage's 256 xq of each token
@@ -107,86 +109,79 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const 
 	const __amdgpu_buffer_rsrc_t ars = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
 	const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
 
-	// Stage map: weights 64 rows x 9 pieces of 16 B (3 per thread; SwiGLU:
-	// each half of the workgroup 32 rows of its matrix), xq 64 tokens x 16
-	// pieces (4 per thread), xs 64 tokens x 8 (2 per thread).
-	auto wpiece = [&](int u, int &row, int &piece, int &srow) -> bool {   // tile row, piece, row in S
-		if (EPI == kSkSwiGLU) {
-			const int c = (tid & 127) + 128 * u;
-			row = 32 * (wave >> 1) + c / 9;
-			piece = c % 9;
-			srow = r0 + c / 9;
-			return c < 32 * 9;
-		}
-		const int c = tid + kGT * u;
-		row = c / 9;
-		piece = c - row * 9;
-		srow = r0 + row;
-		return c < kTN * 9;
-	};
-	uint4 wreg[3], areg[4];
-	float sreg[2];
+	// Stage map (one super-block of K per stage). Weights: the tile's 64 rows
+	// x 8 pieces of 16 qs bytes, 2 per thread; a thread's rows come from the
+	// matrix of its half of the workgroup (SwiGLU: threads 0-127 gate rows,
+	// 128-255 the same up rows), so each wave's descriptor is uniform. Each
+	// thread also loads the 16-byte header (d, dmin, scales) of row tid/4 and
+	// derives (d*s, dmin*m) of its sub-blocks 2(tid%4), 2(tid%4)+1.
+	// Activations: 64 tokens x 16 pieces of 16 xq bytes (half a sub-block),
+	// 4 per thread, all of piece tid%16: the two halves of a sub-block sit in
+	// neighbouring lanes, which add their sums of xq; and the q8 scale of each
+	// of the thread's four (token, sub-block) pairs.
+	const int half = tid >> 7;                       // matrix half of the tile
+	auto srow_of = [&](int row) { return r0 + (EPI == kSkSwiGLU ? row - 32 * half : row); };
+	const int wpc = tid & 7;                         // qs piece
+	const int hrow = tid >> 2, hg = tid & 3;         // header row, 64-weight group
+	const int apc = tid & 15, asb = apc >> 1;        // activation piece, its sub-block
+	uint4 wreg[2], hreg, areg[4];
+	float sreg[4];
 	auto load_stage = [&](int kb) {
+		const uint32_t kbo = (uint32_t)kb * kQ4Bytes;
 #pragma unroll
-		for (int u = 0; u < 3; u++) {
-			int row, piece, srow;
-			const bool on = wpiece(u, row, piece, srow) && srow < S.rows;
-			wreg[u] = ld_b128(wrs, on ? (uint32_t)srow * rb + (uint32_t)kb * kQ4Bytes + 16u * piece : kBufNone);
+		for (int u = 0; u < 2; u++) {
+			const int row = 32 * half + (((tid & 127) + 128 * u) >> 3), srow = srow_of(row);
+			wreg[u] = ld_b128(wrs, srow < S.rows ? (uint32_t)srow * rb + kbo + 16u + 16u * wpc : kBufNone);
+		}
+		{
+			const int srow = srow_of(hrow);
+			hreg = ld_b128(wrs, srow < S.rows ? (uint32_t)srow * rb + kbo : kBufNone);
 		}
 #pragma unroll
 		for (int u = 0; u < 4; u++) {
-			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
+			const int tok = (tid >> 4) + 16 * u;
 			const bool on = m0 + tok < M;
-			areg[u] = ld_b128(ars, on ? (uint32_t)(m0 + tok) * K + 256u * kb + 16u * piece : kBufNone);
-		}
-#pragma unroll
-		for (int u = 0; u < 2; u++) {
-			const int c = tid + kGT * u, tok = c >> 3, sb = c & 7;
-			const bool on = m0 + tok < M;
-			sreg[u] = ld_f32(srs, on ? 4u * ((uint32_t)(m0 + tok) * NS + 8u * kb + sb) : kBufNone);
+			areg[u] = ld_b128(ars, on ? (uint32_t)(m0 + tok) * K + 256u * kb + 16u * apc : kBufNone);
+			sreg[u] = ld_f32(srs, on ? 4u * ((uint32_t)(m0 + tok) * NS + 8u * kb + asb) : kBufNone);
 		}
 	};
+	// the loaded stage into LDS, with the per-row and per-token factors of the fold
 	auto store_stage = [&]() {
 #pragma unroll
-		for (int u = 0; u < 3; u++) {
-			int row, piece, srow;
-			if (wpiece(u, row, piece, srow)) *(uint4 *)(w_s + row * kQ4Bytes + 16 * piece) = wreg[u];
+		for (int u = 0; u < 2; u++) {
+			const int row = 32 * half + (((tid & 127) + 128 * u) >> 3);
+			*(uint4 *)(w_s + row * kQ4Bytes + 16 + 16 * wpc) = wreg[u];
+		}
+		{
+			uint32_t S2, M2;
+			q4_scales2(hreg.y, hreg.z, hreg.w, 16u * (hg & 1), hg >= 2 ? ~0u : 0u, S2, M2);
+			const float d = f16_to_f32(hreg.x & 0xFFFFu), dmin = f16_to_f32(hreg.x >> 16);
+			ds_s[2 * hg][hrow] = d * (float)(S2 & 0xFFu);
+			ds_s[2 * hg + 1][hrow] = d * (float)((S2 >> 8) & 0xFFu);
+			dm_s[2 * hg][hrow] = dmin * (float)(M2 & 0xFFu);
+			dm_s[2 * hg + 1][hrow] = dmin * (float)((M2 >> 8) & 0xFFu);
 		}
 #pragma unroll
 		for (int u = 0; u < 4; u++) {
-			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
-			*(uint4 *)(a_s + tok * kAPad + 16 * piece) = areg[u];
-		}
-	};
-	// per (row, sub-block): ds, dm; per (token, sub-block): xs, -xs*Σxq
-	auto derive = [&]() {
-#pragma unroll
-		for (int u = 0; u < 2; u++) {
-			const int c = tid + kGT * u, r = c >> 3, sb = c & 7;
-			const uint4 h = *(const uint4 *)(w_s + r * kQ4Bytes);
-			uint32_t s, m;
-			scale_min_k4((uint32_t)sb, h.y, h.z, h.w, s, m);
-			ds_s[sb][r] = f16_to_f32(h.x & 0xFFFFu) * (float)s;
-			dm_s[sb][r] = f16_to_f32(h.x >> 16) * (float)m;
-			const int4 *p = (const int4 *)(a_s + r * kAPad + 32 * sb);   // r doubles as the token here
-			const int4 p0 = p[0], p1 = p[1];
-			int ix = 0;
-			ix = sdot4(p0.x, 0x01010101, ix); ix = sdot4(p0.y, 0x01010101, ix);
-			ix = sdot4(p0.z, 0x01010101, ix); ix = sdot4(p0.w, 0x01010101, ix);
-			ix = sdot4(p1.x, 0x01010101, ix); ix = sdot4(p1.y, 0x01010101, ix);
-			ix = sdot4(p1.z, 0x01010101, ix); ix = sdot4(p1.w, 0x01010101, ix);
-			xn_s[sb][r] = make_float2(sreg[u], -sreg[u] * (float)ix);
+			const int tok = (tid >> 4) + 16 * u;
+			*(uint4 *)(a_s + tok * kAPad + 16 * apc) = areg[u];
+			int ix = sdot4((int)areg[u].x, 0x01010101, 0);
+			ix = sdot4((int)areg[u].y, 0x01010101, ix);
+			ix = sdot4((int)areg[u].z, 0x01010101, ix);
+			ix = sdot4((int)areg[u].w, 0x01010101, ix);
+			ix += dpp_i<kDppQuadSwap1>(ix);   // + the other half of the sub-block
+			// both lanes of the pair write the same value
+			xn_s[asb][tok] = make_float2(sreg[u], -sreg[u] * (float)ix);
 		}
 	};
 
 	v16f acc = {}, accm = {};
 	const v16i zero = {};
+	const v32f zero32 = {};
 	const uint32_t lo4 = 0x0F0F0F0Fu;
 	load_stage(0);
 	for (int kb = 0; kb < NB; kb++) {
 		store_stage();
-		__syncthreads();
-		derive();
 		__syncthreads();
 		if (kb + 1 < NB) load_stage(kb + 1);   // in flight during this stage's arithmetic
 		// The min term Σ_sb dm[row][sb] * (−xs*Σxq)[token][sb] is a small fp32
@@ -200,6 +195,12 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const 
 		}
 #pragma unroll
 		for (int g = 0; g < 4; g++) {
+			// The fold's scale products P[row][token] = (d*s)[row] * xs[token] of
+			// sub-blocks 2g and 2g+1 as one two-block outer product on the matrix
+			// cores (block h: lane half h supplies sub-block 2g+h), laid out like
+			// the int8 products: P[16h + v] pairs with d[v] of sub-block 2g+h.
+			const v32f P = __builtin_amdgcn_mfma_f32_32x32x1f32(ds_s[2 * g + kh][32 * wr + li],
+			                                                    xn_s[2 * g + kh][32 * wt + li].x, zero32, 0, 0, 0);
 			// weight row 32wr+li: qs bytes 32g+16kh.. hold K 16kh.. of sub-blocks 2g (low
 			// nibbles) and 2g+1 (high nibbles)
 			const uint4 q = *(const uint4 *)(w_s + (32 * wr + li) * kQ4Bytes + 16 + 32 * g + 16 * kh);
@@ -211,17 +212,8 @@ __global__ __launch_bounds__(kGT) void q4k_gemm_kernel(const SkSegs segs, const 
 				const int sb = 2 * g + h;
 				const v4i b = *(const v4i *)(a_s + (32 * wt + li) * kAPad + 32 * sb + 16 * kh);
 				const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? qhi : qlo, b, zero, 0, 0, 0);
-				const float xsj = xn_s[sb][32 * wt + li].x;
 #pragma unroll
-				for (int q4 = 0; q4 < 4; q4++) {
-					const float4 dsv = *(const float4 *)&ds_s[sb][32 * wr + 8 * q4 + 4 * kh];
-					const float dsa[4] = {dsv.x, dsv.y, dsv.z, dsv.w};
-#pragma unroll
-					for (int r = 0; r < 4; r++) {
-						const int v = 4 * q4 + r;
-						acc[v] = __builtin_fmaf((float)d[v], xsj * dsa[r], acc[v]);
-					}
-				}
+				for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)d[v], P[16 * h + v], acc[v]);
 			}
 		}
 		__syncthreads();   // before the next stage overwrites LDS

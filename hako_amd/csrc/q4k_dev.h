@@ -63,14 +63,24 @@ __device__ __forceinline__ void q4_isum(const Q4Buf &b, const Q4Col &c, int &ia,
 // split 6-bit layout of sub-blocks 4-7 (reference quant.c:57-66).
 // `hmask` is all ones for g >= 2, zero otherwise (a lane constant, blended
 // without branches).
-__device__ __forceinline__ float q4_fold(const Q4Buf &b, uint32_t sh, uint32_t hmask, int ia, int ib,
-                                         const Q4Col &c) {
-	const float d = f16_to_f32(b.h.x & 0xFFFFu), dmin = f16_to_f32(b.h.x >> 16);
-	const uint32_t a0 = b.h.y >> sh, a1 = b.h.z >> sh, a2 = b.h.w >> sh;
+// The 6-bit (scale, min) pairs of sub-blocks 2g and 2g+1 from the three
+// scale words of a block header: S holds s(2g) in bits 0-7 and s(2g+1) in
+// bits 8-15, M the mins alike.
+__device__ __forceinline__ void q4_scales2(uint32_t hy, uint32_t hz, uint32_t hw, uint32_t sh, uint32_t hmask,
+                                           uint32_t &S, uint32_t &M) {
+	const uint32_t a0 = hy >> sh, a1 = hz >> sh, a2 = hw >> sh;
 	const uint32_t s_lo = a0 & 0x3F3Fu, m_lo = a1 & 0x3F3Fu;
 	const uint32_t s_hi = (a2 & 0x0F0Fu) | ((a0 >> 2) & 0x3030u);
 	const uint32_t m_hi = ((a2 >> 4) & 0x0F0Fu) | ((a1 >> 2) & 0x3030u);
-	const uint32_t S = s_lo ^ ((s_lo ^ s_hi) & hmask), M = m_lo ^ ((m_lo ^ m_hi) & hmask);
+	S = s_lo ^ ((s_lo ^ s_hi) & hmask);
+	M = m_lo ^ ((m_lo ^ m_hi) & hmask);
+}
+
+__device__ __forceinline__ float q4_fold(const Q4Buf &b, uint32_t sh, uint32_t hmask, int ia, int ib,
+                                         const Q4Col &c) {
+	const float d = f16_to_f32(b.h.x & 0xFFFFu), dmin = f16_to_f32(b.h.x >> 16);
+	uint32_t S, M;
+	q4_scales2(b.h.y, b.h.z, b.h.w, sh, hmask, S, M);
 	const float sA = (float)(S & 0xFFu), sB = (float)((S >> 8) & 0xFFu);
 	const float mA = (float)(M & 0xFFu), mB = (float)((M >> 8) & 0xFFu);
 	const float t1 = (c.xsa * sA) * (float)ia + (c.xsb * sB) * (float)ib;
