@@ -341,7 +341,7 @@ __device__ __forceinline__ uint32_t q6_pair(uint32_t v, uint32_t sel) {
 constexpr int kQ6Stage = 128;        // K per stage: half a super-block
 constexpr int kHPad = kQ6Stage + 8;  // fp16 per staged row (272 B: conflict-free 16-byte reads)
 
-__global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restrict__ w,
                                                        const _Float16 *__restrict__ xh,
                                                        const _Float16 *__restrict__ xl,
                                                        const float *__restrict__ esc,
@@ -372,42 +372,57 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 	// (low nibbles) and that + 64 (high nibbles) of the half — with qh
 	// [32n+16(p%2), +16), and the scales 8n+2p, 8n+2p+1 and d.
 	const int wrow = tid >> 2, part = tid & 3;
-	uint4 hreg[4], lreg[4];
-	uint2 qlr[2], qhr[2];
-	uint32_t scr, dr;
-	auto load_stage = [&](int st) {
-		const int kb = st >> 1, n = st & 1;
+	// The activation loads of two stages are in flight while a third is
+	// computed: the workgroups per compute unit are bounded by LDS (two), not
+	// registers, so a second set of staging registers costs no occupancy,
+	// and one stage's arithmetic is too short to cover a load's latency by
+	// itself. The weight pieces (a sixth of the bytes) go one stage ahead.
+	struct Acts {
+		uint4 h[4], l[4];
+	};
+	struct Wts {
+		uint2 ql[2], qh[2];
+		uint32_t sc, d;
+	};
+	const int NSt = NB * 2;
+	// unconditional: a stage past the last loads nothing (out-of-range offsets)
+	auto load_acts = [&](Acts &r, int st) {
 		const uint32_t k0 = (uint32_t)kQ6Stage * st;
 #pragma unroll
 		for (int u = 0; u < 4; u++) {
 			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
-			const bool on = m0 + tok < M;
+			const bool on = st < NSt && m0 + tok < M;
 			const uint32_t off = on ? 2u * ((uint32_t)(m0 + tok) * K + k0 + 8u * piece) : kBufNone;
-			hreg[u] = ld_b128(hrs, off);
-			lreg[u] = ld_b128(lrs, off);
+			r.h[u] = ld_b128(hrs, off);
+			r.l[u] = ld_b128(lrs, off);
 		}
-		const bool on = n0 + wrow < N;
+	};
+	auto load_wts = [&](Wts &r, int st) {
+		const int kb = st >> 1, n = st & 1;
+		const bool on = st < NSt && n0 + wrow < N;
 		const uint32_t blk = on ? (uint32_t)(n0 + wrow) * rb + (uint32_t)kb * kQ6Bytes : kBufNone;
 		const uint32_t oql = 64u * n + 16u * part, oqh = 128u + 32u * n + 16u * (part & 1);
-		qlr[0] = ld_b64(wrs, blk + oql);
-		qlr[1] = ld_b64(wrs, blk + oql + 8);
-		qhr[0] = ld_b64(wrs, blk + oqh);
-		qhr[1] = ld_b64(wrs, blk + oqh + 8);
-		scr = ld_b16(wrs, blk + 192u + 8u * n + 2u * part);
-		dr = ld_b16(wrs, blk + 208u);
+		r.ql[0] = ld_b64(wrs, blk + oql);
+		r.ql[1] = ld_b64(wrs, blk + oql + 8);
+		r.qh[0] = ld_b64(wrs, blk + oqh);
+		r.qh[1] = ld_b64(wrs, blk + oqh + 8);
+		r.sc = ld_b16(wrs, blk + 192u + 8u * n + 2u * part);
+		r.d = ld_b16(wrs, blk + 208u);
 	};
-	auto store_stage = [&]() {
+	auto store_acts = [&](const Acts &r) {
 #pragma unroll
 		for (int u = 0; u < 4; u++) {
 			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
-			*(uint4 *)(ah_s + tok * kHPad + 8 * piece) = hreg[u];
-			*(uint4 *)(al_s + tok * kHPad + 8 * piece) = lreg[u];
+			*(uint4 *)(ah_s + tok * kHPad + 8 * piece) = r.h[u];
+			*(uint4 *)(al_s + tok * kHPad + 8 * piece) = r.l[u];
 		}
+	};
+	auto store_wts = [&](const Wts &r) {
 		// 6-bit values: low nibble | qh bits 2k1 (k1 = part/2) -> K 32k1 + l,
 		// high nibble | qh bits 2k1+4 -> K 32(k1+2) + l, with l = 16(part%2) + b.
 		const int k1 = part >> 1, l0 = 16 * (part & 1);
-		const uint32_t ql[4] = {qlr[0].x, qlr[0].y, qlr[1].x, qlr[1].y};
-		const uint32_t qh[4] = {qhr[0].x, qhr[0].y, qhr[1].x, qhr[1].y};
+		const uint32_t ql[4] = {r.ql[0].x, r.ql[0].y, r.ql[1].x, r.ql[1].y};
+		const uint32_t qh[4] = {r.qh[0].x, r.qh[0].y, r.qh[1].x, r.qh[1].y};
 		uint32_t lo[8], hi[8];   // fp16 pairs
 #pragma unroll
 		for (int j = 0; j < 4; j++) {
@@ -424,22 +439,17 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 		*(uint4 *)(wrow_s + 2 * (32 * (k1 + 2) + l0)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
 		*(uint4 *)(wrow_s + 2 * (32 * (k1 + 2) + l0 + 8)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
 		// group gg = 2*part + i covers K [16gg, 16gg+16): scale 8n + gg
-		const float d = f16_to_f32(dr);
-		dsc_s[2 * part][wrow] = d * (float)(int8_t)(scr & 0xFFu);
-		dsc_s[2 * part + 1][wrow] = d * (float)(int8_t)(scr >> 8);
+		const float d = f16_to_f32(r.d);
+		dsc_s[2 * part][wrow] = d * (float)(int8_t)(r.sc & 0xFFu);
+		dsc_s[2 * part + 1][wrow] = d * (float)(int8_t)(r.sc >> 8);
 	};
 
 	v16f acc = {};
 	const v16f zero = {};
-	const int NSt = NB * 2;
-	load_stage(0);
-	for (int st = 0; st < NSt; st++) {
-		store_stage();
-		__syncthreads();
-		if (st + 1 < NSt) load_stage(st + 1);
-		const _Float16 *ah = ah_s + (32 * wt + li) * kHPad + 8 * kh;
-		const _Float16 *al = al_s + (32 * wt + li) * kHPad + 8 * kh;
-		const _Float16 *wq = wq_s + (32 * wr + li) * kHPad + 8 * kh;
+	const _Float16 *ah = ah_s + (32 * wt + li) * kHPad + 8 * kh;
+	const _Float16 *al = al_s + (32 * wt + li) * kHPad + 8 * kh;
+	const _Float16 *wq = wq_s + (32 * wr + li) * kHPad + 8 * kh;
+	auto compute = [&]() {
 #pragma unroll
 		for (int gg = 0; gg < 8; gg++) {
 			const v8h b = *(const v8h *)(wq + 16 * gg);
@@ -449,6 +459,28 @@ __global__ __launch_bounds__(kGT) void q6k_gemm_kernel(const uint8_t *__restrict
 #pragma unroll
 			for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf(p[v], s, acc[v]);
 		}
+	};
+	Acts aa, ab;
+	Wts wts;
+	load_acts(aa, 0);
+	load_wts(wts, 0);
+	load_acts(ab, 1);
+	// NSt is even: the loop takes the stages in pairs, so each activation
+	// register set is named statically
+	for (int st = 0; st < NSt; st += 2) {
+		store_acts(aa);
+		store_wts(wts);
+		__syncthreads();
+		load_wts(wts, st + 1);
+		load_acts(aa, st + 2);
+		compute();
+		__syncthreads();
+		store_acts(ab);
+		store_wts(wts);
+		__syncthreads();
+		load_wts(wts, st + 2);
+		load_acts(ab, st + 3);
+		compute();
 		__syncthreads();
 	}
 	// lane: row n0+32wr+li, tokens m0+32wt+8q4+4kh+r. Every operand load
