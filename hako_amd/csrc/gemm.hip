@@ -147,10 +147,16 @@ __global__ __launch_bounds__(kGT, 3) void q4k_gemm_kernel(const SkSegs segs, con
 	};
 	// the loaded stage into LDS, with the per-row and per-token factors of the fold
 	auto store_stage = [&]() {
+		// LDS addresses recomputed per stage from an opaque copy of the thread
+		// index: kept live across the loop they would be spilled (and reloaded
+		// from scratch every stage)
+		int t = threadIdx.x;
+		asm volatile("" : "+v"(t));
+		const int hrow = t >> 2, hg = t & 3, asb = (t & 15) >> 1;
 #pragma unroll
 		for (int u = 0; u < 2; u++) {
-			const int row = 32 * half + (((tid & 127) + 128 * u) >> 3);
-			*(uint4 *)(w_s + row * kQ4Bytes + 16 + 16 * wpc) = wreg[u];
+			const int row = 32 * (t >> 7) + (((t & 127) + 128 * u) >> 3);
+			*(uint4 *)(w_s + row * kQ4Bytes + 16 + 16 * (t & 7)) = wreg[u];
 		}
 		{
 			uint32_t S2, M2;
@@ -163,8 +169,8 @@ __global__ __launch_bounds__(kGT, 3) void q4k_gemm_kernel(const SkSegs segs, con
 		}
 #pragma unroll
 		for (int u = 0; u < 4; u++) {
-			const int tok = (tid >> 4) + 16 * u;
-			*(uint4 *)(a_s + tok * kAPad + 16 * apc) = areg[u];
+			const int tok = (t >> 4) + 16 * u;
+			*(uint4 *)(a_s + tok * kAPad + 16 * (t & 15)) = areg[u];
 			int ix = sdot4((int)areg[u].x, 0x01010101, 0);
 			ix = sdot4((int)areg[u].y, 0x01010101, ix);
 			ix = sdot4((int)areg[u].z, 0x01010101, ix);
