@@ -36,6 +36,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
@@ -113,15 +114,14 @@ constexpr int kQ4SkPieces = 3;       // 16-byte pieces per thread and group: 16 
 // LDS of a workgroup over nbk super-blocks (W waves, nbk <= W). Region A
 // holds first the staged q8 rows [16][nbk*256 + 16], then two slots of a
 // group's weights [16][nbk*144 + 16]; then xs and -xs*sum(xq) per
-// (sub-block, token), d*s per (wave, row, sub-block) and two slots of the
-// waves' sums of a group.
+// (sub-block, token) and two slots of the waves' sums of a group.
 __host__ __device__ constexpr size_t q4sk_arow(int nbk) { return (size_t)nbk * kQK + 16; }
 __host__ __device__ constexpr size_t q4sk_rstride(int nbk) { return (size_t)nbk * kQ4Bytes + 16; }
 __host__ __device__ constexpr size_t q4sk_region(int nbk) {
 	return 16 * q4sk_arow(nbk) > 2 * 16 * q4sk_rstride(nbk) ? 16 * q4sk_arow(nbk) : 2 * 16 * q4sk_rstride(nbk);
 }
 __host__ __device__ constexpr size_t q4sk_lds(int nbk, int W) {
-	return q4sk_region(nbk) + 2 * (size_t)nbk * 8 * 16 * 4 + (size_t)W * 16 * 8 * 4 + 2 * (size_t)W * 64 * 16;
+	return q4sk_region(nbk) + 2 * (size_t)nbk * 8 * 16 * 4 + 2 * (size_t)W * 64 * 16;
 }
 
 // The segment of launch row r0 (uniform) with plain selects of its fields:
@@ -159,8 +159,7 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 	uint8_t *w_s = smem;                                  // then: [2][16][rstride]
 	float *xs_s = (float *)(smem + region);               // [nbk*8][16]
 	float *nu_s = xs_s + nbk * 8 * 16;                    // [nbk*8][16]
-	float *ex = nu_s + nbk * 8 * 16 + wave * 128 + j * 8;   // [W][16][8]: this lane's row
-	float4 *red_s = (float4 *)(nu_s + nbk * 8 * 16 + W * 128);   // [2][W][64]
+	float4 *red_s = (float4 *)(nu_s + nbk * 8 * 16);   // [2][W][64]
 	const bool live = wave < nbk;   // this wave's super-block: kb_beg + wave
 	const int ngroups = (vrows + 15) >> 4, G = gridDim.x;
 	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
@@ -220,14 +219,15 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 	};
 
 	// the wave's activation operands (registers, filled once): A operand
-	// (token j, bytes 32sb + 8kq.. of the block) and -xs*sum(xq) of (token j,
-	// sub-blocks kq, kq+4); xs of the lane's four tokens stays in LDS
+	// (token j, bytes 32sb + 8kq.. of the block), and xs and -xs*sum(xq) of
+	// (token j, sub-blocks kq, kq+4)
 	long av[8];
 	float nu0 = 0.0f, nu1 = 0.0f;
-	const float *xsw = xs_s + (8 * wave) * 16 + 4 * kq;
+	float xsw_t[2] = {0.0f, 0.0f};   // xs of (token j, sub-blocks kq, kq+4)
+	const v16f zero16 = {};
 
-	// per block: (s, m) of sub-blocks kq, kq+4 of the lane's row; d*s to the
-	// row's other lanes through LDS, dmin*m into the min-term MFMA
+	// per block: (s, m) of sub-blocks kq, kq+4 of the lane's row; d*s into
+	// the scale-product MFMA, dmin*m into the min-term MFMA
 	auto fold = [&](int slot, float (&y)[4]) {
 		v4f acc = {0.0f, 0.0f, 0.0f, 0.0f}, accm = {0.0f, 0.0f, 0.0f, 0.0f};
 		if (live) {
@@ -241,16 +241,18 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 			scale_min_k4((uint32_t)kq, hd.y, hd.z, hd.w, s0, m0);
 			scale_min_k4((uint32_t)kq + 4u, hd.y, hd.z, hd.w, s1, m1);
 			const float dd = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-			ex[kq] = dd * (float)s0;
-			ex[kq + 4] = dd * (float)s1;
 			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu0, dmin * (float)m0, accm, 0, 0, 0);
 			accm = __builtin_amdgcn_mfma_f32_16x16x4f32(nu1, dmin * (float)m1, accm, 0, 0, 0);
-			__builtin_amdgcn_wave_barrier();
-			const float4 dsa = *(const float4 *)ex, dsb = *(const float4 *)(ex + 4);
-			const float ds[8] = {dsa.x, dsa.y, dsa.z, dsa.w, dsb.x, dsb.y, dsb.z, dsb.w};
 			// four integer products at a time, then their folds
 #pragma unroll
 			for (int half = 0; half < 2; half++) {
+				// the fold's scale products P[token][row] = xs[token]*(d*s)[row] of
+				// sub-blocks 4half..4half+3 as one four-block outer product on the
+				// matrix cores: block b (lanes 16b..) is sub-block 4half + b, whose
+				// d*s this lane computed above (b = kq), laid out like the int8
+				// products: P[4i + v] pairs with di[i][v]
+				const v16f P = __builtin_amdgcn_mfma_f32_16x16x1f32(xsw_t[half], dd * (float)(half ? s1 : s0), zero16,
+				                                                   0, 0, 0);
 				v4i di[4];
 #pragma unroll
 				for (int i = 0; i < 4; i++) {
@@ -262,16 +264,10 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 					                                              0, 0);
 				}
 #pragma unroll
-				for (int i = 0; i < 4; i++) {
-					const int sb = 4 * half + i;
-					const float4 x4 = *(const float4 *)(xsw + sb * 16);
-					acc[0] = __builtin_fmaf((float)di[i][0], x4.x * ds[sb], acc[0]);
-					acc[1] = __builtin_fmaf((float)di[i][1], x4.y * ds[sb], acc[1]);
-					acc[2] = __builtin_fmaf((float)di[i][2], x4.z * ds[sb], acc[2]);
-					acc[3] = __builtin_fmaf((float)di[i][3], x4.w * ds[sb], acc[3]);
-				}
+				for (int i = 0; i < 4; i++)
+#pragma unroll
+					for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf((float)di[i][v], P[4 * i + v], acc[v]);
 			}
-			__builtin_amdgcn_wave_barrier();   // ex is rewritten by the next group
 		}
 #pragma unroll
 		for (int v = 0; v < 4; v++) y[v] = acc[v] + accm[v];
@@ -366,6 +362,8 @@ __global__ __launch_bounds__(64 * W) void q4k_skinny_kernel(SkSegs segs, const i
 		for (int sb = 0; sb < 8; sb++) av[sb] = *(const long *)(arow_p + 32 * sb);
 		nu0 = nu_s[(8 * wave + kq) * 16 + j];
 		nu1 = nu_s[(8 * wave + kq + 4) * 16 + j];
+		xsw_t[0] = xs_s[(8 * wave + kq) * 16 + j];
+		xsw_t[1] = xs_s[(8 * wave + kq + 4) * 16 + j];
 	}
 	__syncthreads();   // the staging area becomes the weight slots
 	gstore(X, 0, 0);
