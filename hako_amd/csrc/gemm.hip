@@ -122,7 +122,7 @@ __global__ __launch_bounds__(kGT, 3) void q4k_gemm_kernel(const SkSegs segs, con
 	const int half = tid >> 7;                       // matrix half of the tile
 	auto srow_of = [&](int row) { return r0 + (EPI == kSkSwiGLU ? row - 32 * half : row); };
 	const int wpc = tid & 7;                         // qs piece
-	const int hrow = tid >> 2, hg = tid & 3;         // header row, 64-weight group
+	const int hrow = tid >> 2;                       // header row
 	const int apc = tid & 15, asb = apc >> 1;        // activation piece, its sub-block
 	uint4 wreg[2], hreg, areg[4];
 	float sreg[4];

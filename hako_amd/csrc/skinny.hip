@@ -43,7 +43,6 @@ typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 constexpr int kT = 256;      // threads per workgroup: 4 waves
 constexpr int kRowsWave = 16;
 constexpr int kRowsWg = 4 * kRowsWave;
-constexpr int kAPadQ4 = 16;  // bytes of padding per staged token row
 
 __device__ __forceinline__ uint32_t ld_b32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 	return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
