@@ -72,6 +72,7 @@ __device__ __forceinline__ void tile_mn(int t, int ntiles, int gm, int &mt, int 
 // ── Q4_K x q8 ──
 
 constexpr int kAPad = 272;   // bytes per staged token row: 256 + 16 (conflict-free 16-byte reads)
+constexpr int kFPad = 72;    // entries per sub-block row of the fold factors (64 + 8)
 
 // Rows of a launch come from up to three segments (SkSegs: weight rows
 // [row0, row0 + rows) of the launch's N rows, each with its own output matrix
@@ -84,9 +85,12 @@ __global__ __launch_bounds__(kGT, 3) void q4k_gemm_kernel(const SkSegs segs, con
                                                        const float *__restrict__ xs, int M, int N, int K, int gm) {
 	__shared__ __align__(16) uint8_t w_s[kTN * kQ4Bytes];   // this stage's block of each row
 	__shared__ __align__(16) int8_t a_s[kTM * kAPad];       // this stage's 256 xq of each token
-	__shared__ __align__(16) float ds_s[8][kTN];            // d*s   [sub-block][row]
-	__shared__ __align__(16) float dm_s[8][kTN];            // dmin*m
-	__shared__ __align__(16) float2 xn_s[8][kTM];           // (xs, -xs*Σxq) [sub-block][token]
+	// [sub-block][row or token], rows padded to 72: the stores of a stage
+	// (four sub-blocks of one row, eight of one token, from neighbouring
+	// lanes) then fall in different banks
+	__shared__ __align__(16) float ds_s[8][kFPad];          // d*s   [sub-block][row]
+	__shared__ __align__(16) float dm_s[8][kFPad];          // dmin*m
+	__shared__ __align__(16) float2 xn_s[8][kFPad];         // (xs, -xs*Σxq) [sub-block][token]
 
 	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
 	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
