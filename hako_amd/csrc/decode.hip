@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		float sc;
 		const uint32_t packed = q8_quant4(v, sc);
 		if (e < n_in) {
-			*(uint32_t *)(xq_s + e) = packed;
+			*(uint32_t *)(xq_s + q8_lds_pos(e)) = packed;
 			if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
 		}
 	}
@@ -840,7 +840,7 @@ __global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ 
 	// 3. q8_32 of the block's 256 outputs (32 lanes per 32-block)
 	{
 		float sc;
-		xq_s[tid] = q8_lane32(acc, sc);
+		xq_s[q8_lds_pos(tid)] = q8_lane32(acc, sc);
 		if ((tid & 31) == 0) xs_s[tid >> 5] = sc;
 	}
 	__syncthreads();

@@ -133,7 +133,7 @@ __global__ __launch_bounds__(WAVES * kWave) void q4k_gemv_kernel(
 			float sc;
 			const uint32_t packed = q8_quant4(xv[k], sc);
 			if (e < n_in) {
-				*(uint32_t *)(xq_s + e) = packed;
+				*(uint32_t *)(xq_s + q8_lds_pos(e)) = packed;
 				if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
 			}
 		}
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(WAVES * kWave) void q4k_gemv_kernel(
 		for (int k = 0; k < XP; k++) {
 			const int e = (threadIdx.x + k * T) * 16;
 			const int4 v = qv[k];
-			if (e < n_in) *(int4 *)(xq_s + e) = v;
+			if (e < n_in) *(int4 *)(xq_s + q8_lds_pos(e)) = v;
 		}
 #pragma unroll
 		for (int k = 0; k < 2; k++) {
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(WAVES * kWave) void q4k_gemv_flat_kernel(
 			float sc;
 			const uint32_t packed = q8_quant4(xv[k], sc);
 			if (e < n_in) {
-				*(uint32_t *)(xq_s + e) = packed;
+				*(uint32_t *)(xq_s + q8_lds_pos(e)) = packed;
 				if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
 			}
 		}
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(WAVES * kWave) void q4k_gemv_flat_kernel(
 #pragma unroll
 		for (int k = 0; k < XP; k++) {
 			const int e = (threadIdx.x + k * T) * 16;
-			if (e < n_in) *(int4 *)(xq_s + e) = qv[k];
+			if (e < n_in) *(int4 *)(xq_s + q8_lds_pos(e)) = qv[k];
 		}
 #pragma unroll
 		for (int k = 0; k < 2; k++) {

@@ -21,11 +21,21 @@ struct Q4Col {
 	int ia_sum, ib_sum; // Σxq of each sub-block (integer-sums mode)
 };
 
+// Place of byte e of a q8 activation row in LDS: the four 16-byte pieces of
+// each 64-byte chunk c (one lane's two sub-blocks) are rotated by c/4, so
+// that the 16-byte reads of sixteen neighbouring lanes' chunks (one piece
+// each) fall in distinct banks (unrotated, chunks 64 bytes apart share four
+// bank groups). Whole pieces stay contiguous.
+__device__ __forceinline__ int q8_lds_pos(int e) {
+	const int c = e >> 6, k = (e >> 4) & 3;
+	return (e & ~63) | (((k + (c >> 2)) & 3) << 4) | (e & 15);
+}
+
 __device__ __forceinline__ void q4_col(const int8_t *xq_s, const float *xs_s, int c, Q4Col &col) {
-	const int i = c >> 2, g = c & 3;
-	const int8_t *p = xq_s + kQK * i + 64 * g;
-	const int4 a0 = *(const int4 *)p, a1 = *(const int4 *)(p + 16);
-	const int4 b0 = *(const int4 *)(p + 32), b1 = *(const int4 *)(p + 48);
+	const int i = c >> 2, g = c & 3, rot = i & 3;
+	const int8_t *p = xq_s + 64 * c;
+	const int4 a0 = *(const int4 *)(p + 16 * (rot & 3)), a1 = *(const int4 *)(p + 16 * ((1 + rot) & 3));
+	const int4 b0 = *(const int4 *)(p + 16 * ((2 + rot) & 3)), b1 = *(const int4 *)(p + 16 * ((3 + rot) & 3));
 	col.xa[0] = a0.x; col.xa[1] = a0.y; col.xa[2] = a0.z; col.xa[3] = a0.w;
 	col.xa[4] = a1.x; col.xa[5] = a1.y; col.xa[6] = a1.z; col.xa[7] = a1.w;
 	col.xb[0] = b0.x; col.xb[1] = b0.y; col.xb[2] = b0.z; col.xb[3] = b0.w;
