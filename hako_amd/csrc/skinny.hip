@@ -24,8 +24,8 @@
 //
 // Q6_K x fp32 (src/nn.c:84-95): q-32 exact in fp16 against the activation as
 // fp16 hi + lo after an exact per-token power-of-two scaling (the prefill
-// GEMM's representation); two v_mfma_f32_16x16x16_f16 per 16-wide scale group
-// then the group sum times d*sc (exact fp32). Activations are staged through
+// GEMM's representation); two v_mfma_f32_16x16x16_f16 per 16-wide scale group,
+// the group sums times sc, their block sum times d. Activations are staged through
 // LDS one super-block at a time, double-buffered.
 #include "hako_dev.h"
 #include "hako_rt.h"
@@ -558,7 +558,6 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 			if (kb < kb_end) {
 				const _Float16 *ah = ah_s[half] + j * kHPadSk + 4 * kq;
 				const _Float16 *al = al_s[half] + j * kHPadSk + 4 * kq;
-				const float dd = f16_to_f32(b.d);
 				const uint32_t scw[4] = {b.sc.x, b.sc.y, b.sc.z, b.sc.w};
 				v4f accb = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -567,35 +566,39 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 					const int n = gg >> 3, k = (gg >> 1) & 3, p = gg & 1;
 					const uint32_t qlw = b.ql[n][2 * (k & 1) + p], qhw = b.qh[n][p];
 					const uint32_t nib = (k >> 1) ? (qlw >> 4) & 0x0F0F0F0Fu : qlw & 0x0F0F0F0Fu;
-					const uint32_t q6 = nib | (((qhw >> (2 * k)) & 0x03030303u) << 4);
-					const uint32_t lo2 = (__builtin_amdgcn_perm(q6, q6, 0x0C010C00u) | 0x64006400u);
-					const uint32_t hi2 = (__builtin_amdgcn_perm(q6, q6, 0x0C030C02u) | 0x64006400u);
+					// qh bits 2k, 2k+1 of each byte to bits 4, 5 with one shift (what
+					// the neighbouring bytes shift in is masked off)
+					const uint32_t hs = k < 2 ? qhw << (4 - 2 * k) : qhw >> (2 * k - 4);
+					const uint32_t q6 = (hs & 0x30303030u) | nib;
+					// 1024 + q as fp16: the exponent byte 0x64 picked beside each
+					// 6-bit byte by the permute itself; minus 1056 gives q - 32 exactly
+					const uint32_t lo2 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04010400u);
+					const uint32_t hi2 = __builtin_amdgcn_perm(0x64646464u, q6, 0x04030402u);
 					const v2h bias2 = {(_Float16)1056.0f, (_Float16)1056.0f};
 					const v2h w01 = __builtin_bit_cast(v2h, lo2) - bias2, w23 = __builtin_bit_cast(v2h, hi2) - bias2;
 					const v4h wv = {w01[0], w01[1], w23[0], w23[1]};
 					v4f pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(ah + 16 * gg), wv, zero, 0, 0, 0);
 					pr = __builtin_amdgcn_mfma_f32_16x16x16f16(*(const v4h *)(al + 16 * gg), wv, pr, 0, 0, 0);
-					const float sgg = dd * (float)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 0xFFu);
-					if (BLK) {
-						accb[0] = __builtin_fmaf(pr[0], sgg, accb[0]);
-						accb[1] = __builtin_fmaf(pr[1], sgg, accb[1]);
-						accb[2] = __builtin_fmaf(pr[2], sgg, accb[2]);
-						accb[3] = __builtin_fmaf(pr[3], sgg, accb[3]);
-					} else {
-						acc[0] = __builtin_fmaf(pr[0], sgg, acc[0]);
-						acc[1] = __builtin_fmaf(pr[1], sgg, acc[1]);
-						acc[2] = __builtin_fmaf(pr[2], sgg, acc[2]);
-						acc[3] = __builtin_fmaf(pr[3], sgg, acc[3]);
-					}
+					const float sg = (float)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 0xFFu);
+					accb[0] = __builtin_fmaf(pr[0], sg, accb[0]);
+					accb[1] = __builtin_fmaf(pr[1], sg, accb[1]);
+					accb[2] = __builtin_fmaf(pr[2], sg, accb[2]);
+					accb[3] = __builtin_fmaf(pr[3], sg, accb[3]);
 				}
+				// the block's sums times d of the row (and, BLK, this block's
+				// powers of two of the lane's tokens, staged with the activations)
+				const float dd = f16_to_f32(b.d);
 				if (BLK) {
-					// this block's powers of two of the lane's tokens, staged with the
-					// activations
 					const float4 eb = *(const float4 *)&es_s[half][t0];
-					acc[0] = __builtin_fmaf(accb[0], eb.x, acc[0]);
-					acc[1] = __builtin_fmaf(accb[1], eb.y, acc[1]);
-					acc[2] = __builtin_fmaf(accb[2], eb.z, acc[2]);
-					acc[3] = __builtin_fmaf(accb[3], eb.w, acc[3]);
+					acc[0] = __builtin_fmaf(accb[0], dd * eb.x, acc[0]);
+					acc[1] = __builtin_fmaf(accb[1], dd * eb.y, acc[1]);
+					acc[2] = __builtin_fmaf(accb[2], dd * eb.z, acc[2]);
+					acc[3] = __builtin_fmaf(accb[3], dd * eb.w, acc[3]);
+				} else {
+					acc[0] = __builtin_fmaf(accb[0], dd, acc[0]);
+					acc[1] = __builtin_fmaf(accb[1], dd, acc[1]);
+					acc[2] = __builtin_fmaf(accb[2], dd, acc[2]);
+					acc[3] = __builtin_fmaf(accb[3], dd, acc[3]);
 				}
 			}
 			store_stage(A, half ^ 1);
