@@ -10,24 +10,26 @@
 // is nibble (k>>1) of ql[64n + 32(k&1) + l] with bits 2k..2k+1 of qh[32n + l]
 // on top, minus 32, times d*scales[8n + 2k + l/16].
 //
-// Lane work. Chunk c = 8i + s of a row is block i, half n = s/4, k pair
-// kp = (s/2)%2 and l half lh = s%2: the 32 weights k in {kp, kp+2}, l in
-// [16lh, 16lh+16) of half n, two 16-wide scale groups. They come from one
-// 16-byte load of ql at 64n+32kp+16lh (low nibbles k = kp, high k = kp+2),
-// one of qh at 32n+16lh (bits 2k..2k+1), 8 bytes of scales and d: the eight
-// lanes of a block read its ql as one 128-byte run and its qh as 32-byte
-// runs. Blocks are only 2-byte aligned in the verbatim stream (210 = 2*105),
-// so the loads are unaligned; gfx950 serves them in the HSA unaligned-access
-// mode the compiler itself assumes for byte copies. The 6-bit values are
-// assembled four to a dword (nibbles | qh bits moved to bits 4-5 of each
-// byte), converted per byte (v_cvt_f32_ubyteN) and multiplied into the
-// lane's fp32 activations; per scale group the sum is Σq·x − 32·Σx with
-// −32·Σx precomputed.
+// Lane work. Chunk c = 4i + s of a row is block i, half n = s/2 and l half
+// lh = s%2: the 64 weights k = 0..3, l in [16lh, 16lh+16) of half n, four
+// 16-wide scale groups. They come from two 16-byte loads of ql at
+// 64n+16lh (low nibbles k = 0, high k = 2) and 64n+32+16lh (k = 1, 3), one
+// of qh at 32n+16lh (bits 2k..2k+1), 8 bytes of scales and d: the four lanes
+// of a block read each of its bytes once (232 bytes loaded per 210-byte
+// block; a no-arithmetic probe of this pattern streams the 151936x2048
+// vocab matrix at 5.9 TB/s against 4.7 for eight lanes of 32 weights, which
+// load each qh byte twice and the scales four times). Blocks are only 2-byte
+// aligned in the verbatim stream (210 = 2*105), so the loads are unaligned;
+// gfx950 serves them in the HSA unaligned-access mode the compiler itself
+// assumes for byte copies. The 6-bit values are assembled four to a dword
+// (nibbles | qh bits moved to bits 4-5 of each byte), converted per byte
+// (v_cvt_f32_ubyteN) and multiplied into the lane's fp32 activations; per
+// scale group the sum is Σq·x − 32·Σx with −32·Σx precomputed.
 //
 // Grid. Persistent: about one workgroup per CU, each owning a contiguous row
-// range. A row of C = 8*NB chunks is cut into ceil(C/64) parts; the
+// range. A row of C = 4*NB chunks is cut into ceil(C/64) parts; the
 // workgroup has one wave group per part (W = parts x row-slices waves, at
-// most 16), and wave (part p, slice r) visits rows r, r+RW, ... of the range
+// most 8), and wave (part p, slice r) visits rows r, r+RW, ... of the range
 // with part p's activations hoisted in registers for all of them. Partial sums
 // of a row meet in LDS. Each wave keeps four row loads in flight ahead of the
 // row it computes.
@@ -38,71 +40,73 @@ namespace hako {
 namespace {
 
 constexpr int kQ6Depth = 4;
-constexpr int kQ6MaxWaves = 16;
+constexpr int kQ6MaxWaves = 8;
 
 struct Q6Buf {
-	uint4 ql, qh;
+	uint4 qa, qb;    // ql 64n+16lh .. +16 (k = 0, 2) and 64n+32+16lh .. +16 (k = 1, 3)
+	uint4 qh;        // qh 32n+16lh .. +16
 	uint2 s;         // scales 8n .. 8n+8
 	uint32_t d;
 };
 
-// The lane's activation columns for one chunk: xv[kk][j] = x at weight
-// 128n + 32(kp + 2kk) + 16lh + j of block i, and -32·Σ_j xv[kk][j].
+// The lane's activation columns for one chunk: xv[k][j] = x at weight
+// 128n + 32k + 16lh + j of block i, and -32·Σ_j xv[k][j].
 struct Q6Col {
-	float xv[2][16];
-	float nsx[2];
+	float xv[4][16];
+	float nsx[4];
 };
 
 __device__ __forceinline__ void q6_col_load(const float *__restrict__ x, int c, Q6Col &col) {
-	const int i = c >> 3, s = c & 7, n = s >> 2, kp = (s >> 1) & 1, lh = s & 1;
-	const float *xb = x + kQK * i + 128 * n + 32 * kp + 16 * lh;
+	const int i = c >> 2, s = c & 3, n = s >> 1, lh = s & 1;
+	const float *xb = x + kQK * i + 128 * n + 16 * lh;
 #pragma unroll
-	for (int kk = 0; kk < 2; kk++) {
+	for (int k = 0; k < 4; k++) {
 #pragma unroll
 		for (int m = 0; m < 4; m++) {
-			const float4 u = *(const float4 *)(xb + 64 * kk + 4 * m);
-			col.xv[kk][4 * m] = u.x; col.xv[kk][4 * m + 1] = u.y;
-			col.xv[kk][4 * m + 2] = u.z; col.xv[kk][4 * m + 3] = u.w;
+			const float4 u = *(const float4 *)(xb + 32 * k + 4 * m);
+			col.xv[k][4 * m] = u.x; col.xv[k][4 * m + 1] = u.y;
+			col.xv[k][4 * m + 2] = u.z; col.xv[k][4 * m + 3] = u.w;
 		}
 	}
 }
 
 __device__ __forceinline__ void q6_col_sums(Q6Col &col) {
 #pragma unroll
-	for (int kk = 0; kk < 2; kk++) {
+	for (int k = 0; k < 4; k++) {
 		float t = 0.0f;
 #pragma unroll
-		for (int j = 0; j < 16; j++) t += col.xv[kk][j];
-		col.nsx[kk] = -32.0f * t;
+		for (int j = 0; j < 16; j++) t += col.xv[k][j];
+		col.nsx[k] = -32.0f * t;
 	}
 }
 
 __device__ __forceinline__ float byte_f(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 
-// d · Σ_kk sc_kk · (Σ_j q_kk,j·x_kk,j − 32·Σ_j x_kk,j) over the lane's 32
-// weights (k = kp + 2kk; qh bits 2k..2k+1 taken at shift 2kp, 2kp+4).
-__device__ __forceinline__ float q6_dot(const Q6Buf &W, const Q6Col &col, int kp, int sel) {
-	float acc0 = col.nsx[0], acc1 = col.nsx[1];
+// d · Σ_k sc_k · (Σ_j q_k,j·x_k,j − 32·Σ_j x_k,j) over the lane's 64 weights
+// (scale 8n + 2k + lh: byte 2k + lh of the lane's 8 scale bytes).
+__device__ __forceinline__ float q6_dot(const Q6Buf &W, const Q6Col &col, int lh) {
+	float acc[4] = {col.nsx[0], col.nsx[1], col.nsx[2], col.nsx[3]};
 	const uint32_t lo = 0x0F0F0F0Fu, hb = 0x30303030u;
-	const uint32_t ql[4] = {W.ql.x, W.ql.y, W.ql.z, W.ql.w}, qh[4] = {W.qh.x, W.qh.y, W.qh.z, W.qh.w};
-	const int sh = 2 * kp;
+	const uint32_t qa[4] = {W.qa.x, W.qa.y, W.qa.z, W.qa.w}, qb[4] = {W.qb.x, W.qb.y, W.qb.z, W.qb.w};
+	const uint32_t qh[4] = {W.qh.x, W.qh.y, W.qh.z, W.qh.w};
 #pragma unroll
 	for (int u = 0; u < 4; u++) {
-		// qh bits 2k, 2k+1 of each byte to bits 4, 5 with one shift each (k = kp:
-		// left by 4 - 2kp; k = kp + 2: right by 2kp); what other bytes shift in
-		// lands outside bits 4-5
-		const uint32_t w0 = (ql[u] & lo) | ((qh[u] << (4 - sh)) & hb);
-		const uint32_t w1 = ((ql[u] >> 4) & lo) | ((qh[u] >> sh) & hb);
+		// qh bits 2k, 2k+1 of each byte to bits 4, 5 with at most one shift;
+		// what the neighbouring bytes shift in lands outside bits 4-5
+		uint32_t wk[4];
+		wk[0] = (qa[u] & lo) | ((qh[u] << 4) & hb);
+		wk[1] = (qb[u] & lo) | ((qh[u] << 2) & hb);
+		wk[2] = ((qa[u] >> 4) & lo) | (qh[u] & hb);
+		wk[3] = ((qb[u] >> 4) & lo) | ((qh[u] >> 2) & hb);
 #pragma unroll
-		for (int b = 0; b < 4; b++) {
-			acc0 = __builtin_fmaf(byte_f(w0, b), col.xv[0][4 * u + b], acc0);
-			acc1 = __builtin_fmaf(byte_f(w1, b), col.xv[1][4 * u + b], acc1);
-		}
+		for (int k = 0; k < 4; k++)
+#pragma unroll
+			for (int b = 0; b < 4; b++) acc[k] = __builtin_fmaf(byte_f(wk[k], b), col.xv[k][4 * u + b], acc[k]);
 	}
-	// scales[8n + 2k + lh]: byte sel = 2kp + lh of each dword (k = kp, kp+2)
-	const float s0 = (float)(int8_t)((W.s.x >> (8 * sel)) & 0xFFu);
-	const float s1 = (float)(int8_t)((W.s.y >> (8 * sel)) & 0xFFu);
-	return f16_to_f32(W.d) * (s0 * acc0 + s1 * acc1);
+	const int sh = 8 * lh;
+	const float s0 = (float)(int8_t)((W.s.x >> sh) & 0xFFu), s1 = (float)(int8_t)((W.s.x >> (sh + 16)) & 0xFFu);
+	const float s2 = (float)(int8_t)((W.s.y >> sh) & 0xFFu), s3 = (float)(int8_t)((W.s.y >> (sh + 16)) & 0xFFu);
+	return f16_to_f32(W.d) * ((s0 * acc[0] + s1 * acc[1]) + (s2 * acc[2] + s3 * acc[3]));
 }
 
 struct Q6Geom {
@@ -112,7 +116,7 @@ struct Q6Geom {
 // `target` waves per workgroup (4 or 8): row slices = target / parts, >= 1.
 __host__ __device__ inline Q6Geom q6_geom(int n_in, int target) {
 	Q6Geom g;
-	g.C = n_in / kQK * 8;
+	g.C = n_in / kQK * 4;
 	if (g.C <= 64) {
 		g.seg = 1;
 		while (g.seg < g.C) g.seg <<= 1;
@@ -152,7 +156,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 	auto item_row = [&](int it) -> int { return r0 + G.rt * (slice + G.rw * it) + rsub; };
 
 	const int cc = min(c, G.C - 1);           // in-bounds chunk for idle lanes' loads
-	const int i = cc >> 3, s = cc & 7, hn = s >> 2, kp = (s >> 1) & 1, lh = s & 1, sel = 2 * kp + lh;
+	const int i = cc >> 2, s = cc & 3, hn = s >> 1, lh = s & 1;
 	const size_t in_row = (size_t)i * kQ6Bytes;
 	// Weight loads are raw buffer loads, never predicated: slots with no work
 	// use an offset past the stream (zeros, no memory traffic). A branch
@@ -162,7 +166,8 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 		const int row = item_row(it);
 		const bool on = it < nit && row < r1 && lane_on;
 		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + in_row) : kBufNone;
-		b.ql = ld_b128(wr, blk + 64 * hn + 32 * kp + 16 * lh);
+		b.qa = ld_b128(wr, blk + 64 * hn + 16 * lh);
+		b.qb = ld_b128(wr, blk + 64 * hn + 32 + 16 * lh);
 		b.qh = ld_b128(wr, blk + 128 + 32 * hn + 16 * lh);
 		b.s = ld_b64(wr, blk + 192 + 8 * hn);
 		b.d = ld_b16(wr, blk + 208);
@@ -201,7 +206,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 			const int row = item_row(it);
 			float d = 0.0f;
 			// Consume buf[j] in place, then reload it (no register rotation).
-			if (it < nit) d = q6_dot(buf[j], col, kp, sel);
+			if (it < nit) d = q6_dot(buf[j], col, lh);
 			issue(buf[j], it + kQ6Depth);
 			__builtin_amdgcn_sched_barrier(0);
 			rsum[j] = (lane_on && row < r1) ? d : 0.0f;
@@ -250,7 +255,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(cons
 	constexpr int NG = (ITEMS + 3) / 4;   // groups of four items reduced together
 	__shared__ float red_s[kQ6MaxWaves][4 * NG];
 	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-	const int NB = n_in >> 8, C = NB * 8;
+	const int NB = n_in >> 8, C = NB * 4;
 	const bool wide = C > 64;
 	const int seg = wide ? 64 : next_pow2(C), rt = 64 / seg;
 	const int sub = lane & (seg - 1), rsub = lane / seg;
@@ -263,7 +268,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(cons
 	const size_t rb = (size_t)NB * kQ6Bytes;
 
 	const int cc = min(c, C - 1);
-	const int i = cc >> 3, s = cc & 7, hn = s >> 2, kp = (s >> 1) & 1, lh = s & 1, sel = 2 * kp + lh;
+	const int i = cc >> 2, s = cc & 3, hn = s >> 1, lh = s & 1;
 
 	// 1. activation, then bias / residual of the row this lane writes
 	Q6Col col;
@@ -289,7 +294,8 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(cons
 		const int row = item_row(j);
 		const bool on = row < n_out && lane_on;
 		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + (size_t)i * kQ6Bytes) : kBufNone;
-		buf[j].ql = ld_b128(wr, blk + 64 * hn + 32 * kp + 16 * lh);
+		buf[j].qa = ld_b128(wr, blk + 64 * hn + 16 * lh);
+		buf[j].qb = ld_b128(wr, blk + 64 * hn + 32 + 16 * lh);
 		buf[j].qh = ld_b128(wr, blk + 128 + 32 * hn + 16 * lh);
 		buf[j].s = ld_b64(wr, blk + 192 + 8 * hn);
 		buf[j].d = ld_b16(wr, blk + 208);
@@ -303,7 +309,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(cons
 	for (int j = 0; j < 4 * NG; j++) {
 		rsum[j] = 0.0f;
 		if (j >= ITEMS) continue;
-		const float d = q6_dot(buf[j], col, kp, sel);
+		const float d = q6_dot(buf[j], col, lh);
 		rsum[j] = (lane_on && item_row(j) < n_out) ? d : 0.0f;
 	}
 	// 4. lane sub = j (< 4) of each segment holds item 4g + j
@@ -338,15 +344,18 @@ int g_q6_waves = 4;
 // -1: by shape (below); 0: persistent grid; 1, 2, 4, 8: flat grid with that many items per wave
 int g_q6_flat_items = -1;
 
-// Measured on MI355X (us per launch, persistent / flat with 1, 2, 4 items):
-// 2048x11008 9.18 / 12.0 / 9.38 / 8.06; 1000x4608 4.76 / 4.45 / 4.15 / 3.91;
-// 256x2048 3.75 / 2.99 / 3.38 / 3.92; 151936x2048 65.8 / 104 / 78.8 / 68.4;
-// 3584x18944 19.2 / 30.0 / 27.1 / 21.9. Rows of 2..6 parts take the flat grid
-// with 4 items; short matrices of one part the flat grid with one item;
-// wider rows and tall matrices the persistent grid.
+// Measured on MI355X (us per launch, persistent / flat with 1, 2, 4, 8
+// items): 2048x11008 (3 parts) 8.08 / 10.8 / 8.58 / 7.45 / 8.24; 1000x4608
+// (2 parts) 5.29 / 4.75 / 4.66 / 4.45 / 6.40; 3584x18944 (5 parts) 18.1 /
+// 28.5 / 25.0 / 22.7 / 22.5; 16384x3584 (4 parts) 13.0 / 20.7 / 16.8 / 13.6
+// / 13.6; 151936x2048 48.4 / 88.7 / 65.3 / 54.5 / 53.3; 152064x3584 89.7 /
+// 165 / 129 / 98.1 / 90.5; earlier, 256x2048 (one part) 3.75 / 2.99 / 3.38 /
+// 3.92. Rows of 2..3 parts take the flat grid with 4 items; short matrices
+// of one part the flat grid with one item; wider rows and tall matrices the
+// persistent grid.
 int q6_flat_items_for(int n_out, const Q6Geom &G) {
 	if (g_q6_flat_items >= 0) return g_q6_flat_items;
-	if (G.C > 64 && G.tpr <= 6 && n_out <= 8192) return 4;   // past ~8K rows the persistent grid streams faster
+	if (G.C > 64 && G.tpr <= 3 && n_out <= 8192) return 4;   // past ~8K rows the persistent grid streams faster
 	if (G.C <= 64 && n_out <= 4096) return 1;
 	return 0;
 }
@@ -375,7 +384,7 @@ int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n
 	if ((size_t)n_out * (n_in / kQK) * kQ6Bytes >= kBufNone)
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV weight of %d x %d exceeds 2 GiB", n_out, n_in);
 	if (G.waves > kQ6MaxWaves || G.tpr > kQ6MaxWaves)
-		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV n_in %d exceeds %d", n_in, kQ6MaxWaves * 64 * 32);
+		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV n_in %d exceeds %d", n_in, kQ6MaxWaves * 64 * 64);
 	if (const int items = q6_flat_items_for(n_out, G)) {
 		const bool wide = G.C > 64;
 		const int rows_wg = wide ? items : 4 * items * G.rt;
