@@ -339,11 +339,12 @@ __global__ __launch_bounds__(kSplitT) void f16_split_kernel(const float *__restr
 }
 
 // Two of the 6-bit values in `v` (bytes picked by the v_perm selector `sel`
-// into the low byte of each half) as the fp16 pair (q0 - 32, q1 - 32):
-// 0x6400 | q is 1024 + q exactly, and 1024 + q - 1056 is exact.
+// into the low byte of each half, selector byte 4 placing the exponent byte
+// 0x64 above each) as the fp16 pair (q0 - 32, q1 - 32): 0x6400 | q is
+// 1024 + q exactly, and 1024 + q - 1056 is exact.
 __device__ __forceinline__ uint32_t q6_pair(uint32_t v, uint32_t sel) {
 	typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-	const uint32_t t = __builtin_amdgcn_perm(v, v, sel) | 0x64006400u;
+	const uint32_t t = __builtin_amdgcn_perm(0x64646464u, v, sel);
 	const v2h r = __builtin_bit_cast(v2h, t) - (v2h){(_Float16)1056.0f, (_Float16)1056.0f};
 	return __builtin_bit_cast(uint32_t, r);
 }
@@ -436,12 +437,13 @@ __global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restr
 		uint32_t lo[8], hi[8];   // fp16 pairs
 #pragma unroll
 		for (int j = 0; j < 4; j++) {
-			const uint32_t vlo = (ql[j] & 0x0F0F0F0Fu) | (((qh[j] >> (2 * k1)) & 0x03030303u) << 4);
-			const uint32_t vhi = ((ql[j] >> 4) & 0x0F0F0F0Fu) | (((qh[j] >> (2 * k1 + 4)) & 0x03030303u) << 4);
-			lo[2 * j] = q6_pair(vlo, 0x0C010C00u);
-			lo[2 * j + 1] = q6_pair(vlo, 0x0C030C02u);
-			hi[2 * j] = q6_pair(vhi, 0x0C010C00u);
-			hi[2 * j + 1] = q6_pair(vhi, 0x0C030C02u);
+			// qh bits 2k1, 2k1+1 (and 2k1+4, 2k1+5) of each byte to bits 4, 5
+			const uint32_t vlo = ((qh[j] << (4 - 2 * k1)) & 0x30303030u) | (ql[j] & 0x0F0F0F0Fu);
+			const uint32_t vhi = ((qh[j] >> (2 * k1)) & 0x30303030u) | ((ql[j] >> 4) & 0x0F0F0F0Fu);
+			lo[2 * j] = q6_pair(vlo, 0x04010400u);
+			lo[2 * j + 1] = q6_pair(vlo, 0x04030402u);
+			hi[2 * j] = q6_pair(vhi, 0x04010400u);
+			hi[2 * j + 1] = q6_pair(vhi, 0x04030402u);
 		}
 		uint8_t *wrow_s = (uint8_t *)(wq_s + wrow * kHPad);
 		*(uint4 *)(wrow_s + 2 * (32 * k1 + l0)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
