@@ -343,6 +343,27 @@ def test_mirror_overlaps_are_refused(gpu):
     assert d
 
 
+def test_q6k_widest_row(gpu, oracle):
+    """n_in = 32768 fills the widest workgroup (8 parts of 64 chunks of 64
+    weights) and matches the reference's generic row path; one super-block
+    more is refused before anything is launched."""
+    from hako_amd.gpu import HakoGpuError
+    rng = np.random.default_rng(32768)
+    n_out, n_in = 7, 32768
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    got = gpu_matmul(gpu, Q6, w, x, n_out, n_in)
+    assert maxabs_rel(got, oracle.matmul(Q6, w, x, n_out, n_in, f64=True, threads=16)) < TOL
+    wide = n_in + 256
+    dw, dx, do = gpu.alloc(wide // 256 * 210 * 2), gpu.alloc(wide * 4), gpu.alloc(64)
+    try:
+        with pytest.raises(HakoGpuError, match="exceeds"):
+            gpu.q6k_gemv(do, dw, dx, None, 2, wide)
+    finally:
+        for b in (dw, dx, do):
+            b.free()
+
+
 def test_bad_shapes_are_rejected(gpu):
     from hako_amd.gpu import HakoGpuError
     dw, dx, do = gpu.alloc(4096), gpu.alloc(4096), gpu.alloc(4096)
