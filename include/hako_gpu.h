@@ -140,7 +140,8 @@ int hako_gpu_dequant(int type, const void *src, float *out, int64_t nelem);
 /* Q4_K x q8 GEMV on a pre-quantized activation: out[r] = sum over the
  * sub-blocks sb of xs[sb]*(d*s*iqx - dmin*m*ix) (+ bias[r]), i.e.
  * q4k_vec_dot per row (reference src/quant.c:150-232, src/nn.c:76-82).
- * bias may be NULL. n_in % 256 == 0. */
+ * bias may be NULL. n_in % 256 == 0, n_in <= 32768 (the activation is held
+ * in LDS; EINVAL past it). */
 int hako_gpu_q4k_gemv(float *out, const void *w, const int8_t *xq, const float *xs,
                       const float *bias, int n_out, int n_in);
 
@@ -152,7 +153,8 @@ int hako_gpu_q4k_isums(int32_t *iqx, int32_t *ix, const void *w, const int8_t *x
 
 /* Q6_K x fp32 GEMV: out[r] = sum_i deq(W[r])[i] * x[i] (+ bias[r]), the
  * reference's generic path for Q6_K rows (src/nn.c:84-95, src/quant.c:94-123).
- * The activation stays fp32. n_in % 256 == 0. */
+ * The activation stays fp32. n_in % 256 == 0, n_in <= 32768 (EINVAL past it),
+ * the weight under 2 GiB. */
 int hako_gpu_q6k_gemv(float *out, const void *w, const float *x, const float *bias,
                       int n_out, int n_in);
 
