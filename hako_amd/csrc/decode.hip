@@ -692,6 +692,174 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 	}
 }
 
+// Prompt pass on the matrix cores, for passes whose tokens all lie below
+// kFlashPos cache positions (every key of a token in one workgroup): workgroup
+// (64-token tile, query head), 4 waves of 16 query tokens. The tile's rotated
+// query rows are staged through LDS into registers once; then per 64-key
+// chunk (keys and values staged in LDS, rows 132 floats apart) each wave
+// forms S^T = K Q^T with v_mfma_f32_16x16x4_f32 (4 key tiles x 32 steps, lane
+// l's steps taking dims 32(l/16) + s), masks keys past each token's position,
+// keeps a running max and sum per token (online softmax, -inf scores weigh
+// 0), and adds V^T P^T into O^T (8 dim tiles x 16 steps; step (t, v) is keys
+// 16t + 4k + v for lane group k, which is where the S^T layout left p, and
+// tile dt row i is dim 8i + dt). O / sum goes to att and, with xq, each
+// lane's 32 dims (one whole 32-block) to q8_32. The math is the reference's
+// (src/model.c:123-142: scores, softmax, weighted values) in fp32 with a
+// different order of additions.
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kFlashPos = 512;   // positions a pass may reach for this kernel
+constexpr int kFlashRow = 132;   // floats per staged key / value / query row
+__global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restrict__ q_all,
+                                                            const float2 *__restrict__ rope,
+                                                            const float *__restrict__ kc, const float *__restrict__ vc,
+                                                            const int *__restrict__ posv, float *__restrict__ att,
+                                                            int8_t *__restrict__ xq, float *__restrict__ xs, int H,
+                                                            int KVH, int max_seq, int ntok, float scale) {
+	constexpr int HD = 128, HALF = 64;
+	__shared__ __align__(16) float k_s[64 * kFlashRow];   // keys of the chunk (first: the tile's queries)
+	__shared__ __align__(16) float v_s[64 * kFlashRow];   // values of the chunk
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int qi = lane & 15, kg = lane >> 4;
+	const int t0 = blockIdx.x * 64, h = blockIdx.y, kvh = h / (H / KVH);
+	const int KV = KVH * HD, D = H * HD;
+	const int tq = t0 + 16 * wave + qi;   // this lane's query token
+	int pos_q = tq < ntok ? posv[tq] : -1;
+	pos_q = pos_q < max_seq ? pos_q : -1;
+	const int plast = posv[min(t0 + 63, ntok - 1)];   // positions rise with the token
+	if (plast < 0 || plast >= max_seq) return;        // the host refuses such passes
+	const int nch = plast / 64 + 1;
+
+	// 1. the tile's rotated query rows (NeoX rope at each token's position) into k_s
+#pragma unroll 4
+	for (int r = 0; r < 16; r++) {
+		const int e = tid + 256 * r, i = e >> 6, p = e & 63;
+		const int tok = min(t0 + i, ntok - 1);
+		const int pos = min(max(posv[tok], 0), max_seq - 1);
+		const float *q = q_all + (size_t)tok * D + h * HD;
+		const float a = q[p], b = q[p + HALF];
+		const float2 cs = rope[(size_t)pos * HALF + p];
+		k_s[i * kFlashRow + p] = a * cs.x - b * cs.y;
+		k_s[i * kFlashRow + p + HALF] = a * cs.y + b * cs.x;
+	}
+	__syncthreads();
+	float qv[32];   // Q[query qi][32 kg + s]
+	{
+		const float *src = k_s + (16 * wave + qi) * kFlashRow + 32 * kg;
+#pragma unroll
+		for (int i = 0; i < 8; i++) {
+			const float4 t = *(const float4 *)(src + 4 * i);
+			qv[4 * i] = t.x; qv[4 * i + 1] = t.y; qv[4 * i + 2] = t.z; qv[4 * i + 3] = t.w;
+		}
+	}
+	__syncthreads();   // the query rows are in registers: k_s takes the keys
+
+	const uint32_t cache_bytes = (uint32_t)((size_t)max_seq * KV * 4);
+	const __amdgpu_buffer_rsrc_t krs = stream_rsrc(kc, cache_bytes), vrs = stream_rsrc(vc, cache_bytes);
+	v4f acco[8];
+#pragma unroll
+	for (int dt = 0; dt < 8; dt++) acco[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+	float m_run = -INFINITY, l_run = 0.0f;
+	const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+	for (int c = 0; c < nch; c++) {
+		// 2. the chunk's keys and values (rows past the tile's last position
+		//    read that row: in bounds, masked below)
+#pragma unroll
+		for (int r = 0; r < 8; r++) {
+			const int e = tid + 256 * r, row = e >> 5, f = e & 31;
+			const int key = min(64 * c + row, plast);
+			const uint32_t off = ((uint32_t)key * KV + kvh * HD + 4 * f) * 4u;
+			*(float4 *)(k_s + row * kFlashRow + 4 * f) = __builtin_bit_cast(float4, ld_b128(krs, off));
+			*(float4 *)(v_s + row * kFlashRow + 4 * f) = __builtin_bit_cast(float4, ld_b128(vrs, off));
+		}
+		__syncthreads();
+		// 3. S^T tiles: keys 16t + 4kg + v of this lane, query qi
+		v4f sc[4];
+#pragma unroll
+		for (int t = 0; t < 4; t++) {
+			v4f a = zero;
+			const float *kr = k_s + (16 * t + qi) * kFlashRow + 32 * kg;
+#pragma unroll
+			for (int i = 0; i < 8; i++) {
+				const float4 kv = *(const float4 *)(kr + 4 * i);
+				a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qv[4 * i], a, 0, 0, 0);
+				a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qv[4 * i + 1], a, 0, 0, 0);
+				a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qv[4 * i + 2], a, 0, 0, 0);
+				a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qv[4 * i + 3], a, 0, 0, 0);
+			}
+			sc[t] = a;
+		}
+		// 4. online softmax of query qi (its 64 keys over lanes qi, qi+16, qi+32, qi+48)
+		float mc = -INFINITY;
+#pragma unroll
+		for (int t = 0; t < 4; t++)
+#pragma unroll
+			for (int v = 0; v < 4; v++) {
+				const int key = 64 * c + 16 * t + 4 * kg + v;
+				sc[t][v] = key <= pos_q ? sc[t][v] * scale : -INFINITY;
+				mc = __builtin_fmaxf(mc, sc[t][v]);
+			}
+		mc = __builtin_fmaxf(mc, __shfl_xor(mc, 16));
+		mc = __builtin_fmaxf(mc, __shfl_xor(mc, 32));
+		const float m_new = __builtin_fmaxf(m_run, mc);
+		const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+		float ps = 0.0f;
+#pragma unroll
+		for (int t = 0; t < 4; t++)
+#pragma unroll
+			for (int v = 0; v < 4; v++) {
+				const float p = sc[t][v] == -INFINITY ? 0.0f : expf(sc[t][v] - m_new);
+				sc[t][v] = p;
+				ps += p;
+			}
+		ps += __shfl_xor(ps, 16);
+		ps += __shfl_xor(ps, 32);
+		l_run = l_run * alpha + ps;
+		m_run = m_new;
+#pragma unroll
+		for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+			for (int v = 0; v < 4; v++) acco[dt][v] *= alpha;
+		// 5. O^T += V^T P^T: step (t, v) = keys 16t + 4kg + v, tile dt row i = dim 8i + dt
+#pragma unroll
+		for (int t = 0; t < 4; t++)
+#pragma unroll
+			for (int v = 0; v < 4; v++) {
+				const float *vr = v_s + (16 * t + 4 * kg + v) * kFlashRow + 8 * qi;
+				const float4 va = *(const float4 *)vr, vb = *(const float4 *)(vr + 4);
+				const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+				for (int dt = 0; dt < 8; dt++)
+					acco[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[dt], sc[t][v], acco[dt], 0, 0, 0);
+			}
+		__syncthreads();   // before the next chunk's rows land
+	}
+	// 6. O / sum: this lane holds dims 32kg + 8v + dt of query qi (one 32-block)
+	if (tq >= ntok || pos_q < 0) return;
+	const float inv_l = 1.0f / l_run;
+	float o[32];
+#pragma unroll
+	for (int v = 0; v < 4; v++)
+#pragma unroll
+		for (int dt = 0; dt < 8; dt++) o[8 * v + dt] = acco[dt][v] * inv_l;
+	const size_t ob = (size_t)tq * D + h * HD + 32 * kg;
+#pragma unroll
+	for (int i = 0; i < 8; i++) *(float4 *)(att + ob + 4 * i) = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+	if (xq) {
+		float amax = 0.0f;
+#pragma unroll
+		for (int i = 0; i < 32; i++) amax = __builtin_fmaxf(amax, __builtin_fabsf(ftz(o[i])));
+		const float s = q8_xs(amax), inv = q8_inv(amax, s);
+		uint32_t pk[8];
+#pragma unroll
+		for (int i = 0; i < 8; i++)
+			pk[i] = q8_code(ftz(o[4 * i]), inv) | (q8_code(ftz(o[4 * i + 1]), inv) << 8) |
+			        (q8_code(ftz(o[4 * i + 2]), inv) << 16) | (q8_code(ftz(o[4 * i + 3]), inv) << 24);
+		*(uint4 *)(xq + ob) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+		*(uint4 *)(xq + ob + 16) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+		xs[ob >> 5] = s;
+	}
+}
+
 // The merge of one query head's chunk records by the HD threads of its waves
 // (waves hw0 .. hw0 + HD/64 - 1 of the workgroup; thread ht = value dim):
 // M = max m_c, weights e^(m_c - M) / L with L = sum l_c e^(m_c - M), output
@@ -1462,13 +1630,19 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 		// exit at once), also the record stride of the pass
 		const int pchunks = prefill_chunks(pos0 + n - 1);
 		const dim3 ag(pchunks, KVH, n), mg(G, KVH, n);
-		if (HD == 128) {
+		if (HD == 128 && pos0 + n <= kFlashPos) {
+			// every token's keys in one workgroup: matrix cores, no merge pass
+			hipLaunchKernelGGL(attn_flash_kernel, dim3((n + 63) / 64, m.n_heads), dim3(256), 0, stream(), d->pf_q,
+			                   d->rope, kcl, vcl, d->pf_pos, d->pf_att, mxq, mxs, m.n_heads, KVH, d->max_seq, n, scale);
+			HK_LAUNCHED("attention");
+		} else if (HD == 128) {
 			hipLaunchKernelGGL((attn_kernel<128, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
 			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, pchunks, (size_t)0, D, scale,
 			                   1);
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(128), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
 			                   mxq, mxs, m.n_heads, KVH, d->max_seq, pchunks);
+			HK_LAUNCHED("attention merge");
 		} else {
 			hipLaunchKernelGGL((attn_kernel<64, false>), ag, dim3(256), 0, stream(), d->pf_q, d->rope, kcl, vcl,
 			                   d->pf_pos, d->pf_part, m.n_heads, KVH, d->max_seq, pchunks, (size_t)0, D, scale,
@@ -1476,8 +1650,8 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 			HK_LAUNCHED("attention");
 			hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, stream(), d->pf_part, d->pf_pos, d->pf_att,
 			                   mxq, mxs, m.n_heads, KVH, d->max_seq, pchunks);
+			HK_LAUNCHED("attention merge");
 		}
-		HK_LAUNCHED("attention merge");
 		if (f_o) {
 			SkSegs s{};
 			s.n = 1;
