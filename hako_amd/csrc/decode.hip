@@ -694,35 +694,41 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ qkv
 
 // Prompt pass on the matrix cores, for passes whose tokens all lie below
 // kFlashPos cache positions (every key of a token in one workgroup): workgroup
-// (64-token tile, query head), 4 waves of 16 query tokens. The tile's rotated
-// query rows are staged through LDS into registers once; then per 64-key
-// chunk (keys and values staged in LDS, rows 132 floats apart) each wave
-// forms S^T = K Q^T with v_mfma_f32_16x16x4_f32 (4 key tiles x 32 steps, lane
-// l's steps taking dims 32(l/16) + s), masks keys past each token's position,
-// keeps a running max and sum per token (online softmax, -inf scores weigh
-// 0), and adds V^T P^T into O^T (8 dim tiles x 16 steps; step (t, v) is keys
-// 16t + 4k + v for lane group k, which is where the S^T layout left p, and
-// tile dt row i is dim 8i + dt). O / sum goes to att and, with xq, each
-// lane's 32 dims (one whole 32-block) to q8_32. The math is the reference's
-// (src/model.c:123-142: scores, softmax, weighted values) in fp32 with a
-// different order of additions.
+// (64-token tile, query head) of 8 waves, wave w taking the 16 query tokens
+// 16(w%4).. and key half w/4 of every chunk. The tile's rotated query rows
+// are staged through LDS into registers once; then per 64-key chunk (keys and
+// values staged in LDS, rows 132 floats apart) each wave forms its half of
+// S^T = K Q^T with v_mfma_f32_16x16x4_f32 (2 key tiles x 32 steps, lane l's
+// steps taking dims 32(l/16) + s), masks keys past each token's position,
+// keeps its own running max and sum per token (online softmax, -inf scores
+// weigh 0), and adds V^T P^T into its O^T (8 dim tiles x 8 steps; step
+// (t, v) is keys 16t + 4k + v for lane group k, which is where the S^T
+// layout left p, and tile dt row i is dim 8i + dt). The two halves of a
+// token meet once at the end (max, rescaled sums and outputs through LDS);
+// O / sum goes to att and, with xq, each lane's 32 dims (one whole 32-block)
+// to q8_32. The math is the reference's (src/model.c:123-142: scores,
+// softmax, weighted values) in fp32 with a different order of additions.
 typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kFlashPos = 512;   // positions a pass may reach for this kernel
 constexpr int kFlashRow = 132;   // floats per staged key / value / query row
-__global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restrict__ q_all,
+__global__ __launch_bounds__(512, 1) void attn_flash_kernel(const float *__restrict__ q_all,
                                                             const float2 *__restrict__ rope,
                                                             const float *__restrict__ kc, const float *__restrict__ vc,
                                                             const int *__restrict__ posv, float *__restrict__ att,
                                                             int8_t *__restrict__ xq, float *__restrict__ xs, int H,
                                                             int KVH, int max_seq, int ntok, float scale) {
-	constexpr int HD = 128, HALF = 64;
-	__shared__ __align__(16) float k_s[64 * kFlashRow];   // keys of the chunk (first: the tile's queries)
-	__shared__ __align__(16) float v_s[64 * kFlashRow];   // values of the chunk
+	constexpr int HD = 128, HALF = 64, NT = 512;
+	// keys of the chunk (first: the tile's queries), then its values; at the
+	// end the combine area of the key halves (4 x 64 lanes x 34 floats)
+	__shared__ __align__(16) float kv_s[2 * 64 * kFlashRow];
+	float *k_s = kv_s, *v_s = kv_s + 64 * kFlashRow;
+	static_assert(4 * 64 * 34 <= 2 * 64 * kFlashRow, "combine area inside the chunk rows");
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int qg = wave & 3, kh = wave >> 2;   // query group, key half
 	const int qi = lane & 15, kg = lane >> 4;
 	const int t0 = blockIdx.x * 64, h = blockIdx.y, kvh = h / (H / KVH);
 	const int KV = KVH * HD, D = H * HD;
-	const int tq = t0 + 16 * wave + qi;   // this lane's query token
+	const int tq = t0 + 16 * qg + qi;   // this lane's query token
 	int pos_q = tq < ntok ? posv[tq] : -1;
 	pos_q = pos_q < max_seq ? pos_q : -1;
 	const int plast = posv[min(t0 + 63, ntok - 1)];   // positions rise with the token
@@ -731,8 +737,8 @@ __global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restr
 
 	// 1. the tile's rotated query rows (NeoX rope at each token's position) into k_s
 #pragma unroll 4
-	for (int r = 0; r < 16; r++) {
-		const int e = tid + 256 * r, i = e >> 6, p = e & 63;
+	for (int r = 0; r < 64 * HALF / NT; r++) {
+		const int e = tid + NT * r, i = e >> 6, p = e & 63;
 		const int tok = min(t0 + i, ntok - 1);
 		const int pos = min(max(posv[tok], 0), max_seq - 1);
 		const float *q = q_all + (size_t)tok * D + h * HD;
@@ -744,7 +750,7 @@ __global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restr
 	__syncthreads();
 	float qv[32];   // Q[query qi][32 kg + s]
 	{
-		const float *src = k_s + (16 * wave + qi) * kFlashRow + 32 * kg;
+		const float *src = k_s + (16 * qg + qi) * kFlashRow + 32 * kg;
 #pragma unroll
 		for (int i = 0; i < 8; i++) {
 			const float4 t = *(const float4 *)(src + 4 * i);
@@ -764,20 +770,20 @@ __global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restr
 		// 2. the chunk's keys and values (rows past the tile's last position
 		//    read that row: in bounds, masked below)
 #pragma unroll
-		for (int r = 0; r < 8; r++) {
-			const int e = tid + 256 * r, row = e >> 5, f = e & 31;
+		for (int r = 0; r < 64 * 32 / NT; r++) {
+			const int e = tid + NT * r, row = e >> 5, f = e & 31;
 			const int key = min(64 * c + row, plast);
 			const uint32_t off = ((uint32_t)key * KV + kvh * HD + 4 * f) * 4u;
 			*(float4 *)(k_s + row * kFlashRow + 4 * f) = __builtin_bit_cast(float4, ld_b128(krs, off));
 			*(float4 *)(v_s + row * kFlashRow + 4 * f) = __builtin_bit_cast(float4, ld_b128(vrs, off));
 		}
 		__syncthreads();
-		// 3. S^T tiles: keys 16t + 4kg + v of this lane, query qi
-		v4f sc[4];
+		// 3. this wave's S^T tiles: keys 32kh + 16t + 4kg + v, query qi
+		v4f sc[2];
 #pragma unroll
-		for (int t = 0; t < 4; t++) {
+		for (int t = 0; t < 2; t++) {
 			v4f a = zero;
-			const float *kr = k_s + (16 * t + qi) * kFlashRow + 32 * kg;
+			const float *kr = k_s + (32 * kh + 16 * t + qi) * kFlashRow + 32 * kg;
 #pragma unroll
 			for (int i = 0; i < 8; i++) {
 				const float4 kv = *(const float4 *)(kr + 4 * i);
@@ -788,13 +794,14 @@ __global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restr
 			}
 			sc[t] = a;
 		}
-		// 4. online softmax of query qi (its 64 keys over lanes qi, qi+16, qi+32, qi+48)
+		// 4. online softmax of query qi over this half's 32 keys (lanes qi,
+		//    qi+16, qi+32, qi+48 of the wave)
 		float mc = -INFINITY;
 #pragma unroll
-		for (int t = 0; t < 4; t++)
+		for (int t = 0; t < 2; t++)
 #pragma unroll
 			for (int v = 0; v < 4; v++) {
-				const int key = 64 * c + 16 * t + 4 * kg + v;
+				const int key = 64 * c + 32 * kh + 16 * t + 4 * kg + v;
 				sc[t][v] = key <= pos_q ? sc[t][v] * scale : -INFINITY;
 				mc = __builtin_fmaxf(mc, sc[t][v]);
 			}
@@ -804,7 +811,7 @@ __global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restr
 		const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
 		float ps = 0.0f;
 #pragma unroll
-		for (int t = 0; t < 4; t++)
+		for (int t = 0; t < 2; t++)
 #pragma unroll
 			for (int v = 0; v < 4; v++) {
 				const float p = sc[t][v] == -INFINITY ? 0.0f : expf(sc[t][v] - m_new);
@@ -819,28 +826,43 @@ __global__ __launch_bounds__(256, 2) void attn_flash_kernel(const float *__restr
 		for (int dt = 0; dt < 8; dt++)
 #pragma unroll
 			for (int v = 0; v < 4; v++) acco[dt][v] *= alpha;
-		// 5. O^T += V^T P^T: step (t, v) = keys 16t + 4kg + v, tile dt row i = dim 8i + dt
+		// 5. O^T += V^T P^T: step (t, v) = keys 32kh + 16t + 4kg + v, tile dt row i = dim 8i + dt
 #pragma unroll
-		for (int t = 0; t < 4; t++)
+		for (int t = 0; t < 2; t++)
 #pragma unroll
 			for (int v = 0; v < 4; v++) {
-				const float *vr = v_s + (16 * t + 4 * kg + v) * kFlashRow + 8 * qi;
+				const float *vr = v_s + (32 * kh + 16 * t + 4 * kg + v) * kFlashRow + 8 * qi;
 				const float4 va = *(const float4 *)vr, vb = *(const float4 *)(vr + 4);
 				const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
 				for (int dt = 0; dt < 8; dt++)
 					acco[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[dt], sc[t][v], acco[dt], 0, 0, 0);
 			}
-		__syncthreads();   // before the next chunk's rows land
+		__syncthreads();   // before the next chunk's rows land (and, last, before the combine)
 	}
-	// 6. O / sum: this lane holds dims 32kg + 8v + dt of query qi (one 32-block)
-	if (tq >= ntok || pos_q < 0) return;
-	const float inv_l = 1.0f / l_run;
+	// 6. the two key halves of each token: half 1 hands (m, l, O) to half 0
+	//    through LDS (the chunk rows are free)
+	float *x_s = kv_s + (size_t)(qg * 64 + lane) * 34;
+	if (kh == 1) {
+#pragma unroll
+		for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+			for (int v = 0; v < 4; v++) x_s[4 * dt + v] = acco[dt][v];
+		x_s[32] = m_run;
+		x_s[33] = l_run;
+	}
+	__syncthreads();
+	if (kh == 1 || tq >= ntok || pos_q < 0) return;
+	const float m1 = x_s[32], l1 = x_s[33];
+	const float m = __builtin_fmaxf(m_run, m1);
+	const float a0 = m_run == -INFINITY ? 0.0f : expf(m_run - m), a1 = m1 == -INFINITY ? 0.0f : expf(m1 - m);
+	const float inv_l = 1.0f / (l_run * a0 + l1 * a1);
+	// this lane holds dims 32kg + 8v + dt of query qi (one 32-block)
 	float o[32];
 #pragma unroll
 	for (int v = 0; v < 4; v++)
 #pragma unroll
-		for (int dt = 0; dt < 8; dt++) o[8 * v + dt] = acco[dt][v] * inv_l;
+		for (int dt = 0; dt < 8; dt++) o[8 * v + dt] = (acco[dt][v] * a0 + x_s[4 * dt + v] * a1) * inv_l;
 	const size_t ob = (size_t)tq * D + h * HD + 32 * kg;
 #pragma unroll
 	for (int i = 0; i < 8; i++) *(float4 *)(att + ob + 4 * i) = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
@@ -1632,7 +1654,7 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 		const dim3 ag(pchunks, KVH, n), mg(G, KVH, n);
 		if (HD == 128 && pos0 + n <= kFlashPos) {
 			// every token's keys in one workgroup: matrix cores, no merge pass
-			hipLaunchKernelGGL(attn_flash_kernel, dim3((n + 63) / 64, m.n_heads), dim3(256), 0, stream(), d->pf_q,
+			hipLaunchKernelGGL(attn_flash_kernel, dim3((n + 63) / 64, m.n_heads), dim3(512), 0, stream(), d->pf_q,
 			                   d->rope, kcl, vcl, d->pf_pos, d->pf_att, mxq, mxs, m.n_heads, KVH, d->max_seq, n, scale);
 			HK_LAUNCHED("attention");
 		} else if (HD == 128) {
