@@ -248,16 +248,17 @@ def cpu_prefill_baseline(qtype: int, m: int, n_out: int, n_in: int, seed: int) -
             "host": host_info()}
 
 
-def bench_decode(g, steps: int, cpu_steps: int, seed: int = 30) -> dict:
-    """Greedy decode of a Qwen2.5-3B-shaped model (36 layers, Q4_K_M mix, tied
-    Q6_K embedding, random weights) with the KV cache prefilled to 1024
-    positions of seeded N(0,1) keys and values: `steps` graph-replayed device
-    steps; the reference's own hakm_forward on the same file and cache timed
-    for `cpu_steps` tokens on the host cores."""
+def bench_decode(g, steps: int, cpu_steps: int, seed: int = 30, shape: str = "3b") -> dict:
+    """Batch-1 greedy decode with the KV cache prefilled to 1024 positions of
+    seeded N(0,1) keys and values: shape "3b" is the Qwen2.5-3B shape (36
+    layers, Q4_K_M mix, tied Q6_K embedding), "7b" the Qwen2-7B shape (28
+    layers, Q4_K attn/gate/up, Q6_K down and untied output), random weights.
+    `steps` graph-replayed device steps; the reference's own hakm_forward on
+    the same file and cache timed for `cpu_steps` tokens on the host cores."""
     import tempfile
     from hako_amd import mlf2
     from hako_amd.decoder import Decoder
-    cfg, pos = mlf2.QWEN2_3B, 1024
+    cfg, pos = (mlf2.QWEN2_3B if shape == "3b" else mlf2.QWEN2_7B), 1024
     max_seq = pos + steps + 8
     kvd = cfg.n_kv_heads * cfg.head_dim
     fd, path = tempfile.mkstemp(suffix=".mlf2")
@@ -282,12 +283,15 @@ def bench_decode(g, steps: int, cpu_steps: int, seed: int = 30) -> dict:
             ms = g.elapsed_ms(e0, e1)
         finally:
             dec.close()
-        weight_bytes = sum(e[4] for e in info.values())
+        # an untied embedding contributes one row per token, not its matrix
+        weight_bytes = sum(e[4] for name, e in info.items() if cfg.tied or name != "token_embd.weight")
         kv_bytes = cfg.n_layers * 2 * kvd * 4 * (pos + 1 + steps // 2)
         per_tok = weight_bytes + kv_bytes
         us = ms * 1e3 / steps
-        res = {"workload": "Qwen2.5-3B-shaped greedy decode (36 layers, Q4_K attn/gate/up, Q6_K down and tied "
-                           "embedding), batch 1, KV cache from position 1024",
+        res = {"workload": ("Qwen2.5-3B-shaped greedy decode (36 layers, Q4_K attn/gate/up, Q6_K down and tied "
+                            "embedding), batch 1, KV cache from position 1024") if shape == "3b" else
+                           ("Qwen2-7B-shaped greedy decode (28 layers, Q4_K attn/gate/up, Q6_K down and untied "
+                            "output), batch 1, KV cache from position 1024"),
                "steps": steps, "us_per_token": round(us, 2), "tok_per_s": round(1e6 / us, 1),
                "bytes_per_token": per_tok, "gbps": round(per_tok / (us * 1e-6) / 1e9, 1),
                "hbm_frac": round(per_tok / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
@@ -503,7 +507,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "decode", "decode16", "prompt", "prefill"],
+    ap.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "decode", "decode7b", "decode16", "prompt",
+                                                          "prefill"],
                     help="run one workload and print its timing only (profiling runs)")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     ap.add_argument("--decode-steps", type=int, default=100)
@@ -525,9 +530,11 @@ def main():
     info = g.info()
     log(f"device {info.name.decode()} CUs={info.compute_units} HBM={info.hbm_bytes / 2**30:.0f} GiB")
 
-    if args.only in ("decode", "decode16", "prompt", "prefill"):
+    if args.only in ("decode", "decode7b", "decode16", "prompt", "prefill"):
         if args.only == "decode":
             r = bench_decode(g, args.decode_steps, 0)
+        elif args.only == "decode7b":
+            r = bench_decode(g, args.decode_steps, 0, seed=35, shape="7b")
         elif args.only == "decode16":
             r = bench_decode_batched(g, args.batched_steps, 0)
         elif args.only == "prompt":
@@ -572,6 +579,13 @@ def main():
         log(f"decode: {decode['us_per_token']:.1f} us/token, {decode['tok_per_s']:.1f} tok/s, "
             f"{decode['gbps']:.0f} GB/s" + (f"; cpu {decode['cpu_baseline']['value']:.2f} tok/s"
                                           if 'cpu_baseline' in decode else ""))
+    decode7 = None
+    if not args.no_decode:
+        decode7 = bench_decode(g, args.decode_steps, 0 if args.no_cpu else args.cpu_decode_steps, seed=35,
+                               shape="7b")
+        log(f"decode 7B: {decode7['us_per_token']:.1f} us/token, {decode7['tok_per_s']:.1f} tok/s, "
+            f"{decode7['gbps']:.0f} GB/s" + (f"; cpu {decode7['cpu_baseline']['value']:.2f} tok/s"
+                                           if 'cpu_baseline' in decode7 else ""))
     batched = None
     if not args.no_decode:
         batched = bench_decode_batched(g, args.batched_steps, 0 if args.no_cpu else args.cpu_batched_steps)
@@ -610,6 +624,7 @@ def main():
         "single_launch_us": round(head["single_launch_us"], 3),
         "extra": extra,
         "decode": decode,
+        "decode_7b": decode7,
         "decode_batched": batched,
         "prompt_prefill": prompt,
         "prefill": prefill,

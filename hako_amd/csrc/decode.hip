@@ -43,6 +43,11 @@ constexpr int kMaxG = 8;     // query heads per KV head
 constexpr int kArgBlocks = 64;
 constexpr int kDecItems = 4; // row items per wave of the fused GEMV
 constexpr int kDecItemsQkv = 2; // ... of the q/k/v launch (fewer rows: more workgroups)
+// ... of the gate/up launch: 0 = by shape (8 when a row item is one row,
+// d_model > 2048: half the workgroups, each repeating the rmsnorm prologue
+// over the whole activation; 7B step 1781 -> 1744 us, the 3B shape slower
+// with 8), else 4 or 8 (tuning knob)
+int g_dec_gu_items = 0;
 
 // One sequence's output projection adds its per-input-block row sums into a
 // residual accumulator of 64-bit fixed-point values (2^-32 units): integer
@@ -1147,6 +1152,9 @@ bool known_type(int t) {
 }
 
 }  // namespace
+
+void dec_set_gu_items(int v) { g_dec_gu_items = (v == 4 || v == 8) ? v : 0; }
+
 }  // namespace hako
 
 using namespace hako;
@@ -1468,6 +1476,7 @@ int enqueue_step(hako_gpu_decoder *d) {
 		// 4. gate, up, SwiGLU (after merge_o: on x + the accumulator, that sum
 		// kept in xa as the residual of step 5)
 		const float *resid = d->x;
+		const int gu_items = g_dec_gu_items ? g_dec_gu_items : (D > 2048 ? 8 : kDecItems);
 		if (fused_gu) {
 			DecSegs s{};
 			s.n = 2;
@@ -1475,8 +1484,12 @@ int enqueue_step(hako_gpu_decoder *d) {
 			s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, 0, F};
 			if (merge_o) {
 				// (a workgroup must not clear what the others still read)
-				if (int rc = launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F, oacc, d->xa,
-				                                              self_next ? d->oacc + (size_t)3 * D : oacc_next))
+				long long *on = self_next ? d->oacc + (size_t)3 * D : oacc_next;
+				if (int rc = gu_items == 8
+				                 ? launch_dec<kProNorm, kEpiSwiGLU, 8>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F, oacc,
+				                                                       d->xa, on)
+				                 : launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F, oacc,
+				                                                    d->xa, on))
 					return rc;
 				if (self_next) {
 					hipLaunchKernelGGL(oacc_apply_kernel, dim3((D + 255) / 256), dim3(256), 0, stream(), d->tmp,
@@ -1484,7 +1497,9 @@ int enqueue_step(hako_gpu_decoder *d) {
 					HK_LAUNCHED("residual accumulator clear");
 				}
 				resid = d->xa;
-			} else if (int rc = launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)) {
+			} else if (int rc = gu_items == 8
+			                        ? launch_dec<kProNorm, kEpiSwiGLU, 8>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)
+			                        : launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)) {
 				return rc;
 			}
 		} else {

@@ -31,6 +31,7 @@ void q4k_set_flat_items(int v);
 // Target workgroups of the skinny (<= 16 token) launches (0: default).
 void q4k_skinny_set_target_wgs(int wgs);
 void q6k_skinny_set_target_wgs(int wgs);
+void dec_set_gu_items(int v);
 // Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
 int workspace(int slot, size_t bytes, void **ptr);
 // Look up this device's address of the no-allocation scratch array (with

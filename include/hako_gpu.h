@@ -67,6 +67,7 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_SKINNY_Q4K_WGS 6
 #define HAKO_TUNE_SKINNY_Q6K_WGS 7
 #define HAKO_TUNE_Q6K_FLAT_ITEMS 8   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
+#define HAKO_TUNE_DEC_GU_ITEMS   9   /* one-sequence decoder gate/up launch: row items per wave, 4 or 8, or 0 = by shape (default); read when a step is enqueued or captured */
 int hako_gpu_tune(int knob, int value);
 
 typedef struct {

@@ -278,3 +278,77 @@ def test_steps_are_bit_reproducible(gpu, tmp_path, cfg, seed, pos):
     for r in runs[1:]:
         assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32))
     assert toks[0] == toks[1]
+
+
+@pytest.mark.timeout(600)
+def test_qwen2_7b_decode_at_position_1024(gpu, ref, tmp_path):
+    """The full Qwen2-7B shape (28 layers, d_model 3584, 28/4 heads, ffn
+    18944, Q4_K attn/gate/up, Q6_K down and untied Q6_K output 152064 x 3584)
+    through the one-sequence step, KV cache prefilled to 1024 positions:
+    greedy tokens equal the reference's forward (src/model.c:93-165) over four
+    steps, and four distinct start tokens, one step each from the same cache,
+    give its argmax and logits."""
+    from dropin import prefilled_greedy
+    cfg = mlf2.QWEN2_7B
+    path = str(tmp_path / "qwen2_7b.mlf2")
+    mlf2.write_qwen2(path, cfg, 60)
+    pos, max_seq, steps = 1024, 1040, 4
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    kv = np.random.default_rng(61).standard_normal((2, cfg.n_layers, pos, kvd)).astype(np.float32)
+    starts = [int(t) for t in np.random.default_rng(62).choice(cfg.vocab, 4, replace=False)]
+    want, want_logits = prefilled_greedy(ref, path, kv, pos, start=starts[0], steps=steps, vocab=cfg.vocab,
+                                         max_seq=max_seq)
+    want_one = [prefilled_greedy(ref, path, kv, pos, start=t, steps=1, vocab=cfg.vocab, max_seq=max_seq)[1][0]
+                for t in starts[1:]]
+    assert np.all(np.isfinite(want_logits))
+    dec = make_decoder(gpu, path, max_seq=max_seq)
+    try:
+        k, v = dec.kv()
+        for l in range(cfg.n_layers):
+            gpu.h2d(k + dec.kv_offset(0, l, 0), kv[0, l])
+            gpu.h2d(v + dec.kv_offset(0, l, 0), kv[1, l])
+        dec.set_pos(pos)
+        first, lg = dec.step(starts[0], logits=True)
+        got = [int(first[0])] + dec.generate(int(first[0]), steps - 1)[:, 0].tolist()
+        got_one = []
+        for t in starts[1:]:
+            dec.set_pos(pos)
+            nxt, l1 = dec.step(t, logits=True)
+            assert int(nxt[0]) == int(np.argmax(l1[0]))
+            got_one.append(l1[0])
+    finally:
+        dec.close()
+    assert got == want
+    # measured: 8.5e-6 (first start), 9.9e-6 .. 1.1e-5 over the other three
+    within(f"7B logits, start {starts[0]}", lg[0], want_logits[0], 6e-5)
+    assert [int(np.argmax(r)) for r in got_one] == [int(np.argmax(r)) for r in want_one]
+    for t, g, w in zip(starts[1:], got_one, want_one):
+        within(f"7B logits, start {t}", g, w, 6e-5)
+
+
+def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
+    """The gate/up launch's row items per wave (4 or 8; by shape by default)
+    changes only which workgroup computes a row, never the order of a row's
+    additions: three greedy steps give bit-identical logits either way."""
+    cfg = GQA7
+    path = str(tmp_path / "gqa7.mlf2")
+    mlf2.write_qwen2(path, cfg, 21)
+    HAKO_TUNE_DEC_GU_ITEMS = 9
+    runs = []
+    try:
+        for items in (4, 8):
+            gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, items)
+            dec = make_decoder(gpu, path, max_seq=64)
+            try:
+                tok, lg = 7, []
+                for _ in range(3):
+                    nxt, l1 = dec.step(tok, logits=True)
+                    lg.append(l1[0].copy())
+                    tok = int(nxt[0])
+            finally:
+                dec.close()
+            runs.append(np.stack(lg))
+    finally:
+        gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, 0)
+    assert np.all(np.isfinite(runs[0]))
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
