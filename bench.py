@@ -107,8 +107,11 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
                 launch(k)
             return g.capture_end()
         # the timed launches start on the weight copy after the warm-up's last,
-        # so none of them finds its weights left in the last-level cache
-        warm, timed = capture(0, max(warmup, 1)), capture(max(warmup, 1), steps)
+        # so none of them finds its weights left in the last-level cache; the
+        # warm-up graph holds at least 64 launches, so the host queues its
+        # replays faster than the GPU runs them
+        nwarm = max(warmup, 64)
+        warm, timed = capture(0, nwarm), capture(nwarm, steps)
         # the warm-up graph replayed for at least 30 ms: a GPU idle during the
         # host-side set-up runs its first milliseconds at lower clocks
         g.record(e0)
@@ -117,7 +120,10 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
         reps = int(math.ceil(30.0 / max(g.elapsed_ms(e0, e1), 1e-3)))
         for _ in range(min(reps, 1000)):
             g.graph_launch(warm)
-        g.sync()
+        # no synchronization here: the timed graph is queued while the warm-up
+        # still runs, and e0 completes when the warm-up's last launch does,
+        # so the timed region holds the K launches and not the start-up of a
+        # graph on an idle GPU (~14 us)
         g.record(e0)
         g.graph_launch(timed)
         g.record(e1)

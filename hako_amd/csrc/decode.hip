@@ -52,19 +52,42 @@ int g_dec_gu_items = 0;
 // One sequence's output projection adds its per-input-block row sums into a
 // residual accumulator of 64-bit fixed-point values (2^-32 units): integer
 // addition is associative, so the sum does not depend on the order in which
-// the blocks arrive and the step is bit-reproducible. |sum| stays below 2^31
-// for any activation a model produces (non-finite or larger sums saturate at
-// +-2^30). The value a block adds is its fp32 sum rounded to the 2^-32 grid;
-// the accumulated sum is converted back to fp32 once.
-constexpr double kFixScale = 4294967296.0;        // 2^32
-constexpr double kFixInv = 1.0 / 4294967296.0;    // 2^-32
-constexpr double kFixMax = 4611686018427387904.0; // 2^62
+// the blocks arrive and the step is bit-reproducible. The value a block adds
+// is its fp32 sum rounded to the 2^-32 grid; the accumulated sum is
+// converted back to fp32 once.
+//
+// An accumulator row is D int64 sums followed by D int32 flags. A block sum
+// that is not finite adds nothing to the sum and ORs its kind into the
+// row's flags (NaN, +inf, -inf), and the consumer turns a flagged row back
+// into what an fp32 sum of those terms gives: NaN for a NaN or for both
+// infinities, else the infinity — as the reference's fp32 fold and residual
+// add propagate them (src/quant.c:222-225, src/model.c:146). A finite block
+// sum is clamped to +-2^25 (2^57 units), so the sum of up to 64 blocks
+// (d_model <= 16384) cannot wrap; the decoder takes this path only within
+// that width, and no model's residual comes near 2^25.
+constexpr double kFixScale = 4294967296.0;          // 2^32
+constexpr double kFixInv = 1.0 / 4294967296.0;      // 2^-32
+constexpr double kFixMax = 144115188075855872.0;    // 2^57
+constexpr int kFixMaxBlocks = 64;                   // d_model / 256 blocks per row at most
+enum : int { kFlagNaN = 1, kFlagPosInf = 2, kFlagNegInf = 4 };
 __device__ __forceinline__ long long to_fixed(float f) {
+	if (!__builtin_isfinite(f)) return 0;
 	double v = (double)f * kFixScale;
-	v = __builtin_fmin(__builtin_fmax(v, -kFixMax), kFixMax);   // NaN -> -2^62 (fmax takes the number)
+	v = __builtin_fmin(__builtin_fmax(v, -kFixMax), kFixMax);
 	return (long long)__builtin_rint(v);
 }
-__device__ __forceinline__ float from_fixed(long long a) { return (float)((double)a * kFixInv); }
+__device__ __forceinline__ int fixed_flag(float f) {
+	return f != f ? kFlagNaN : (__builtin_isinf(f) ? (f > 0.0f ? kFlagPosInf : kFlagNegInf) : 0);
+}
+__device__ __forceinline__ float from_fixed(long long a, int flags) {
+	if (flags == 0) return (float)((double)a * kFixInv);
+	if ((flags & kFlagNaN) || (flags & (kFlagPosInf | kFlagNegInf)) == (kFlagPosInf | kFlagNegInf))
+		return __builtin_nanf("");
+	return (flags & kFlagPosInf) ? __builtin_inff() : -__builtin_inff();
+}
+// the flags of an accumulator row of n sums
+__device__ __forceinline__ int *acc_flags(long long *acc, int n) { return (int *)(acc + n); }
+__device__ __forceinline__ const int *acc_flags(const long long *acc, int n) { return (const int *)(acc + n); }
 
 // ── embedding row (deq_row, reference src/nn.c:55-59) ──
 
@@ -289,9 +312,10 @@ enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2 };
 // q8_32 scheme in the prologue, after rmsnorm with weight nw for kProNorm.
 //
 // OACC: the activation is x plus the fixed-point residual accumulator oacc
-// (the output projection's sums, merge_o_kernel), added in the prologue;
-// workgroup 0 stores that sum to xmid (the residual the down projection adds
-// to) and clears the accumulator oacc_next for the next layer's projection.
+// (the output projection's sums and their non-finite flags, merge_o_kernel),
+// added in the prologue; workgroup 0 stores that sum to xmid (the residual
+// the down projection adds to) and clears the accumulator oacc_next (sums and
+// flags) for the next layer's projection.
 template <int PRO, int EPI, int XP, int ITEMS, bool OACC = false>
 __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float *__restrict__ x,
                                                       const float *__restrict__ nw, float eps, int n_in,
@@ -337,6 +361,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 	// 1. activation (and norm weight) loads, then residual / bias, then weights
 	float4 xv[XP], nv[XP];
 	uint4 oa[XP][2];
+	int4 of[XP];
 #pragma unroll
 	for (int k = 0; k < XP; k++) {
 		const int e = min((int)(threadIdx.x + k * T) * 4, n_in - 4);
@@ -345,6 +370,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		if (OACC) {
 			oa[k][0] = *(const uint4 *)(oacc + e);
 			oa[k][1] = *(const uint4 *)(oacc + e + 2);
+			of[k] = *(const int4 *)(acc_flags(oacc, n_in) + e);
 		}
 	}
 	float pre[NG];   // bias (Store) or the residual (Add) of the row this lane writes
@@ -371,15 +397,15 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 
 	// 2. prologue: (residual accumulator,) (rmsnorm and) q8_32 quantization into LDS
 	if (OACC) {
-		auto fx = [](uint32_t lo, uint32_t hi) -> float {
-			return from_fixed((long long)(((unsigned long long)hi << 32) | lo));
+		auto fx = [](uint32_t lo, uint32_t hi, int fl) -> float {
+			return from_fixed((long long)(((unsigned long long)hi << 32) | lo), fl);
 		};
 #pragma unroll
 		for (int k = 0; k < XP; k++) {
-			xv[k].x += fx(oa[k][0].x, oa[k][0].y);
-			xv[k].y += fx(oa[k][0].z, oa[k][0].w);
-			xv[k].z += fx(oa[k][1].x, oa[k][1].y);
-			xv[k].w += fx(oa[k][1].z, oa[k][1].w);
+			xv[k].x += fx(oa[k][0].x, oa[k][0].y, of[k].x);
+			xv[k].y += fx(oa[k][0].z, oa[k][0].w, of[k].y);
+			xv[k].z += fx(oa[k][1].x, oa[k][1].y, of[k].z);
+			xv[k].w += fx(oa[k][1].z, oa[k][1].w, of[k].w);
 		}
 	}
 	float scale = 1.0f;
@@ -425,6 +451,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 				*(float4 *)(xmid + e) = xv[k];
 				*(uint4 *)(oacc_next + e) = make_uint4(0u, 0u, 0u, 0u);
 				*(uint4 *)(oacc_next + e + 2) = make_uint4(0u, 0u, 0u, 0u);
+				*(int4 *)(acc_flags(oacc_next, n_in) + e) = make_int4(0, 0, 0, 0);
 			}
 		}
 	}
@@ -1048,20 +1075,25 @@ __global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ 
 	float f = q4_fold(wb, 16u * (g & 1), g >= 2 ? ~0u : 0u, ia, ib, col);
 	f += __shfl_xor(f, 1);
 	f += __shfl_xor(f, 2);
-	if (g == 0 && row < D)
+	if (g == 0 && row < D) {
 		__hip_atomic_fetch_add(oacc + row, to_fixed(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		if (const int fl = fixed_flag(f))
+			__hip_atomic_fetch_or(acc_flags(oacc, D) + row, fl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+	}
 }
 
-// x = a + the fixed-point accumulator oacc, which is then cleared (the
-// merged output projection's residual add when no fused gate/up kernel
-// takes it), and oacc_next cleared for the next layer.
+// x += the fixed-point accumulator oacc (with its flags), which is then
+// cleared (the merged output projection's residual add when no fused gate/up
+// kernel takes it), and oacc_next cleared for the next layer.
 __global__ __launch_bounds__(256) void oacc_apply_kernel(float *__restrict__ x, long long *__restrict__ oacc,
                                                          long long *__restrict__ oacc_next, int n) {
 	const int i = blockIdx.x * 256 + threadIdx.x;
 	if (i < n) {
-		x[i] += from_fixed(oacc[i]);
+		x[i] += from_fixed(oacc[i], acc_flags(oacc, n)[i]);
 		oacc[i] = 0;
+		acc_flags(oacc, n)[i] = 0;
 		oacc_next[i] = 0;
+		acc_flags(oacc_next, n)[i] = 0;
 	}
 }
 
@@ -1119,16 +1151,20 @@ __global__ __launch_bounds__(256) void argmax_part_kernel(const float *__restric
 }
 
 // Grid (n_seq), one wave: the token of the blocks' best, appended to the ring;
-// the position advances.
-__global__ __launch_bounds__(64) void argmax_final_kernel(const float2 *__restrict__ part, int *tok, int *posv,
-                                                          int *ring, int ring_len, int *nout) {
+// the position advances. The reference's scan starts from logits[0] and
+// only a strictly larger value replaces it, so a NaN at index 0 is never
+// replaced (src/sample.c:28-31): token 0 then, whatever follows.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float2 *__restrict__ part,
+                                                          const float *__restrict__ logits, int V, int *tok,
+                                                          int *posv, int *ring, int ring_len, int *nout) {
 	const int sq = blockIdx.x, lane = threadIdx.x;
 	const float2 p = part[sq * kArgBlocks + lane];
+	const float l0 = logits[(size_t)sq * V];
 	float v = p.x;
 	int i = __builtin_bit_cast(int, p.y);
 	argmax_wave(v, i);
 	if (lane == 0) {
-		const int t = i == 0x7FFFFFFF ? 0 : i;   // all NaN: index 0, as the reference
+		const int t = (i == 0x7FFFFFFF || l0 != l0) ? 0 : i;   // all NaN, or NaN first: index 0
 		tok[sq] = t;
 		const int n = nout[sq];
 		if (n < ring_len) ring[(size_t)sq * ring_len + n] = t;
@@ -1308,8 +1344,8 @@ int argmax(hako_gpu_decoder *d) {
 	hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgBlocks, d->n_seq), dim3(256), 0, stream(), d->logits, d->m.vocab,
 	                   d->apart);
 	HK_LAUNCHED("argmax");
-	hipLaunchKernelGGL(argmax_final_kernel, dim3(d->n_seq), dim3(64), 0, stream(), d->apart, d->tok, d->pos, d->ring,
-	                   d->max_seq, d->nout);
+	hipLaunchKernelGGL(argmax_final_kernel, dim3(d->n_seq), dim3(64), 0, stream(), d->apart, d->logits, d->m.vocab,
+	                   d->tok, d->pos, d->ring, d->max_seq, d->nout);
 	HK_LAUNCHED("argmax final");
 	return HAKO_GPU_OK;
 }
@@ -1403,11 +1439,26 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 	return HAKO_GPU_OK;
 }
 
+// int64 words of one accumulator row: D sums and D int32 flags
+size_t acc_row(int D) { return (size_t)D + (size_t)D / 2; }
+
+// The attention merge joins the Q4_K output projection of one sequence
+// (merge_o_kernel) when every layer's projection can take it: each merged
+// layer clears the accumulator the next layer adds into, so a layer that
+// does not merge would leave the one after it a stale sum.
+bool merge_o_all(const hako_gpu_model &m, const std::vector<hako_gpu_block> &blocks) {
+	if (m.d_model % kQK || kQK % m.head_dim || m.d_model / kQK > kFixMaxBlocks) return false;
+	for (const hako_gpu_block &B : blocks)
+		if (B.t_o != HAKO_TYPE_Q4_K) return false;
+	return true;
+}
+
 // One decode step on the library stream (n_seq == 1).
 int enqueue_step(hako_gpu_decoder *d) {
 	if (d->n_seq > 1) return enqueue_batched_step(d);
 	const hako_gpu_model &m = d->m;
 	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim;
+	const bool merge_o = merge_o_all(m, d->blocks);
 	hipLaunchKernelGGL(embed_kernel, dim3(d->n_seq), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
 	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
 	HK_LAUNCHED("embed");
@@ -1435,14 +1486,15 @@ int enqueue_step(hako_gpu_decoder *d) {
 		// (merged with the attention records in one launch for Q4_K, its sums
 		// into the fixed-point accumulator of this layer, taken up by the
 		// gate/up kernel's prologue or by oacc_apply_kernel)
-		const bool merge_o = B.t_o == HAKO_TYPE_Q4_K && D % kQK == 0 && kQK % m.head_dim == 0;
 		const bool fused_gu = B.t_gate == HAKO_TYPE_Q4_K && B.t_up == HAKO_TYPE_Q4_K && fusable_q4(D);
 		// accumulators alternate by layer; with an odd layer count the last
 		// layer takes a third, so that it differs from the next step's layer 0
-		// (one layer: the same one, cleared by a launch of its own below)
+		// (one layer: the same one, cleared by a launch of its own below).
+		// Each merged layer clears the next layer's accumulator, so the merge
+		// is taken for all layers or none (merge_o_all).
 		auto acc_of = [&](int layer) -> long long * {
 			const int i = (m.n_layers & 1) && layer == m.n_layers - 1 && m.n_layers > 1 ? 2 : (layer & 1);
-			return d->oacc + (size_t)i * D;
+			return d->oacc + (size_t)i * acc_row(D);
 		};
 		long long *oacc = acc_of(l);
 		long long *oacc_next = acc_of(l + 1 == m.n_layers ? 0 : l + 1);
@@ -1484,7 +1536,7 @@ int enqueue_step(hako_gpu_decoder *d) {
 			s.s[1] = {(const uint8_t *)B.up, nullptr, d->h, 0, F};
 			if (merge_o) {
 				// (a workgroup must not clear what the others still read)
-				long long *on = self_next ? d->oacc + (size_t)3 * D : oacc_next;
+				long long *on = self_next ? d->oacc + (size_t)3 * acc_row(D) : oacc_next;
 				if (int rc = gu_items == 8
 				                 ? launch_dec<kProNorm, kEpiSwiGLU, 8>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F, oacc,
 				                                                       d->xa, on)
@@ -1804,7 +1856,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	HK_ALLOC(d->pos, sizeof(int) * n_seq);
 	HK_ALLOC(d->ring, sizeof(int) * n_seq * max_seq);
 	HK_ALLOC(d->nout, sizeof(int) * n_seq);
-	HK_ALLOC(d->oacc, sizeof(long long) * 4 * D);   // three accumulators and a scratch row
+	HK_ALLOC(d->oacc, sizeof(long long) * 4 * acc_row(D));   // three accumulators and a scratch row
 	HK_ALLOC(d->xa, sizeof(float) * D);
 	const int DF = F > D ? F : D;
 	// split-K partials of the largest skinny matmul of a step
@@ -1843,7 +1895,7 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	if (e == hipSuccess) e = hipMemset(d->vc, 0, sizeof(float) * kvn);
 	if (e == hipSuccess) e = hipMemset(d->pos, 0, sizeof(int) * n_seq);
 	if (e == hipSuccess) e = hipMemset(d->nout, 0, sizeof(int) * n_seq);
-	if (e == hipSuccess) e = hipMemset(d->oacc, 0, sizeof(long long) * 4 * D);
+	if (e == hipSuccess) e = hipMemset(d->oacc, 0, sizeof(long long) * 4 * acc_row(D));
 	if (e == hipSuccess) e = hipDeviceSynchronize();
 	if (e != hipSuccess) {
 		hako_gpu_decoder_destroy(d);

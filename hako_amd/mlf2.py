@@ -52,6 +52,9 @@ class Qwen2Config:
     down_type: int = synth.TYPE_Q6_K
     embd_type: int = synth.TYPE_Q6_K
     out_type: int = synth.TYPE_Q6_K
+    # per-layer exceptions: ((layer, role), type) pairs, role one of attn_q,
+    # attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down
+    layer_types: tuple = ()
 
 
 # The two model shapes the benchmarks use (Qwen2.5-3B and Qwen2-7B).
@@ -67,22 +70,26 @@ def tensor_plan(cfg: Qwen2Config):
     (reference src/model.c:30-57), in directory order. 1-D tensors have
     n_out = 1."""
     D, F, KV = cfg.d_model, cfg.ffn_dim, cfg.n_kv_heads * cfg.head_dim
+    over = dict(cfg.layer_types)
     plan = [("token_embd.weight", cfg.embd_type, D, cfg.vocab)]
     for l in range(cfg.n_layers):
         p = f"blk.{l}."
+
+        def t(role, default):
+            return over.get((l, role), default)
         plan += [(p + "attn_norm.weight", synth.TYPE_F32, D, 1),
-                 (p + "attn_q.weight", cfg.attn_type, D, D),
-                 (p + "attn_k.weight", cfg.attn_type, D, KV),
-                 (p + "attn_v.weight", cfg.attn_type, D, KV)]
+                 (p + "attn_q.weight", t("attn_q", cfg.attn_type), D, D),
+                 (p + "attn_k.weight", t("attn_k", cfg.attn_type), D, KV),
+                 (p + "attn_v.weight", t("attn_v", cfg.attn_type), D, KV)]
         if cfg.qkv_bias:
             plan += [(p + "attn_q.bias", synth.TYPE_F32, D, 1),
                      (p + "attn_k.bias", synth.TYPE_F32, KV, 1),
                      (p + "attn_v.bias", synth.TYPE_F32, KV, 1)]
-        plan += [(p + "attn_output.weight", cfg.attn_type, D, D),
+        plan += [(p + "attn_output.weight", t("attn_output", cfg.attn_type), D, D),
                  (p + "ffn_norm.weight", synth.TYPE_F32, D, 1),
-                 (p + "ffn_gate.weight", cfg.gate_up_type, D, F),
-                 (p + "ffn_up.weight", cfg.gate_up_type, D, F),
-                 (p + "ffn_down.weight", cfg.down_type, F, D)]
+                 (p + "ffn_gate.weight", t("ffn_gate", cfg.gate_up_type), D, F),
+                 (p + "ffn_up.weight", t("ffn_up", cfg.gate_up_type), D, F),
+                 (p + "ffn_down.weight", t("ffn_down", cfg.down_type), F, D)]
     plan.append(("output_norm.weight", synth.TYPE_F32, D, 1))
     if not cfg.tied:
         plan.append(("output.weight", cfg.out_type, D, cfg.vocab))

@@ -211,6 +211,30 @@ class HakmCtx(C.Structure):
 assert C.sizeof(HakmCtx) == 344
 
 
+class Sampler(C.Structure):
+    """The reference's sampler (src/sample.h:6-11); temp <= 0 is greedy."""
+    _fields_ = [("temp", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int), ("rng", C.c_uint64)]
+
+
+_PICK = None
+
+
+def ref_greedy_pick(logits: np.ndarray) -> int:
+    """The reference's greedy pick (sample_token with temp 0,
+    src/sample.c:27-32, from the compiled reference): the scan starts from
+    logits[0] and only a strictly larger value replaces the best, so the
+    first maximum wins, a NaN never does, and a NaN at index 0 is kept."""
+    global _PICK
+    if _PICK is None:
+        lib = C.CDLL(REF_LIB)
+        lib.sample_token.restype = C.c_int
+        lib.sample_token.argtypes = [C.POINTER(Sampler), _vp, _i]
+        _PICK = lib
+    lg = np.ascontiguousarray(logits, np.float32).copy()
+    s = Sampler(0.0, 0.0, 0, 1)
+    return int(_PICK.sample_token(C.byref(s), _p(lg), lg.size))
+
+
 def prefilled_greedy(lib: C.CDLL, path: str, kv: np.ndarray, pos: int, start: int, steps: int, vocab: int,
                      max_seq: int, times: list | None = None, release=None):
     """Greedy decode through the reference's model.h API after writing the
@@ -235,7 +259,7 @@ def prefilled_greedy(lib: C.CDLL, path: str, kv: np.ndarray, pos: int, start: in
                 times.append(time.perf_counter() - t0)
             lg = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(vocab,)).copy()
             logits.append(lg)
-            toks.append(int(np.argmax(lg)))
+            toks.append(ref_greedy_pick(lg))
     finally:
         if release is not None:
             release(ctx)

@@ -76,7 +76,7 @@ def greedy(lib: C.CDLL, path: str, start: int, steps: int, vocab: int, max_seq: 
             p = lib.hakm_forward(ctx, toks[-1])
             lg = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(vocab,)).copy()
             logits.append(lg)
-            toks.append(int(np.argmax(lg)))   # first maximum, as src/sample.c:28-32
+            toks.append(ref_greedy_pick(lg))   # the reference's own pick, src/sample.c:28-32
     finally:
         if release is not None:
             release(ctx)
@@ -84,4 +84,4 @@ def greedy(lib: C.CDLL, path: str, start: int, steps: int, vocab: int, max_seq: 
     return toks[1:], np.stack(logits)
 
 
-from oracle.hako_oracle import HakmCtx, prefilled_greedy  # noqa: E402,F401
+from oracle.hako_oracle import HakmCtx, prefilled_greedy, ref_greedy_pick  # noqa: E402,F401

@@ -352,3 +352,112 @@ def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
         gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, 0)
     assert np.all(np.isfinite(runs[0]))
     assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+
+
+# Per-layer mixes of weight types (the reference's matmul takes any type per
+# tensor, src/nn.c:179-210): an output projection that is not Q4_K in some
+# layers, the last layer's among them, and FFN matrices of other types.
+MIXED_O = mlf2.Qwen2Config(n_layers=4, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=768,
+                           vocab=1024, ctx=256,
+                           layer_types=(((1, "attn_output"), synth.TYPE_Q6_K), ((3, "attn_output"), synth.TYPE_F16)))
+MIXED_FFN = mlf2.Qwen2Config(n_layers=3, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=768,
+                             vocab=1024, ctx=256, tied=False, embd_type=synth.TYPE_Q4_K,
+                             layer_types=(((0, "attn_output"), synth.TYPE_F16), ((1, "ffn_gate"), synth.TYPE_Q6_K),
+                                          ((1, "ffn_up"), synth.TYPE_Q6_K), ((2, "ffn_down"), synth.TYPE_Q4_K),
+                                          ((2, "attn_v"), synth.TYPE_Q6_K)))
+
+
+@pytest.mark.parametrize("cfg,seed,bar", [(MIXED_O, 25, 2e-5), (MIXED_FFN, 14, 2e-5)])
+def test_mixed_layer_types_match_reference(gpu, ref, tmp_path, cfg, seed, bar):
+    """Greedy tokens and logits of models whose layers differ in their
+    matrices' types, eager steps and the captured graph, against the
+    reference's forward."""
+    from dropin import greedy
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, seed)
+    steps = 16
+    want, want_logits = greedy(ref, path, start=3, steps=steps, vocab=cfg.vocab, max_seq=128)
+    assert np.all(np.isfinite(want_logits))
+    dec = make_decoder(gpu, path, max_seq=128)
+    try:
+        dec.set_pos(0)
+        got, logits, tok = [], [], 3
+        for _ in range(4):
+            nxt, lg = dec.step(tok, logits=True)
+            tok = int(nxt[0])
+            got.append(tok)
+            logits.append(lg[0])
+        got += dec.generate(tok, steps - 4)[:, 0].tolist()
+    finally:
+        dec.close()
+    assert got == want
+    within(f"mixed-type logits {seed}", np.stack(logits), want_logits[:4], bar)
+
+
+def plant(path: str, info: dict, name: str, where, value: float):
+    """Overwrite one value of tensor `name` in an MLF2 file: element `where`
+    of an F32 tensor, or the fp16 scale d of block (row, block) `where` of a
+    Q4_K (bytes 0-1) or Q6_K (bytes 208-209) matrix."""
+    qt, n_in, _, off, _ = info[name]
+    f = mlf2.Mlf2File(path)
+    base = f.header["data_off"] + off
+    del f
+    if qt == synth.TYPE_F32:
+        at, data = base + 4 * where, np.float32(value).tobytes()
+    else:
+        r, b = where
+        bsz = synth.Q4K_BYTES if qt == synth.TYPE_Q4_K else synth.Q6K_BYTES
+        at = base + r * synth.row_nbytes(qt, n_in) + b * bsz + (0 if qt == synth.TYPE_Q4_K else 208)
+        data = np.float16(value).tobytes()
+    with open(path, "r+b") as fh:
+        fh.seek(at)
+        fh.write(data)
+
+
+# (tensor, element or (row, block), value): NaN in norm weights and a bias
+# (the q8 quantizer of the next Q4_K matmul maps NaN to code 0, so the
+# reference's logits stay finite, or all turn NaN through the fp32 lm_head);
+# a non-finite scale in an output projection block (NaN or +inf in the
+# residual: every later logit NaN, token 0); NaN in one lm_head row (row 0:
+# the reference's pick keeps index 0; row 7: NaN never wins).
+NON_FINITE = [("blk.0.attn_norm.weight", 5, np.nan), ("blk.1.ffn_norm.weight", 100, np.nan),
+              ("output_norm.weight", 7, np.nan), ("blk.1.attn_q.bias", 3, np.nan),
+              ("blk.0.attn_output.weight", (5, 1), np.nan), ("blk.0.attn_output.weight", (9, 0), np.inf),
+              ("blk.1.ffn_down.weight", (3, 1), np.inf),
+              ("output.weight", (0, 0), np.nan), ("output.weight", (7, 1), np.nan)]
+
+
+@pytest.mark.parametrize("name,where,value", NON_FINITE)
+def test_non_finite_values_follow_reference(gpu, ref, tmp_path, name, where, value):
+    """A non-finite weight value: the device step gives the reference's
+    greedy tokens (src/sample.c:28-31), the same NaN and infinite logits,
+    and the finite logits within the usual bar."""
+    from dropin import greedy
+    cfg = TINY_UNTIED
+    path = str(tmp_path / "m.mlf2")
+    info = mlf2.write_qwen2(path, cfg, 2)
+    plant(path, info, name, where, value)
+    want, want_logits = greedy(ref, path, start=3, steps=3, vocab=cfg.vocab, max_seq=64)
+    dec = make_decoder(gpu, path, max_seq=64)
+    try:
+        dec.set_pos(0)
+        got, logits, tok = [], [], 3
+        for _ in range(3):
+            nxt, lg = dec.step(tok, logits=True)
+            tok = int(nxt[0])
+            got.append(tok)
+            logits.append(lg[0])
+        dec.set_pos(0)
+        replayed = dec.generate(3, 3)[:, 0].tolist()
+    finally:
+        dec.close()
+    got_logits = np.stack(logits)
+    print(f"[non-finite] {name} {where}: tokens {want}, NaN logits per step "
+          f"{[int(n) for n in np.isnan(want_logits).sum(1)]}", flush=True)
+    assert got == want and replayed == want
+    assert np.array_equal(np.isnan(got_logits), np.isnan(want_logits))
+    assert np.array_equal(np.isposinf(got_logits), np.isposinf(want_logits))
+    assert np.array_equal(np.isneginf(got_logits), np.isneginf(want_logits))
+    fin = np.isfinite(want_logits)
+    if fin.any():
+        within(f"finite logits, {name}", got_logits[fin], want_logits[fin], 3e-5)

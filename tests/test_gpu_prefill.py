@@ -167,20 +167,26 @@ def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt,
     assert got == want
 
 
-def test_prefill_after_decode_steps(gpu, ref, tmp_path):
+# head_dim 64 takes the chunk-record attention, head_dim 128 (SMALL_128) the
+# matrix-core prompt attention, here for a pass that starts past position 0
+# (measured K/V 2.4e-7, 1.1e-4; logits 3.1e-7, 4.6e-7)
+@pytest.mark.parametrize("cfg,kv_bar,lg_bar", [(TINY, 2e-6, 2e-6), (SMALL_128, 6e-4, 3e-6)])
+def test_prefill_after_decode_steps(gpu, ref, tmp_path, cfg, kv_bar, lg_bar):
     """Prompt, three decode steps, a second prompt at the new position, then
-    greedy decoding: as the reference fed the same tokens one by one."""
-    cfg = TINY
+    greedy decoding: as the reference fed the same tokens one by one; the
+    second prompt's K/V rows and last logits against the reference's."""
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, 7)
     rng = np.random.default_rng(7)
-    p1, p2 = rng.integers(0, cfg.vocab, 20), rng.integers(0, cfg.vocab, 15)
+    p1, p2 = rng.integers(0, cfg.vocab, 20), rng.integers(0, cfg.vocab, 45)
+    at = len(p1) + 3
     r = RefSeq(ref, path, 128, cfg)
     try:
         lg = r.feed(p1)
         fed = r.greedy(lg, 3)                 # tokens fed by the three steps
-        lg = r.feed(p2)
-        want = r.greedy(lg, 5)
+        want_lg = r.feed(p2)
+        want_k, want_v = r.kv(at + len(p2), at)
+        want = r.greedy(want_lg, 5)
     finally:
         r.close()
     dec = make(gpu, path, 1, 128)
@@ -191,18 +197,25 @@ def test_prefill_after_decode_steps(gpu, ref, tmp_path):
         for _ in range(3):
             steps.append(t)
             t = int(dec.step(t)[0])
-        nxt = dec.prefill(p2)
+        nxt, lg = dec.prefill(p2, logits=True)
+        got_k, got_v = device_kv(gpu, dec, 0, at + len(p2), at)
         got = [nxt] + dec.generate(nxt, 4)[:, 0].tolist()
     finally:
         dec.close()
     assert steps == fed
+    within(f"continued prompt K {cfg.head_dim}", got_k, want_k, kv_bar)
+    within(f"continued prompt V {cfg.head_dim}", got_v, want_v, kv_bar)
+    within(f"continued prompt logits {cfg.head_dim}", lg, want_lg, lg_bar)
     assert got == want
 
 
-def test_prefill_sequences_of_a_batched_decoder(gpu, ref, tmp_path):
+# measured K/V 2.9e-7, 1.2e-4 (worst sequence)
+@pytest.mark.parametrize("cfg,kv_bar", [(TINY, 2e-6), (SMALL_128, 6e-4)])
+def test_prefill_sequences_of_a_batched_decoder(gpu, ref, tmp_path, cfg, kv_bar):
     """Four sequences, each prefilled with its own prompt length, then decoded
-    together: every sequence as the reference's own context."""
-    cfg = TINY
+    together: every sequence as the reference's own context, and every
+    sequence's K/V rows (each in its own slice of the caches) as the
+    reference's."""
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, 8)
     rng = np.random.default_rng(8)
@@ -212,6 +225,7 @@ def test_prefill_sequences_of_a_batched_decoder(gpu, ref, tmp_path):
     try:
         dec.set_pos([0, 0, 0, 0])
         firsts = [dec.prefill(p, seq=s) for s, p in enumerate(prompts)]
+        kvs = [device_kv(gpu, dec, s, len(p)) for s, p in enumerate(prompts)]
         got = np.concatenate([np.array(firsts)[None], dec.generate(np.array(firsts), steps - 1)])
     finally:
         dec.close()
@@ -219,8 +233,11 @@ def test_prefill_sequences_of_a_batched_decoder(gpu, ref, tmp_path):
         r = RefSeq(ref, path, 256, cfg)
         try:
             want = r.greedy(r.feed(p), steps)
+            want_k, want_v = r.kv(len(p))
         finally:
             r.close()
+        within(f"sequence {s} prompt K {cfg.head_dim}", kvs[s][0], want_k, kv_bar)
+        within(f"sequence {s} prompt V {cfg.head_dim}", kvs[s][1], want_v, kv_bar)
         assert got[:, s].tolist() == want, f"sequence {s}"
 
 
@@ -245,6 +262,42 @@ def test_prefill_qwen2_3b_prompt(gpu, ref, tmp_path):
     finally:
         dec.close()
     within("prefill 3B logits", lg, want_lg, 1.7e-5)   # measured 3.5e-6
+    assert got == want
+
+
+@pytest.mark.timeout(900)
+def test_prefill_qwen2_7b_512_token_prompt(gpu, ref, tmp_path):
+    """The benchmarked prompt workload: the full Qwen2-7B shape (28 layers,
+    28/4 heads, ffn 18944, Q4_K attn/gate/up, Q6_K down and untied output), a
+    512-token prompt from position 0 in one pass (the q/k/v, gate/up and
+    residual GEMM epilogues at 3584 + 512 + 512 and 2 x 18944 rows, the prompt
+    attention at 7 query heads per KV head). Against the reference's feed,
+    one hakm_forward per token: the last logits, the K/V rows of layers 0
+    and 27, and three greedy tokens."""
+    cfg = mlf2.QWEN2_7B
+    path = str(tmp_path / "qwen2_7b.mlf2")
+    mlf2.write_qwen2(path, cfg, 50)
+    n = 512
+    prompt = np.random.default_rng(50).integers(0, cfg.vocab, n)
+    r = RefSeq(ref, path, n + 8, cfg)
+    try:
+        want_lg = r.feed(prompt)
+        want_k, want_v = r.kv(n)
+        want = r.greedy(want_lg, 3)
+    finally:
+        r.close()
+    dec = make(gpu, path, 1, n + 8)
+    try:
+        dec.set_pos(0)
+        first, lg = dec.prefill(prompt, logits=True)
+        got_k, got_v = device_kv(gpu, dec, 0, n)
+        got = [first] + dec.generate(first, 2)[:, 0].tolist()
+    finally:
+        dec.close()
+    for l in (0, cfg.n_layers - 1):
+        within(f"7B prompt K layer {l}", got_k[l], want_k[l], 5e-3)
+        within(f"7B prompt V layer {l}", got_v[l], want_v[l], 5e-3)
+    within("7B prompt logits", lg, want_lg, 1e-4)
     assert got == want
 
 

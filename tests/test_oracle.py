@@ -232,3 +232,18 @@ def test_matmul_batch_equals_rows(oracle):
 def test_argmax_lowest_index_wins(oracle):
     v = np.array([0.5, 2.0, -1.0, 2.0, 2.0], np.float32)
     assert oracle.argmax(v) == 1
+
+
+def test_greedy_pick_non_finite_rules(oracle):
+    """The reference's compiled greedy pick (src/sample.c:28-31) and the
+    oracle's agree on the non-finite rules the device argmax follows: a NaN
+    at index 0 is kept, a NaN elsewhere never wins, ties go to the lowest
+    index, +inf wins, all -inf keeps index 0."""
+    from oracle.hako_oracle import ref_greedy_pick
+    nan, inf = np.nan, np.inf
+    cases = [([nan, 1.0, 2.0], 0), ([0.0, nan, 2.0, 2.0], 2), ([1.0, nan, nan], 0), ([nan, nan], 0),
+             ([-1.0, inf, 3.0, inf], 1), ([-inf, -inf, nan], 0), ([0.5, 2.0, -1.0, 2.0], 1)]
+    for v, want in cases:
+        v = np.array(v, np.float32)
+        assert ref_greedy_pick(v) == want, v
+        assert oracle.argmax(v) == want, v

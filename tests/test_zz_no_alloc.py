@@ -28,11 +28,15 @@ def run(gpu, fn, qt, dw, x, m, n_out, n_in, bias=None):
 
 
 # (type, n_in, [(m, n_out) of the two calls]): a GEMM-sized call, then a
-# skinny one with fewer rows (split-K partials in the scratch)
+# skinny one with fewer rows. The skinny Q4_K matmul splits K only past 4096
+# inputs and the Q6_K one by its own rule: the 18944-wide Q4_K case and the
+# Q6_K case keep split-K partials in the scratch, the other Q4_K cases
+# reduce in LDS.
 CASES = [
     (synth.TYPE_Q4_K, 3584, [(40, 4096), (9, 1024)]),
     (synth.TYPE_Q6_K, 4608, [(33, 1536), (6, 512)]),
     (synth.TYPE_Q4_K, 2048, [(16, 2560), (2, 256)]),
+    (synth.TYPE_Q4_K, 18944, [(24, 512), (8, 256)]),
 ]
 
 
