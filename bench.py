@@ -87,9 +87,10 @@ def bench_copy(g, nbytes: int, steps: int, warmup: int, eager: bool) -> dict:
 
 
 def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
-    """K launches between two events: replayed from a captured HIP graph, or
-    (eager) issued one by one from Python, as profilers' per-dispatch counter
-    collection needs. Also the median single-launch latency."""
+    """K launches: replayed from a captured HIP graph between two device
+    wall-clock marks inside the graph, or (eager) issued one by one from
+    Python between two events, as profilers' per-dispatch counter collection
+    needs. Also the median single-launch latency."""
     e0, e1 = g.event(), g.event()
     if eager:
         for k in range(warmup):
@@ -106,12 +107,28 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
             for k in range(k0, k0 + n):
                 launch(k)
             return g.capture_end()
-        # the timed launches start on the weight copy after the warm-up's last,
-        # so none of them finds its weights left in the last-level cache; the
-        # warm-up graph holds at least 64 launches, so the host queues its
+        # the warm-up graph holds at least 64 launches, so the host queues its
         # replays faster than the GPU runs them
         nwarm = max(warmup, 64)
-        warm, timed = capture(0, nwarm), capture(nwarm, steps)
+        warm = capture(0, nwarm)
+        # The timed graph: nwarm lead-in launches, wall-clock mark t0, the K
+        # timed launches, marks t1 and t2. The marks are one-wave kernels that
+        # are nodes of the graph, so the timed region holds neither the
+        # start-up of a graph launch (~14 us on an idle queue) nor anything of
+        # the host; t1 - t0 spans the t0 mark's own slot and the K launches,
+        # t2 - t1 one mark's slot, which is subtracted. The timed launches
+        # start on the weight copy after the lead-in's last, so none of them
+        # finds its weights left in the last-level cache.
+        stamps = g.alloc(64)
+        g.capture_begin()
+        for k in range(nwarm, 2 * nwarm):
+            launch(k)
+        g.timestamp(stamps.offset(0))
+        for k in range(2 * nwarm, 2 * nwarm + steps):
+            launch(k)
+        g.timestamp(stamps.offset(8))
+        g.timestamp(stamps.offset(16))
+        timed = g.capture_end()
         # the warm-up graph replayed for at least 30 ms: a GPU idle during the
         # host-side set-up runs its first milliseconds at lower clocks
         g.record(e0)
@@ -120,14 +137,14 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
         reps = int(math.ceil(30.0 / max(g.elapsed_ms(e0, e1), 1e-3)))
         for _ in range(min(reps, 1000)):
             g.graph_launch(warm)
-        # no synchronization here: the timed graph is queued while the warm-up
-        # still runs, and e0 completes when the warm-up's last launch does,
-        # so the timed region holds the K launches and not the start-up of a
-        # graph on an idle GPU (~14 us)
         g.record(e0)
         g.graph_launch(timed)
         g.record(e1)
-        ms = g.elapsed_ms(e0, e1)
+        graph_ms = g.elapsed_ms(e0, e1)
+        t = g.download(stamps, np.uint64, (3,)).astype(np.int64)
+        stamps.free()
+        mark_ticks = int(t[2] - t[1])
+        ms = (int(t[1] - t[0]) - mark_ticks) / g.timestamp_hz() * 1e3
         g.graph_destroy(warm)
         g.graph_destroy(timed)
     single = []
@@ -136,7 +153,11 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
         launch(k)
         g.record(e1)
         single.append(g.elapsed_ms(e0, e1))
-    return {"ms_total": ms, "us_per_launch": ms * 1e3 / steps, "single_launch_us": float(np.median(single)) * 1e3}
+    res = {"ms_total": ms, "us_per_launch": ms * 1e3 / steps, "single_launch_us": float(np.median(single)) * 1e3}
+    if not eager:
+        res["graph_ms_with_lead_in"] = graph_ms
+        res["mark_slot_us"] = mark_ticks / g.timestamp_hz() * 1e6
+    return res
 
 
 def host_info() -> dict:
@@ -622,7 +643,8 @@ def main():
         "config": {"workload": "Q4_K x q8 matmul (q8_32 quantize + GEMV, one launch), Qwen2.5-3B ffn_up "
                                "11008x2048, batch 1", "n_out": 11008, "n_in": 2048,
                    "weight_copies": head["weight_copies"], "algo_bytes_per_step": head["algo_bytes"],
-                   "timing": "HIP graph of K launches between two HIP events on the library stream"},
+                   "timing": "K launches in a HIP graph after 64 lead-in launches, between two device wall-clock "
+                             "marks in the graph (one mark's own slot subtracted)"},
         "hbm_frac": round(value / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": read_traffic(HEADLINE)[0]},

@@ -41,6 +41,10 @@ namespace {
 
 constexpr int kQ6Depth = 4;
 constexpr int kQ6MaxWaves = 8;
+// waves of a flat wide workgroup: 8 parts of 64 chunks, 12 of 32 (rows up to
+// 32768 / 24576 weights); the launch bound keeps 170+ registers per lane
+template <int SEGW>
+constexpr int q6_max_parts() { return SEGW == 64 ? 8 : 12; }
 
 struct Q6Buf {
 	uint4 qa, qb;    // ql 64n+16lh .. +16 (k = 0, 2) and 64n+32+16lh .. +16 (k = 1, 3)
@@ -243,40 +247,46 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 // activation (and bias / residual) loads, as the Q4_K flat GEMV does; latency
 // is hidden by the many workgroups resident on each CU instead of a software
 // pipeline. Rows of C <= 64 chunks: a workgroup of 4 waves, a wave owns ITEMS
-// consecutive row tiles of rt = 64/seg rows. Wider rows: a workgroup of P =
-// ceil(C/64) waves, wave p the chunks [64p, 64p + 64) of ITEMS consecutive
-// rows; the P partial sums of a row meet in LDS.
-template <int ITEMS>
-__global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(const uint8_t *__restrict__ w,
-                                                                            const float *__restrict__ x,
-                                                                            const float *__restrict__ bias,
-                                                                            const float *res, float *out,
-                                                                            int n_out, int n_in) {
+// consecutive row tiles of rt = 64/seg rows. Wider rows: parts of SEGW
+// chunks (64, or 32: two rows per wave instruction), a workgroup of P =
+// ceil(C/SEGW) waves, wave p the chunks [SEGW p, SEGW p + SEGW) of ITEMS row
+// tiles of rt = 64/SEGW rows; the P partial sums of a row meet in LDS. With
+// 32-chunk parts a workgroup covers twice the rows for the same work per
+// wave, so each row's activation part is read by half as many workgroups.
+template <int ITEMS, int SEGW>
+__global__ __launch_bounds__(q6_max_parts<SEGW>() * kWave) void q6k_gemv_flat_kernel(const uint8_t *__restrict__ w,
+                                                                           const float *__restrict__ x,
+                                                                           const float *__restrict__ bias,
+                                                                           const float *res, float *out,
+                                                                           int n_out, int n_in) {
 	constexpr int NG = (ITEMS + 3) / 4;   // groups of four items reduced together
-	__shared__ float red_s[kQ6MaxWaves][4 * NG];
+	constexpr int WRT = 64 / SEGW;        // rows per item of a wide workgroup
+	__shared__ float red_s[q6_max_parts<SEGW>()][4 * NG * WRT];
 	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int NB = n_in >> 8, C = NB * 4;
 	const bool wide = C > 64;
-	const int seg = wide ? 64 : next_pow2(C), rt = 64 / seg;
+	const int seg = wide ? SEGW : next_pow2(C), rt = 64 / seg;
 	const int sub = lane & (seg - 1), rsub = lane / seg;
 	const int part = wide ? wave : 0;
-	const int c = 64 * part + sub;
+	const int c = seg * part + sub;
 	const bool lane_on = c < C;
 	// first row of this wave's items; a wide workgroup's waves share rows
-	const int wrow0 = wide ? blockIdx.x * ITEMS : (blockIdx.x * 4 + wave) * ITEMS * rt;
-	auto item_row = [&](int it) -> int { return wide ? wrow0 + it : wrow0 + rt * it + rsub; };
+	const int wrow0 = wide ? blockIdx.x * ITEMS * rt : (blockIdx.x * 4 + wave) * ITEMS * rt;
+	auto item_row = [&](int it) -> int { return wrow0 + rt * it + rsub; };
 	const size_t rb = (size_t)NB * kQ6Bytes;
 
 	const int cc = min(c, C - 1);
 	const int i = cc >> 2, s = cc & 3, hn = s >> 1, lh = s & 1;
 
-	// 1. activation, then bias / residual of the row this lane writes
+	// 1. activation, then bias / residual of the row this lane writes: in a
+	//    narrow workgroup lane sub (< 4) of segment rsub writes item 4g + sub;
+	//    in a wide one lane L of wave 0 writes row wrow0 + L
 	Q6Col col;
 	q6_col_load(x, cc, col);
 	float rv[NG], bv[NG];
 #pragma unroll
 	for (int g = 0; g < NG; g++) {
-		const int r = min(item_row(4 * g + (sub & 3)), n_out - 1);
+		const int r = min(wide ? wrow0 + 64 * g + lane : item_row(4 * g + (sub & 3)), n_out - 1);
 		rv[g] = res ? res[r] : 0.0f;
 		bv[g] = bias ? bias[r] : 0.0f;
 	}
@@ -312,7 +322,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(cons
 		const float d = q6_dot(buf[j], col, lh);
 		rsum[j] = (lane_on && item_row(j) < n_out) ? d : 0.0f;
 	}
-	// 4. lane sub = j (< 4) of each segment holds item 4g + j
+	// 4. lane sub = j (< 4) of each segment holds item 4g + j of its row rsub
 	if (!wide) {
 #pragma unroll
 		for (int g = 0; g < NG; g++) {
@@ -325,17 +335,169 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_flat_kernel(cons
 	}
 #pragma unroll
 	for (int g = 0; g < NG; g++) {
-		const float tot = seg_sum4(rsum + 4 * g, 64, lane);
-		if (lane < 4) red_s[part][4 * g + lane] = tot;
+		const float tot = seg_sum4(rsum + 4 * g, SEGW, lane);
+		if (sub < 4) red_s[part][WRT * (4 * g + sub) + rsub] = tot;
 	}
 	__syncthreads();
-	if (wave == 0 && lane < 4 * NG && lane < ITEMS) {
-		const int row = wrow0 + lane;
-		if (row < n_out) {
-			float v = 0.0f;
-			for (int p = 0; p < (int)(blockDim.x >> 6); p++) v += red_s[p][lane];
-			out[row] = finish(v, lane >> 2);
+	if (wave == 0) {
+#pragma unroll
+		for (int g = 0; g < NG; g++) {
+			const int lr = 64 * g + lane;   // local row: item lr / WRT, segment lr % WRT
+			const int row = wrow0 + lr;
+			if (lr < ITEMS * WRT && row < n_out) {
+				float v = 0.0f;
+				for (int p = 0; p < (int)(blockDim.x >> 6); p++) v += red_s[p][lr];
+				out[row] = finish(v, g);
+			}
 		}
+	}
+}
+
+// Persistent rows grid: one workgroup per CU of W waves (a multiple of 4, so
+// the four SIMDs carry equal work). A row tile is rt = 64/seg rows (seg =
+// min(64, chunks) lanes per row), cut into P = ceil(C/seg) passes of seg
+// chunks; each wave walks whole row tiles of the workgroup's row range pass
+// by pass, so a row's sum never leaves its wave (lane sums over the passes,
+// then the segment's lanes). D pass items are in flight per wave; an item's
+// weight offsets are per-lane constants plus one wave-uniform row/pass
+// offset. Rows of several passes take the activation from LDS, staged once
+// per workgroup as [chunk][68] floats — the chunk's 64 values in the lane's
+// order, then its four -32*sum(x) terms (the 68-float stride puts 8
+// consecutive lanes' 16-byte reads on all 32 banks); one-pass rows keep it
+// in registers.
+constexpr uint32_t kRowsNone = 0x7FF00000u;   // a lane part or row part past every stream
+
+template <int W, int D, bool XREG>
+__global__ __launch_bounds__(W * kWave) void q6k_rows_kernel(const uint8_t *__restrict__ w,
+                                                          const float *__restrict__ x,
+                                                          const float *__restrict__ bias, const float *res,
+                                                          float *out, int n_out, int n_in) {
+	extern __shared__ __align__(16) float lds_f[];
+	constexpr int T = W * kWave;
+	constexpr int XS = 8192 / T;   // float4 loads per thread that stage up to 32768 inputs
+	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int NB = n_in >> 8, C = NB * 4;
+	const int seg = C >= 64 ? 64 : next_pow2(C), rt = 64 / seg, P = (C + seg - 1) / seg;
+	const int sub = lane & (seg - 1), rsub = lane / seg;
+	const int r0 = (int)((int64_t)blockIdx.x * n_out / gridDim.x);
+	const int r1 = (int)((int64_t)(blockIdx.x + 1) * n_out / gridDim.x);
+	const int nrows = r1 - r0, ntiles = (nrows + rt - 1) / rt;
+	const uint32_t rb = (uint32_t)NB * kQ6Bytes;
+	float *xl = lds_f;                               // [C][68] floats (rows of several passes)
+	float *red_s = lds_f + (XREG ? 0 : C * 68);      // [nrows] row sums
+	const int s = sub & 3, hn = s >> 1, lh = s & 1;  // the lane's quarter of a block, every pass
+	const bool last_on = seg * (P - 1) + sub < C;    // the lane has a chunk in the last pass
+	// lane parts of the offsets (row rsub of the tile, block sub/4 of the pass)
+	const uint32_t lb = (uint32_t)rsub * rb + (uint32_t)(sub >> 2) * kQ6Bytes;
+	const uint32_t lbl = last_on ? lb : kRowsNone;
+	const uint32_t oa = 64 * hn + 16 * lh, oh = 128 + 32 * hn + 16 * lh, os = 192 + 8 * hn;
+	const __amdgpu_buffer_rsrc_t wr = stream_rsrc(w, rb * (uint32_t)n_out);
+	// this wave's tiles: wave, wave + W, ...; its items: tile by tile, pass by pass
+	const int nt_w = ntiles > wave ? (ntiles - wave + W - 1) / W : 0;
+	const int NQ = nt_w * P;
+	auto issue = [&](Q6Buf &b, int ti, int p) {
+		const int tl = wave + W * ti;
+		const uint32_t so = tl < ntiles ? (uint32_t)(r0 + rt * tl) * rb + (uint32_t)(p * (seg >> 2)) * kQ6Bytes
+		                                : 0x80000000u;
+		const uint32_t v = (p == P - 1 ? lbl : lb) + so;
+		b.qa = ld_b128(wr, v + oa);
+		b.qb = ld_b128(wr, v + oa + 32);
+		b.qh = ld_b128(wr, v + oh);
+		b.s = ld_b64(wr, v + os);
+		b.d = ld_b16(wr, v + 208);
+	};
+
+	// 1. the first D items' weights, the activation, this thread's row's residual and bias
+	Q6Buf buf[D];
+	int ti_i = 0, p_i = 0;
+	auto advance = [&](int &ti, int &p) {
+		if (++p == P) {
+			p = 0;
+			ti++;
+		}
+	};
+#pragma unroll
+	for (int j = 0; j < D; j++) {
+		issue(buf[j], ti_i, p_i);
+		advance(ti_i, p_i);
+		__builtin_amdgcn_sched_barrier(0);
+	}
+	Q6Col col;
+	if (XREG) {
+		q6_col_load(x, min(sub, C - 1), col);
+	} else {
+		// x as float4 f = t, t + T, ...: element 4f is j0..j0+3 of chunk c's run k
+		const __amdgpu_buffer_rsrc_t xr = stream_rsrc(x, (uint32_t)n_in * 4u);
+		float4 xv4[XS];
+#pragma unroll
+		for (int u = 0; u < XS; u++)
+			xv4[u] = __builtin_bit_cast(float4, ld_b128(xr, (uint32_t)(threadIdx.x + u * T) * 16u));
+#pragma unroll
+		for (int u = 0; u < XS; u++) {
+			const int f = threadIdx.x + u * T;
+			const int e = 4 * f, i = e >> 8, n = (e >> 7) & 1, k = (e >> 5) & 3, l2 = (e >> 4) & 1, j0 = e & 15;
+			const int c = 4 * i + 2 * n + l2;
+			// sum of the run's 16 values: the four lanes of a quad hold it
+			float t = ((xv4[u].x + xv4[u].y) + xv4[u].z) + xv4[u].w;
+			t += dpp_f<kDppQuadSwap1>(t);
+			t += dpp_f<kDppQuadSwap2>(t);
+			if (f < (n_in >> 2)) {
+				*(float4 *)(xl + c * 68 + 16 * k + j0) = xv4[u];
+				if (j0 == 0) xl[c * 68 + 64 + k] = -32.0f * t;
+			}
+		}
+	}
+	float res0 = 0.0f, bias0 = 0.0f;
+	if ((int)threadIdx.x < nrows) {
+		if (res) res0 = res[r0 + threadIdx.x];
+		if (bias) bias0 = bias[r0 + threadIdx.x];
+	}
+	if (!XREG) __syncthreads();
+	else q6_col_sums(col);
+
+	// 2. items in groups of D (the ring's slots are static): compute the
+	//    item in slot j, then issue the item D later into it
+	float racc = 0.0f;
+	int ti_c = 0, p_c = 0;
+	for (int q0 = 0; q0 < NQ; q0 += D) {
+#pragma unroll
+		for (int j = 0; j < D; j++) {
+			if (q0 + j < NQ) {
+				if (!XREG) {
+					const float4 *xc = (const float4 *)(xl + min(seg * p_c + sub, C - 1) * 68);
+#pragma unroll
+					for (int k = 0; k < 4; k++)
+#pragma unroll
+						for (int m = 0; m < 4; m++) {
+							const float4 u = xc[4 * k + m];
+							col.xv[k][4 * m] = u.x; col.xv[k][4 * m + 1] = u.y;
+							col.xv[k][4 * m + 2] = u.z; col.xv[k][4 * m + 3] = u.w;
+						}
+					const float4 ns = xc[16];
+					col.nsx[0] = ns.x; col.nsx[1] = ns.y; col.nsx[2] = ns.z; col.nsx[3] = ns.w;
+				}
+				const float d = q6_dot(buf[j], col, lh);
+				racc += (p_c < P - 1 || last_on) ? d : 0.0f;
+				if (p_c == P - 1) {
+					const float tot = seg_sum(racc, seg);
+					const int lr = rt * (wave + W * ti_c) + rsub;
+					if (sub == 0 && lr < nrows) red_s[lr] = tot;
+					racc = 0.0f;
+				}
+			}
+			issue(buf[j], ti_i, p_i);
+			advance(ti_i, p_i);
+			advance(ti_c, p_c);
+			__builtin_amdgcn_sched_barrier(0);
+		}
+	}
+	// 3. out = res + (sum + bias), each row by one thread
+	__syncthreads();
+	for (int r = threadIdx.x; r < nrows; r += T) {
+		float v = red_s[r];
+		const bool first = r == (int)threadIdx.x;
+		if (bias) v += first ? bias0 : bias[r0 + r];
+		out[r0 + r] = res ? (first ? res0 : res[r0 + r]) + v : v;
 	}
 }
 
@@ -343,6 +505,10 @@ int g_q6_wgs_per_cu = 1;
 int g_q6_waves = 4;
 // -1: by shape (below); 0: persistent grid; 1, 2, 4, 8: flat grid with that many items per wave
 int g_q6_flat_items = -1;
+// chunks per part of the flat grid's wide rows: 64, or 32 (0: by shape)
+int g_q6_flat_seg = 0;
+// rows grid: 0 by shape, -1 never, else 10 * waves + depth (44, 82, 84, 162)
+int g_q6_rows = 0;
 
 // Measured on MI355X (us per launch, persistent / flat with 1, 2, 4, 8
 // items): 2048x11008 (3 parts) 8.08 / 10.8 / 8.58 / 7.45 / 8.24; 1000x4608
@@ -364,6 +530,8 @@ int q6_flat_items_for(int n_out, const Q6Geom &G) {
 
 void q6k_set_wgs_per_cu(int v) { g_q6_wgs_per_cu = v < 1 ? 1 : (v > 8 ? 8 : v); }
 void q6k_set_waves(int v) { g_q6_waves = v >= 8 ? 8 : 4; }
+void q6k_set_rows(int v) { g_q6_rows = v; }
+void q6k_set_flat_seg(int v) { g_q6_flat_seg = v == 32 || v == 64 ? v : 0; }
 void q6k_set_flat_items(int v) { g_q6_flat_items = v < 0 ? -1 : (v == 0 ? 0 : (v <= 1 ? 1 : (v <= 2 ? 2 : (v <= 4 ? 4 : 8)))); }
 
 }  // namespace hako
@@ -385,18 +553,61 @@ int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV weight of %d x %d exceeds 2 GiB", n_out, n_in);
 	if (G.waves > kQ6MaxWaves || G.tpr > kQ6MaxWaves)
 		return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV n_in %d exceeds %d", n_in, kQ6MaxWaves * 64 * 64);
+	// rows of several passes that the flat grid does not take go to the rows
+	// grid (8 waves, 2 items in flight: 7B down 3584x18944 17.9 -> 16.2 us;
+	// 4 waves / 4 items 19.0, 8 / 4 17.7, 16 / 2 16.8)
+	const int rows_cfg = g_q6_rows > 0 ? g_q6_rows
+	                     : (g_q6_rows == 0 && G.C > 64 && q6_flat_items_for(n_out, G) == 0) ? 82 : 0;
+	if (rows_cfg) {
+		const int NB = n_in / kQK, C = 4 * NB;
+		const int seg = C >= 64 ? 64 : next_pow2(C), rt = 64 / seg;
+		const bool xreg = C <= 64;
+		if ((size_t)n_out * NB * kQ6Bytes > kRowsNone)
+			return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV rows grid: weight of %d x %d too large", n_out, n_in);
+		if (n_in > 32768) return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV rows grid: n_in %d > 32768", n_in);
+		int wgs = (n_out + rt - 1) / rt;
+		const int max_wgs = g_q6_wgs_per_cu * cu_count();
+		if (wgs > max_wgs) wgs = max_wgs;
+		const int rows_per_wg = (n_out + wgs - 1) / wgs + 1;
+		const size_t lds = (xreg ? 0 : (size_t)C * 68 * 4) + (size_t)rows_per_wg * 4;
+		if (lds > 160 * 1024) return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV rows grid: %zu bytes of LDS", lds);
+#define HK_Q6R(WV, DP) \
+	hipLaunchKernelGGL((xreg ? q6k_rows_kernel<WV, DP, true> : q6k_rows_kernel<WV, DP, false>), dim3(wgs), \
+	                   dim3(WV * kWave), lds, stream(), (const uint8_t *)w, x, bias, res, out, n_out, n_in)
+		switch (rows_cfg) {
+		case 44: HK_Q6R(4, 4); break;
+		case 84: HK_Q6R(8, 4); break;
+		case 162: HK_Q6R(16, 2); break;
+		default: HK_Q6R(8, 2); break;
+		}
+#undef HK_Q6R
+		HK_LAUNCHED("q6k_rows");
+		return ok();
+	}
 	if (const int items = q6_flat_items_for(n_out, G)) {
 		const bool wide = G.C > 64;
-		const int rows_wg = wide ? items : 4 * items * G.rt;
+		const int segw = g_q6_flat_seg ? g_q6_flat_seg : 64;
+		const int parts = (G.C + segw - 1) / segw;
+		const int max_parts = segw == 32 ? q6_max_parts<32>() : q6_max_parts<64>();
+		if (wide && parts > max_parts)
+			return set_error(HAKO_GPU_EINVAL, "Q6_K GEMV flat grid: n_in %d needs more than %d parts", n_in, max_parts);
+		const int rows_wg = wide ? items * (64 / segw) : 4 * items * G.rt;
 		const int wgs = (n_out + rows_wg - 1) / rows_wg;
-		const dim3 block(wide ? G.tpr * kWave : 4 * kWave);
-#define HK_Q6F(IT) \
-	hipLaunchKernelGGL(q6k_gemv_flat_kernel<IT>, dim3(wgs), block, 0, stream(), (const uint8_t *)w, x, bias, res, out, \
-	                   n_out, n_in)
-		if (items <= 1) HK_Q6F(1);
-		else if (items <= 2) HK_Q6F(2);
-		else if (items <= 4) HK_Q6F(4);
-		else HK_Q6F(8);
+		const dim3 block(wide ? parts * kWave : 4 * kWave);
+#define HK_Q6F(IT, SW) \
+	hipLaunchKernelGGL((q6k_gemv_flat_kernel<IT, SW>), dim3(wgs), block, 0, stream(), (const uint8_t *)w, x, bias, res, \
+	                   out, n_out, n_in)
+		if (segw == 32) {
+			if (items <= 1) HK_Q6F(1, 32);
+			else if (items <= 2) HK_Q6F(2, 32);
+			else if (items <= 4) HK_Q6F(4, 32);
+			else HK_Q6F(8, 32);
+		} else {
+			if (items <= 1) HK_Q6F(1, 64);
+			else if (items <= 2) HK_Q6F(2, 64);
+			else if (items <= 4) HK_Q6F(4, 64);
+			else HK_Q6F(8, 64);
+		}
 #undef HK_Q6F
 		HK_LAUNCHED("q6k_gemv_flat");
 		return ok();

@@ -176,10 +176,15 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
 // q8_32 of one block (reference quant.c:127-144 as compiled with
 // -ffast-math): inputs flushed to zero below FLT_MIN, xs = amax*RN(1/127),
 // inv = RN(127/amax) when xs > 0, codes round-half-even clamped to +-127.
+// The reference's maximum starts at 0 and takes only larger values, so NaN
+// inputs never enter it: a block of NaNs has amax 0 (here a NaN maximum,
+// which only an all-NaN block yields under fmaxf, is taken as 0).
 // A product that is not finite (only from inf/NaN inputs) converts to 0, as
 // the reference's 64-bit conversion yields the "indefinite" value whose low
 // 32 bits are 0. Clamping in float keeps the int conversion defined.
-__device__ __forceinline__ float q8_xs(float amax) { return ftz(amax * 0x1.020408p-7f); }   // RN(1/127) = 0x3C010204
+__device__ __forceinline__ float q8_xs(float amax) {   // RN(1/127) = 0x3C010204
+	return ftz(__builtin_fmaxf(amax, 0.0f) * 0x1.020408p-7f);
+}
 __device__ __forceinline__ float q8_inv(float amax, float xs) { return xs > 0.0f ? 127.0f / amax : 0.0f; }
 __device__ __forceinline__ uint32_t q8_code(float a, float inv) {
 	float r = __builtin_rintf(a * inv);

@@ -27,6 +27,8 @@ void q6k_set_wgs_per_cu(int v);
 void q4k_set_waves(int v);
 void q6k_set_waves(int v);
 void q6k_set_flat_items(int v);
+void q6k_set_flat_seg(int v);
+void q6k_set_rows(int v);
 void q4k_set_flat_items(int v);
 // Target workgroups of the skinny (<= 16 token) launches (0: default).
 void q4k_skinny_set_target_wgs(int wgs);

@@ -24,6 +24,14 @@ __global__ __launch_bounds__(256) void copy16_kernel(const uint4 *__restrict__ s
 		dst[i] = src[i];
 }
 
+// The device's constant-rate wall clock (s_memrealtime) at the moment the
+// kernel runs, stored through a vector store by one lane: a timing mark that
+// can sit inside a captured graph, where events cannot be timed.
+__global__ __launch_bounds__(64) void stamp_kernel(unsigned long long *dst) {
+	const unsigned long long t = wall_clock64();
+	if (threadIdx.x == 0) dst[threadIdx.x] = t;
+}
+
 struct Mirror {
 	const uint8_t *host;
 	size_t bytes;
@@ -159,6 +167,8 @@ int hako_gpu_tune(int knob, int value) {
 	case HAKO_TUNE_Q4K_WAVES: q4k_set_waves(value); return ok();
 	case HAKO_TUNE_Q6K_WAVES: q6k_set_waves(value); return ok();
 	case HAKO_TUNE_Q6K_FLAT_ITEMS: q6k_set_flat_items(value); return ok();
+	case HAKO_TUNE_Q6K_FLAT_SEG: q6k_set_flat_seg(value); return ok();
+	case HAKO_TUNE_Q6K_ROWS: q6k_set_rows(value); return ok();
 	case HAKO_TUNE_Q4K_FLAT_ITEMS: q4k_set_flat_items(value); return ok();
 	case HAKO_TUNE_SKINNY_Q4K_WGS: q4k_skinny_set_target_wgs(value); return ok();
 	case HAKO_TUNE_SKINNY_Q6K_WGS: q6k_skinny_set_target_wgs(value); return ok();
@@ -259,6 +269,23 @@ int hako_gpu_event_elapsed_ms(void *start, void *stop, float *ms) {
 int hako_gpu_event_destroy(void *ev) {
 	if (int rc = require_device()) return rc;
 	HK_HIP(hipEventDestroy((hipEvent_t)ev));
+	return ok();
+}
+
+int hako_gpu_timestamp(void *dst) {
+	if (int rc = require_device()) return rc;
+	if (!dst || ((uintptr_t)dst & 7)) return set_error(HAKO_GPU_EINVAL, "timestamp needs an 8-byte aligned address");
+	hipLaunchKernelGGL(stamp_kernel, dim3(1), dim3(64), 0, st().stream, (unsigned long long *)dst);
+	HK_LAUNCHED("stamp");
+	return ok();
+}
+
+int hako_gpu_timestamp_hz(double *hz) {
+	if (int rc = require_device()) return rc;
+	int khz = 0;
+	HK_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, st().device));
+	if (khz <= 0) return set_error(HAKO_GPU_EINVAL, "device reports no wall-clock rate");
+	*hz = 1e3 * khz;
 	return ok();
 }
 

@@ -38,6 +38,8 @@ SIGNATURES = {
     "hako_gpu_event_record": (_i, [_vp]),
     "hako_gpu_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(C.c_float)]),
     "hako_gpu_event_destroy": (_i, [_vp]),
+    "hako_gpu_timestamp": (_i, [_vp]),
+    "hako_gpu_timestamp_hz": (_i, [C.POINTER(C.c_double)]),
     "hako_gpu_capture_begin": (_i, []),
     "hako_gpu_capture_end": (_i, [C.POINTER(_vp)]),
     "hako_gpu_graph_launch": (_i, [_vp]),
@@ -179,6 +181,15 @@ class Gpu:
         ms = C.c_float()
         self.check(self.lib.hako_gpu_event_elapsed_ms(a, b, C.byref(ms)), "event_elapsed")
         return ms.value
+
+    def timestamp(self, dst):
+        """The device wall clock written to dst (8 bytes) when this mark runs."""
+        self.check(self.lib.hako_gpu_timestamp(_ptr(dst)), "timestamp")
+
+    def timestamp_hz(self) -> float:
+        hz = C.c_double()
+        self.check(self.lib.hako_gpu_timestamp_hz(C.byref(hz)), "timestamp_hz")
+        return hz.value
 
     # graphs
     def capture_begin(self):

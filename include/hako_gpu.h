@@ -68,6 +68,8 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_SKINNY_Q6K_WGS 7
 #define HAKO_TUNE_Q6K_FLAT_ITEMS 8   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
 #define HAKO_TUNE_DEC_GU_ITEMS   9   /* one-sequence decoder gate/up launch: row items per wave, 4 or 8, or 0 = by shape (default); read when a step is enqueued or captured */
+#define HAKO_TUNE_Q6K_FLAT_SEG  10   /* Q6_K flat grid, rows wider than 64 chunks: chunks per part, 64 or 32, or 0 = by shape (default) */
+#define HAKO_TUNE_Q6K_ROWS      11   /* Q6_K rows grid: 10 x waves + items in flight (44, 82, 84, 162), 0 = by shape (default), -1 = never */
 int hako_gpu_tune(int knob, int value);
 
 typedef struct {
@@ -97,6 +99,13 @@ int hako_gpu_event_create(void **ev);
 int hako_gpu_event_record(void *ev);
 int hako_gpu_event_elapsed_ms(void *start, void *stop, float *ms);    /* waits for stop */
 int hako_gpu_event_destroy(void *ev);
+
+/* Timing marks that also work inside a captured graph (no reference
+ * counterpart; measurement only): a one-wave kernel on the library stream
+ * writes the device's constant-rate wall clock, in ticks of
+ * hako_gpu_timestamp_hz, to the 8-byte device address dst when it runs. */
+int hako_gpu_timestamp(void *dst);
+int hako_gpu_timestamp_hz(double *hz);
 
 /* HIP graphs by stream capture: library calls made on this thread between
  * capture_begin and capture_end are recorded, not run; graph_launch replays

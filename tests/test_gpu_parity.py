@@ -69,6 +69,18 @@ def test_q8_random_vs_oracle(gpu, oracle, rows, n):
         assert np.array_equal(xs[r].view(np.uint32), os_.view(np.uint32)), r
 
 
+def test_q8_non_finite_vs_oracle(gpu, oracle):
+    """NaN and infinite inputs (a block of NaNs has scale 0, as the
+    reference's maximum starts at 0 and takes only larger values)."""
+    from test_oracle import q8_non_finite_rows
+    x = q8_non_finite_rows()
+    xq, xs = gpu_q8(gpu, x)
+    for r in range(x.shape[0]):
+        oq, os_ = oracle.quantize_q8_32(x[r])
+        assert np.array_equal(xq[r], oq), r
+        assert np.array_equal(xs[r].view(np.uint32), os_.view(np.uint32)), r
+
+
 # ── dequantizers ──
 
 @pytest.mark.parametrize("qtype,name", [(Q4, "q4k_dequant.npz"), (Q6, "q6k_dequant.npz")])
@@ -259,19 +271,23 @@ def test_q6k_nan_propagates(gpu, n_out, n_in):
 
 
 HAKO_TUNE_Q6K_WGS_PER_CU, HAKO_TUNE_Q6K_WAVES, HAKO_TUNE_Q6K_FLAT_ITEMS = 2, 4, 8
+HAKO_TUNE_Q6K_FLAT_SEG, HAKO_TUNE_Q6K_ROWS = 10, 11
 
 
 @pytest.mark.parametrize("n_out,n_in", [(2048, 11008), (300, 2048), (77, 18944), (100, 1792), (64, 512)])
 def test_q6k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
     """Persistent grid (4 or 8 waves, 1 or 2 workgroups per CU) and flat grid
     (1..8 row items per wave), with and without a bias: the lane work and the
-    order of every addition are the same, so outputs are identical."""
+    order of every addition are the same, so outputs are identical. (The rows
+    grid, which wide rows take by default, adds in its own order: off here,
+    its own test below.)"""
     rng = np.random.default_rng(n_out + 5 * n_in)
     w = synth.q6k_weight(rng, n_out, n_in)
     x = synth.activation(rng, n_in)
     bias = synth.activation(rng, n_out)
     dw, dx, db, do = gpu.upload(w), gpu.upload(x), gpu.upload(bias), gpu.alloc(n_out * 4)
     seen = {}
+    gpu.tune(HAKO_TUNE_Q6K_ROWS, -1)
     try:
         for items, waves, wgs in ((-1, 4, 1), (0, 4, 1), (0, 8, 1), (0, 4, 2), (1, 4, 1), (2, 4, 1), (4, 4, 1),
                                   (8, 4, 1)):
@@ -290,10 +306,72 @@ def test_q6k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
         gpu.tune(HAKO_TUNE_Q6K_FLAT_ITEMS, -1)
         gpu.tune(HAKO_TUNE_Q6K_WAVES, 4)
         gpu.tune(HAKO_TUNE_Q6K_WGS_PER_CU, 1)
+        gpu.tune(HAKO_TUNE_Q6K_ROWS, 0)
         for b in (dw, dx, db, do):
             b.free()
     want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True, threads=16)
     assert maxabs_rel(seen[False], want) < TOL
+
+
+@pytest.mark.parametrize("n_out,n_in", [(77, 18944), (3584, 18944), (5, 32000), (300, 2048), (9, 4608)])
+def test_q6k_rows_grid(gpu, oracle, n_out, n_in):
+    """The rows grid (each wave sums whole rows: its lanes over the passes,
+    then the lanes; activation staged in LDS for rows of several passes) at
+    4, 8 and 16 waves and 2 or 4 items in flight, with and without a bias:
+    identical outputs (the order of additions does not depend on the grid),
+    within 1e-5 of the oracle; a NaN in the activation reaches every row."""
+    rng = np.random.default_rng(n_out + 7 * n_in)
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    bias = synth.activation(rng, n_out)
+    dw, dx, db, do = gpu.upload(w), gpu.upload(x), gpu.upload(bias), gpu.alloc(n_out * 4)
+    seen = {}
+    try:
+        for cfg in (44, 82, 84, 162):
+            gpu.tune(HAKO_TUNE_Q6K_ROWS, cfg)
+            for b in (None, db):
+                gpu.q6k_gemv(do, dw, dx, b, n_out, n_in)
+                v = gpu.download(do, np.float32, (n_out,))
+                key = b is None
+                if key in seen:
+                    assert np.array_equal(seen[key].view(np.uint32), v.view(np.uint32)), (cfg, key)
+                else:
+                    seen[key] = v
+        xn = x.copy()
+        xn[n_in // 2 + 5] = np.nan
+        dxn = gpu.upload(xn)
+        gpu.q6k_gemv(do, dw, dxn, None, n_out, n_in)
+        nan_out = gpu.download(do, np.float32, (n_out,))
+        dxn.free()
+    finally:
+        gpu.tune(HAKO_TUNE_Q6K_ROWS, 0)
+        for b in (dw, dx, db, do):
+            b.free()
+    assert np.all(np.isnan(nan_out))
+    want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True, threads=16)
+    assert maxabs_rel(seen[False], want) < TOL
+    want = oracle.matmul(Q6, w, x, n_out, n_in, f64=True, threads=16)
+    assert maxabs_rel(seen[True], want) < TOL
+
+
+@pytest.mark.parametrize("n_out,n_in", [(2048, 11008), (33, 11008), (500, 18944)])
+def test_q6k_flat_part_widths(gpu, oracle, n_out, n_in):
+    """The flat grid's wide rows cut into 32- or 64-chunk parts (2 and 4 row
+    items per wave): within 1e-5 of the oracle."""
+    rng = np.random.default_rng(n_out + 11 * n_in)
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    want = oracle.matmul(Q6, w, x, n_out, n_in, f64=True, threads=16)
+    try:
+        for seg in (32, 64):
+            for items in (2, 4):
+                gpu.tune(HAKO_TUNE_Q6K_FLAT_SEG, seg)
+                gpu.tune(HAKO_TUNE_Q6K_FLAT_ITEMS, items)
+                got = gpu_matmul(gpu, Q6, w, x, n_out, n_in)
+                assert maxabs_rel(got, want) < TOL, (seg, items)
+    finally:
+        gpu.tune(HAKO_TUNE_Q6K_FLAT_SEG, 0)
+        gpu.tune(HAKO_TUNE_Q6K_FLAT_ITEMS, -1)
 
 
 def test_q6k_full_int8_scales(gpu, oracle):

@@ -149,6 +149,40 @@ def test_q8_golden_bit_exact(oracle, golden):
         assert np.array_equal(xs.view(np.uint32), g["xs"][r].view(np.uint32)), r
 
 
+def q8_non_finite_rows() -> np.ndarray:
+    """32-blocks holding NaN and infinities in the places that matter to the
+    quantizer's maximum and codes: one NaN (first, middle, last), a block of
+    NaNs, +inf, -inf, both, NaN with inf, and a block of infinities."""
+    rng = np.random.default_rng(77)
+    rows = rng.standard_normal((10, 64)).astype(np.float32)
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    rows[0, 0] = nan
+    rows[1, 17] = nan
+    rows[2, 31] = nan
+    rows[3, :32] = nan
+    rows[4, 5] = inf
+    rows[5, 40] = -inf
+    rows[6, 3], rows[6, 9] = inf, -inf
+    rows[7, 3], rows[7, 9] = nan, inf
+    rows[8, 32:] = inf
+    rows[9, :] = nan
+    return rows
+
+
+def test_q8_non_finite_matches_compiled_reference(oracle):
+    """NaN and infinite inputs: the oracle's codes and scales against the
+    reference's compiled quantize_row_q8_32 (a NaN never enters the block
+    maximum; a non-finite product converts to code 0; an infinite maximum
+    gives an infinite scale)."""
+    from oracle.hako_oracle import RefLib
+    ref = RefLib()
+    for r, x in enumerate(q8_non_finite_rows()):
+        wq, ws = ref.quantize_q8_32(x)
+        oq, os_ = oracle.quantize_q8_32(x)
+        assert np.array_equal(oq, wq), r
+        assert np.array_equal(os_.view(np.uint32), ws.view(np.uint32)), r
+
+
 def test_q8_known_answer():
     """amax 0x400861D9: the compiled form gives xs 0x3C8974C2."""
     from oracle.hako_oracle import Oracle
