@@ -361,7 +361,11 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 	// 1. activation (and norm weight) loads, then residual / bias, then weights
 	float4 xv[XP], nv[XP];
 	uint4 oa[XP][2];
-	int4 of[XP];
+	// the accumulator's non-finite flags: read by workgroup 0 alone (an empty
+	// range for the others, no traffic), which stores x + o as the residual
+	uint4 of[XP];
+	const __amdgpu_buffer_rsrc_t fr =
+	    stream_rsrc(OACC ? (const void *)acc_flags(oacc, n_in) : nullptr, (OACC && blockIdx.x == 0) ? 4u * n_in : 0u);
 #pragma unroll
 	for (int k = 0; k < XP; k++) {
 		const int e = min((int)(threadIdx.x + k * T) * 4, n_in - 4);
@@ -370,7 +374,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		if (OACC) {
 			oa[k][0] = *(const uint4 *)(oacc + e);
 			oa[k][1] = *(const uint4 *)(oacc + e + 2);
-			of[k] = *(const int4 *)(acc_flags(oacc, n_in) + e);
+			of[k] = ld_b128(fr, 4u * e);
 		}
 	}
 	float pre[NG];   // bias (Store) or the residual (Add) of the row this lane writes
@@ -396,16 +400,22 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 	}
 
 	// 2. prologue: (residual accumulator,) (rmsnorm and) q8_32 quantization into LDS
+	// The activation is x + the finite part of o. Where o is not finite (a
+	// flag), the residual x + o that workgroup 0 stores carries the NaN or
+	// infinity; the activation here need not: a non-finite residual element
+	// makes every later rmsnorm scale NaN or 0, so every later q8 code is 0 (the
+	// reference's as well) and the logits are NaN, whatever this layer's
+	// gate/up sums were.
 	if (OACC) {
-		auto fx = [](uint32_t lo, uint32_t hi, int fl) -> float {
-			return from_fixed((long long)(((unsigned long long)hi << 32) | lo), fl);
+		auto fx = [](uint32_t lo, uint32_t hi) -> float {
+			return from_fixed((long long)(((unsigned long long)hi << 32) | lo), 0);
 		};
 #pragma unroll
 		for (int k = 0; k < XP; k++) {
-			xv[k].x += fx(oa[k][0].x, oa[k][0].y, of[k].x);
-			xv[k].y += fx(oa[k][0].z, oa[k][0].w, of[k].y);
-			xv[k].z += fx(oa[k][1].x, oa[k][1].y, of[k].z);
-			xv[k].w += fx(oa[k][1].z, oa[k][1].w, of[k].w);
+			xv[k].x += fx(oa[k][0].x, oa[k][0].y);
+			xv[k].y += fx(oa[k][0].z, oa[k][0].w);
+			xv[k].z += fx(oa[k][1].x, oa[k][1].y);
+			xv[k].w += fx(oa[k][1].z, oa[k][1].w);
 		}
 	}
 	float scale = 1.0f;
@@ -448,7 +458,12 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		for (int k = 0; k < XP; k++) {
 			const int e = (threadIdx.x + k * T) * 4;
 			if (e < n_in) {
-				*(float4 *)(xmid + e) = xv[k];
+				// x + o with the non-finite terms: finite + NaN or +-inf is the
+				// same value however the finite part was rounded
+				auto nf = [](float v, uint32_t fl) -> float { return fl ? v + from_fixed(0, (int)fl) : v; };
+				const float4 xm = make_float4(nf(xv[k].x, of[k].x), nf(xv[k].y, of[k].y), nf(xv[k].z, of[k].z),
+				                              nf(xv[k].w, of[k].w));
+				*(float4 *)(xmid + e) = xm;
 				*(uint4 *)(oacc_next + e) = make_uint4(0u, 0u, 0u, 0u);
 				*(uint4 *)(oacc_next + e + 2) = make_uint4(0u, 0u, 0u, 0u);
 				*(int4 *)(acc_flags(oacc_next, n_in) + e) = make_int4(0, 0, 0, 0);
