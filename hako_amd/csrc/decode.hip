@@ -1374,36 +1374,112 @@ int resid_rmsnorm_q8(hako_gpu_decoder *d, const float *part, int nsplit, const f
 	return HAKO_GPU_OK;
 }
 
-// The weight types the batched step runs (the Q4_K_M mix): Q4_K q/k/v/o/
-// gate/up, Q6_K down, Q4_K or Q6_K lm_head; d_model and kv_dim multiples of
-// 16 (skinny row segments start on 16-row boundaries) and d_model <= 4096 (a
-// quad per thread of a 1024-thread workgroup in the row kernels).
-bool batched_ok(const hako_gpu_model &m, const std::vector<hako_gpu_block> &blocks, int kv_dim) {
-	if (kv_dim % 16 || m.d_model % 16 || m.d_model > 4 * kRowT) return false;
-	if (m.t_out != HAKO_TYPE_Q4_K && m.t_out != HAKO_TYPE_Q6_K) return false;
-	for (const hako_gpu_block &B : blocks)
-		if (B.t_q != HAKO_TYPE_Q4_K || B.t_k != HAKO_TYPE_Q4_K || B.t_v != HAKO_TYPE_Q4_K || B.t_o != HAKO_TYPE_Q4_K ||
-		    B.t_gate != HAKO_TYPE_Q4_K || B.t_up != HAKO_TYPE_Q4_K || B.t_down != HAKO_TYPE_Q6_K)
-			return false;
-	return true;
+// A layer of the batched step runs fused (the row kernels, q/k/v as one
+// skinny launch over three segments, the o and down sums left for the next
+// row kernel) when it has the Q4_K_M mix — Q4_K q/k/v/o/gate/up, Q6_K down —
+// and d_model <= 4096 (a quad per thread of a 1024-thread workgroup in the
+// row kernels), with d_model and kv_dim multiples of 16 (skinny row segments
+// start on 16-row boundaries). Any other layer runs generic: one launch per
+// matmul and elementwise launches, as the reference's forward
+// (src/model.c:102-157) for each sequence.
+bool batched_dims_ok(const hako_gpu_model &m, int kv_dim) {
+	return kv_dim % 16 == 0 && m.d_model % 16 == 0 && m.d_model <= 4 * kRowT;
+}
+bool batched_fused_layer(const hako_gpu_model &m, const hako_gpu_block &B, int kv_dim) {
+	return batched_dims_ok(m, kv_dim) && B.t_q == HAKO_TYPE_Q4_K && B.t_k == HAKO_TYPE_Q4_K &&
+	       B.t_v == HAKO_TYPE_Q4_K && B.t_o == HAKO_TYPE_Q4_K && B.t_gate == HAKO_TYPE_Q4_K &&
+	       B.t_up == HAKO_TYPE_Q4_K && B.t_down == HAKO_TYPE_Q6_K;
 }
 
-// One step of n_seq > 1 sequences: every matmul a skinny MFMA GEMM that
-// streams the weights once for all sequences. The o and down matmuls leave
-// their split partial sums for the next kernel, which adds them to the
-// residual stream on its way (rmsnorm + q8, or the lm_head's split); the
-// gate/up sums go straight into the fp16 form of the down matmul.
+// One matmul of the batched step outside the fused layers, for every
+// sequence: y[t * ldy + r] = (W x_t)[r] (+ bias[r]) for t < n_seq, x rows of
+// n_in floats. Q4_K: the q8_32 rows in d->xq / d->xs and the skinny int8
+// kernel; Q6_K: the fp16 hi/lo rows in d->xh / d->xl and the skinny fp16
+// kernel; F16 / F32: one dense GEMV per sequence. Split sums go to the
+// decoder's skpart (sized for these shapes when the decoder is created).
+int batch_matmul(hako_gpu_decoder *d, float *y, int ldy, const float *x, int type, const void *w,
+                 const float *bias, int n_out, int n_in) {
+	const int M = d->n_seq;
+	SkSegs s{};
+	s.n = 1;
+	s.s[0] = {(const uint8_t *)w, bias, y, 0, n_out, ldy};
+	switch (type) {
+	case HAKO_TYPE_Q4_K:
+		if (int rc = hako_gpu_quantize_q8_32(x, M, n_in, d->xq, d->xs)) return rc;
+		return q4k_skinny(s, kSkStore, d->xq, d->xs, M, n_in, n_out, d->skpart, d->skpart_floats);
+	case HAKO_TYPE_Q6_K:
+		if (int rc = f16_split(x, d->xh, d->xl, d->esc, M, n_in)) return rc;
+		return q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, n_in, n_out, d->skpart, d->skpart_floats);
+	default:
+		for (int t = 0; t < M; t++)
+			if (int rc = hako_gpu_dense_gemv(y + (size_t)t * ldy, type, w, x + (size_t)t * n_in, bias, n_out, n_in))
+				return rc;
+		return HAKO_GPU_OK;
+	}
+}
+
+// Split floats the batched step's matmuls need in skpart: the fused layers'
+// launches and every generic matmul shape (either quantized type).
+size_t batched_part_floats(const hako_gpu_model &m, int kv_dim) {
+	const int D = m.d_model, F = m.ffn_dim, qkv_rows = D + 2 * kv_dim;
+	size_t need = 0;
+	auto take = [&](size_t v) { need = v > need ? v : need; };
+	if (batched_dims_ok(m, kv_dim)) {
+		take(q4k_skinny_part_floats(D, qkv_rows, kSkStore));
+		take(q4k_skinny_part_floats(D, D, kSkPart));
+		take(q4k_skinny_part_floats(D, 2 * F, kSkPart));
+		take(q6k_skinny_part_floats(F, D, kSkPart));
+	}
+	const int shapes[6][2] = {{D, D}, {D, kv_dim}, {D, F}, {F, D}, {D, m.vocab}, {D, qkv_rows}};
+	for (const auto &sh : shapes) {
+		take(q4k_skinny_part_floats(sh[0], sh[1], kSkStore));
+		take(q6k_skinny_part_floats(sh[0], sh[1], kSkStore));
+	}
+	return need;
+}
+
+// One step of n_seq > 1 sequences. Fused layers: every matmul a skinny MFMA
+// GEMM that streams the weights once for all sequences; the o and down
+// matmuls leave their split partial sums for the next kernel, which adds
+// them to the residual stream on its way (rmsnorm + q8, or the lm_head's
+// split); the gate/up sums go straight into the fp16 form of the down
+// matmul. Generic layers first add any pending partials to the residual.
 int enqueue_batched_step(hako_gpu_decoder *d) {
 	const hako_gpu_model &m = d->m;
 	const int D = m.d_model, F = m.ffn_dim, KV = d->kv_dim, M = d->n_seq;
 	hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream(), (const uint8_t *)m.tok_embd, m.t_embd,
 	                   row_bytes(m.t_embd, D), d->tok, d->x, D, m.vocab);
 	HK_LAUNCHED("embed");
-	const int ns_o = q4k_skinny_splits(D, D), ns_gu = q4k_skinny_splits(D, 2 * F), ns_down = q6k_skinny_splits(F, D);
-	const float *pend = nullptr;   // the previous down matmul's partials
+	const bool dims_ok = batched_dims_ok(m, KV);
+	const int ns_o = dims_ok ? q4k_skinny_splits(D, D) : 0, ns_gu = dims_ok ? q4k_skinny_splits(D, 2 * F) : 0;
+	const int ns_down = dims_ok ? q6k_skinny_splits(F, D) : 0;
+	const float *pend = nullptr;   // the previous fused down matmul's partials
 	int pend_ns = 0;
 	for (int l = 0; l < m.n_layers; l++) {
 		const hako_gpu_block &B = d->blocks[l];
+		if (!batched_fused_layer(m, B, KV)) {
+			// generic layer (x holds the residual of every sequence)
+			if (pend) {
+				if (int rc = resid_rmsnorm_q8(d, pend, pend_ns, nullptr, D)) return rc;
+				pend = nullptr;
+			}
+			if (int rc = rmsnorm(d->x, B.attn_norm, d->xn, D, m.rms_eps, M)) return rc;
+			if (int rc = batch_matmul(d, d->qkv, d->qkv_dim, d->xn, B.t_q, B.wq, B.bq, D, D)) return rc;
+			if (int rc = batch_matmul(d, d->qkv + D, d->qkv_dim, d->xn, B.t_k, B.wk, B.bk, KV, D)) return rc;
+			if (int rc = batch_matmul(d, d->qkv + D + KV, d->qkv_dim, d->xn, B.t_v, B.wv, B.bv, KV, D)) return rc;
+			if (int rc = attention(d, l)) return rc;
+			if (int rc = batch_matmul(d, d->tmp, D, d->att, B.t_o, B.wo, nullptr, D, D)) return rc;
+			if (int rc = add(d->x, d->x, d->tmp, M * D)) return rc;
+			if (int rc = rmsnorm(d->x, B.ffn_norm, d->xn, D, m.rms_eps, M)) return rc;
+			if (int rc = batch_matmul(d, d->g, F, d->xn, B.t_gate, B.gate, nullptr, F, D)) return rc;
+			if (int rc = batch_matmul(d, d->u, F, d->xn, B.t_up, B.up, nullptr, F, D)) return rc;
+			hipLaunchKernelGGL(silu_mul_kernel, dim3((M * F + 255) / 256), dim3(256), 0, stream(), d->h, d->g, d->u,
+			                   M * F);
+			HK_LAUNCHED("silu_mul");
+			if (int rc = batch_matmul(d, d->tmp, D, d->h, B.t_down, B.down, nullptr, D, F)) return rc;
+			if (int rc = add(d->x, d->x, d->tmp, M * D)) return rc;
+			continue;
+		}
 		// 1. residual, rmsnorm, q8; q, k, v: rows [q | k | v] of qkv[t][D + 2KV]
 		if (int rc = resid_rmsnorm_q8(d, pend, pend_ns, B.attn_norm, D)) return rc;
 		SkSegs s{};
@@ -1441,14 +1517,19 @@ int enqueue_batched_step(hako_gpu_decoder *d) {
 	SkSegs s{};
 	s.n = 1;
 	s.s[0] = {(const uint8_t *)m.out_weight, nullptr, d->logits, 0, m.vocab, m.vocab};
-	if (m.t_out == HAKO_TYPE_Q4_K) {
+	if (dims_ok && m.t_out == HAKO_TYPE_Q4_K) {
 		if (int rc = resid_rmsnorm_q8(d, pend, pend_ns, m.out_norm, D)) return rc;
 		if (int rc = q4k_skinny(s, kSkStore, d->xq, d->xs, M, D, m.vocab, d->skpart, d->skpart_floats)) return rc;
-	} else {
+	} else if (dims_ok && m.t_out == HAKO_TYPE_Q6_K) {
 		hipLaunchKernelGGL(resid_rmsnorm_split_kernel, dim3(M), dim3(kRowT), 0, stream(), d->x, pend, pend_ns,
 		                   m.out_norm, m.rms_eps, d->xh, d->xl, d->esc, D);
 		HK_LAUNCHED("resid_rmsnorm_split");
 		if (int rc = q6k_skinny(s, kSkStore, d->xh, d->xl, d->esc, M, D, m.vocab, d->skpart, d->skpart_floats)) return rc;
+	} else {
+		if (pend)
+			if (int rc = resid_rmsnorm_q8(d, pend, pend_ns, nullptr, D)) return rc;
+		if (int rc = rmsnorm(d->x, m.out_norm, d->xn, D, m.rms_eps, M)) return rc;
+		if (int rc = batch_matmul(d, d->logits, m.vocab, d->xn, m.t_out, m.out_weight, nullptr, m.vocab, D)) return rc;
 	}
 	if (int rc = argmax(d)) return rc;
 	return HAKO_GPU_OK;
@@ -1835,13 +1916,6 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	hako_gpu_decoder *d = new hako_gpu_decoder();
 	d->m = *m;
 	d->blocks.assign(m->blocks, m->blocks + m->n_layers);
-	if (n_seq > 1 && !batched_ok(d->m, d->blocks, m->n_kv_heads * m->head_dim)) {
-		delete d;
-		return set_error(HAKO_GPU_ETYPE,
-		                 "batched decode (n_seq > 1) runs the Q4_K_M mix (Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or "
-		                 "Q6_K output) with d_model <= %d, d_model and n_kv_heads*head_dim multiples of 16",
-		                 4 * kRowT);
-	}
 	d->m.blocks = nullptr;
 	d->n_seq = n_seq;
 	d->max_seq = max_seq;
@@ -1875,16 +1949,11 @@ int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hak
 	HK_ALLOC(d->xa, sizeof(float) * D);
 	const int DF = F > D ? F : D;
 	// split-K partials of the largest skinny matmul of a step
-	size_t skpart = 0;
-	const int qkv_rows = D + 2 * d->kv_dim;
-	const size_t needs[6] = {q4k_skinny_part_floats(D, qkv_rows, kSkStore), q4k_skinny_part_floats(D, D, kSkPart),
-	                         q4k_skinny_part_floats(D, 2 * F, kSkPart), q6k_skinny_part_floats(F, D, kSkPart),
-	                         m->t_out == HAKO_TYPE_Q4_K ? q4k_skinny_part_floats(D, m->vocab, kSkStore) : 0,
-	                         m->t_out == HAKO_TYPE_Q6_K ? q6k_skinny_part_floats(D, m->vocab, kSkStore) : 0};
-	for (size_t nf : needs) skpart = nf > skpart ? nf : skpart;
+	const size_t skpart = batched_part_floats(d->m, d->kv_dim);
 	if (n_seq > 1) {
-		HK_ALLOC(d->xq, (size_t)n_seq * D);
-		HK_ALLOC(d->xs, sizeof(float) * n_seq * (D / 32));
+		// q8 rows of the widest matmul input (generic layers quantize h too)
+		HK_ALLOC(d->xq, (size_t)n_seq * DF);
+		HK_ALLOC(d->xs, sizeof(float) * n_seq * (DF / 32));
 		HK_ALLOC(d->xh, sizeof(_Float16) * n_seq * DF);
 		HK_ALLOC(d->xl, sizeof(_Float16) * n_seq * DF);
 		HK_ALLOC(d->esc, sizeof(float) * n_seq);

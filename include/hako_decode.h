@@ -56,13 +56,14 @@ typedef struct hako_gpu_decoder hako_gpu_decoder;
  * (KV caches, activations and the rope table are allocated here, once).
  * Requires head_dim 64 or 128, n_heads % n_kv_heads == 0 with at most 8
  * query heads per KV head, d_model and ffn_dim multiples of 256, and
- * 1 <= n_seq <= 16. With n_seq > 1 every step advances all sequences
- * together, each matmul streaming its weights once for all of them (the
- * Q4_K_M mix: Q4_K q/k/v/o/gate/up, Q6_K down, Q4_K or Q6_K lm_head, and
- * d_model <= 4096); n_seq == 1 takes any F32/F16/Q4_K/Q6_K mix. Every sum
- * of a step has a fixed order or is exact (with n_seq == 1 and a Q4_K output
- * projection its 256-input block sums meet in a 64-bit fixed-point
- * accumulator on the 2^-32 grid), so steps are bit-reproducible. */
+ * 1 <= n_seq <= 16. Every tensor may be F32, F16, Q4_K or Q6_K, chosen per
+ * layer. With n_seq > 1 every step advances all sequences together, each
+ * matmul streaming its weights once for all of them; layers of the Q4_K_M
+ * mix (Q4_K q/k/v/o/gate/up, Q6_K down) with d_model <= 4096 take fused
+ * launches, other layers one launch per matmul. Every sum of a step has a
+ * fixed order or is exact (with n_seq == 1 and Q4_K output projections their
+ * 256-input block sums meet in a 64-bit fixed-point accumulator on the 2^-32
+ * grid), so steps are bit-reproducible. */
 int hako_gpu_decoder_create(const hako_gpu_model *m, int n_seq, int max_seq, hako_gpu_decoder **dec);
 int hako_gpu_decoder_destroy(hako_gpu_decoder *dec);
 

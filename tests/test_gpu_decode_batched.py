@@ -33,6 +33,21 @@ UNTIED_Q4_OUT = mlf2.Qwen2Config(n_layers=2, d_model=1792, n_heads=14, n_kv_head
 # workgroups of chunks per sequence, the last one partial
 LONG = mlf2.Qwen2Config(n_layers=2, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=2304,
                         vocab=1024, ctx=2304)
+# a Q4_K_M file as the converter writes one: Q6_K attn_v and ffn_down in some
+# layers, Q4_K ffn_down in the others (layers outside the fused mix run one
+# launch per matmul; layer 2 is fused)
+KQM = mlf2.Qwen2Config(n_layers=3, d_model=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=1024, vocab=1024,
+                       ctx=256, tied=False, embd_type=synth.TYPE_Q4_K,
+                       layer_types=(((0, "attn_v"), synth.TYPE_Q6_K), ((1, "ffn_down"), synth.TYPE_Q4_K)))
+# d_model 5120 (the Qwen2.5-14B width): past the fused row kernels' 4096
+WIDE = mlf2.Qwen2Config(n_layers=2, d_model=5120, n_heads=40, n_kv_heads=8, head_dim=128, ffn_dim=1536,
+                        vocab=1000, ctx=256)
+# dense weight types and a Q6_K q/k/v, F32 output
+DENSE = mlf2.Qwen2Config(n_layers=2, d_model=256, n_heads=2, n_kv_heads=1, head_dim=128, ffn_dim=512, vocab=640,
+                         ctx=256, attn_type=synth.TYPE_F16, gate_up_type=synth.TYPE_F32, down_type=synth.TYPE_Q4_K,
+                         embd_type=synth.TYPE_F16, tied=False, out_type=synth.TYPE_F32,
+                         layer_types=(((1, "attn_q"), synth.TYPE_Q6_K), ((1, "attn_k"), synth.TYPE_Q6_K),
+                                      ((1, "attn_v"), synth.TYPE_Q6_K)))
 
 
 @pytest.fixture(scope="module")
@@ -61,12 +76,16 @@ def seq_setup(cfg, n_seq, seed, max_pos):
     return pos.astype(np.int32), starts.astype(np.int32), kvs
 
 
-# logits bars: measured maxima 4.1e-7, 8.1e-5, 2.3e-5, 4.7e-4, 6.5e-7
+# logits bars: measured maxima 4.1e-7, 8.1e-5, 2.3e-5, 4.7e-4, 6.5e-7, 4.2e-7, 3.8e-6, 4.3e-4 (one int8
+# of a q8 row flipped, the Q4_K down projection of the dense-type model)
 @pytest.mark.parametrize("cfg,n_seq,seed,max_seq,max_pos,bar", [(TINY, 4, 1, 256, 200, 2e-6),
                                                                  (TINY, 16, 2, 256, 200, 4e-4),
                                                                  (SMALL_128, 16, 3, 256, 200, 1.1e-4),
                                                                  (UNTIED_Q4_OUT, 5, 4, 256, 200, 2.3e-3),
-                                                                 (LONG, 6, 5, 2304, 2200, 3.2e-6)])
+                                                                 (LONG, 6, 5, 2304, 2200, 3.2e-6),
+                                                                 (KQM, 5, 6, 256, 200, 2.1e-6),
+                                                                 (WIDE, 3, 7, 256, 200, 1.9e-5),
+                                                                 (DENSE, 4, 8, 256, 200, 2.2e-3)])
 def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, n_seq, seed, max_seq, max_pos,
                                                        bar):
     from dropin import prefilled_greedy
@@ -145,18 +164,18 @@ def test_batched_sequences_are_independent(gpu, tmp_path):
     assert batch[:, 3].tolist() == alone.tolist()
 
 
-def test_batched_rejects_other_weight_mixes(gpu, tmp_path):
+def test_batched_decoder_sequence_count(gpu, tmp_path):
+    """1 to 16 sequences per decoder, whatever the weight mix."""
     from hako_amd.decoder import Decoder
     from hako_amd.gpu import HakoGpuError
     path = str(tmp_path / "m.mlf2")
     cfg = mlf2.Qwen2Config(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512,
                            vocab=512, ctx=64, down_type=synth.TYPE_Q4_K)
     mlf2.write_qwen2(path, cfg, 13)
-    with pytest.raises(HakoGpuError, match="Q4_K_M"):
-        Decoder(gpu, path, n_seq=4, max_seq=64)
     with pytest.raises(HakoGpuError, match="sequences"):
         Decoder(gpu, path, n_seq=17, max_seq=64)
-    Decoder(gpu, path, n_seq=1, max_seq=64).close()   # one sequence takes any mix
+    for n in (1, 4, 16):
+        Decoder(gpu, path, n_seq=n, max_seq=64).close()
 
 
 @pytest.mark.timeout(900)
