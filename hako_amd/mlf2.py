@@ -55,6 +55,12 @@ class Qwen2Config:
     # per-layer exceptions: ((layer, role), type) pairs, role one of attn_q,
     # attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down
     layer_types: tuple = ()
+    # Q4_K matrices drawn with zero-mean weights (synth.q4k_blocks_centered):
+    # the greedy tokens of such a random model change from step to step
+    centered: bool = False
+    # scale of the d (and dmin) ranges of the attn_output and ffn_down blocks:
+    # below 1 each layer adds a smaller update to the residual stream
+    resid_scale: float = 1.0
 
 
 # The two model shapes the benchmarks use (Qwen2.5-3B and Qwen2-7B).
@@ -96,13 +102,14 @@ def tensor_plan(cfg: Qwen2Config):
     return plan
 
 
-def _tensor_bytes(rng, name: str, qtype: int, n_in: int, n_out: int) -> np.ndarray:
+def _tensor_bytes(rng, name: str, qtype: int, n_in: int, n_out: int, centered: bool = False,
+                  scale: float = 1.0) -> np.ndarray:
     if name.endswith("norm.weight"):
         v = (1.0 + 0.1 * rng.standard_normal(n_in)).astype(np.float32)
         return v.view(np.uint8)
     if name.endswith(".bias"):
         return (0.1 * rng.standard_normal(n_in)).astype(np.float32).view(np.uint8)
-    return synth.weight(rng, qtype, n_out, n_in).reshape(-1)
+    return synth.weight(rng, qtype, n_out, n_in, centered, scale).reshape(-1)
 
 
 def write_qwen2(path: str, cfg: Qwen2Config, seed: int) -> dict:
@@ -135,7 +142,8 @@ def write_qwen2(path: str, cfg: Qwen2Config, seed: int) -> dict:
         f.write(b"\0" * (data_off - f.tell()))
         for name, qt, n_in, n_out, off, nbytes in entries:
             f.seek(data_off + off)
-            f.write(_tensor_bytes(rng, name, qt, n_in, n_out).tobytes())
+            scale = cfg.resid_scale if name.endswith(("attn_output.weight", "ffn_down.weight")) else 1.0
+            f.write(_tensor_bytes(rng, name, qt, n_in, n_out, cfg.centered, scale).tobytes())
         f.truncate(data_off + cur)
     return {e[0]: e[1:] for e in entries}
 

@@ -22,6 +22,8 @@ ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
 ORACLE_LIB = os.path.join(ORACLE_DIR, "_build", "libhako_oracle.so")
 REF_LIB = os.path.join(ORACLE_DIR, "_ref", "libhakm_ref.so")
 REF_MODEL_LIB = os.path.join(ORACLE_DIR, "_ref", "libhakm_ref_model.so")
+# the same reference sources built without -ffast-math (oracle/ref.mk)
+REF_NOFAST_LIB = os.path.join(ORACLE_DIR, "_ref", "libhakm_ref_nofast.so")
 
 _vp, _i, _i64 = C.c_void_p, C.c_int, C.c_int64
 
@@ -265,3 +267,25 @@ def prefilled_greedy(lib: C.CDLL, path: str, kv: np.ndarray, pos: int, start: in
             release(ctx)
         lib.hakm_ctx_free(ctx)
     return toks[1:], np.stack(logits)
+
+
+def prefilled_forced(lib: C.CDLL, path: str, kv: np.ndarray, pos: int, tokens, vocab: int, max_seq: int):
+    """As prefilled_greedy, but each step is fed the given token (teacher
+    forcing): the logits of hakm_forward for tokens[0], tokens[1], ... from
+    the prefilled caches."""
+    ctx = lib.hakm_ctx_new(path.encode(), max_seq)
+    assert ctx, f"hakm_ctx_new({path}) failed"
+    logits = []
+    try:
+        c = HakmCtx.from_address(ctx)
+        n_layers, kvd = kv.shape[1], kv.shape[3]
+        for which, ptr in ((0, c.k_cache), (1, c.v_cache)):
+            cache = np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_float)), shape=(n_layers, max_seq, kvd))
+            cache[:, :pos, :] = kv[which]
+        c.pos = pos
+        for t in tokens:
+            p = lib.hakm_forward(ctx, int(t))
+            logits.append(np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(vocab,)).copy())
+    finally:
+        lib.hakm_ctx_free(ctx)
+    return np.stack(logits)

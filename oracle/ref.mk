@@ -25,13 +25,21 @@ REF_ALL   := $(REF)/src/quant.c $(REF)/src/nn.c $(REF)/src/loader.c \
 # exporting the nn.h surface was loaded RTLD_GLOBAL first (the drop-in test).
 REF_MODEL := $(REF)/src/model.c $(REF)/src/loader.c
 
-all: $(OUT)/libhakm_ref.so $(OUT)/libhakm_ref_model.so $(OUT)/build_info.txt
+# The same sources without -ffast-math: a second build of the reference whose
+# rounding differs from the first only by the compiler's fast-math rewrites —
+# the yardstick of how far two correct builds drift on a sensitive model.
+NOFAST   := -O2 -std=c11 -Wall -Wextra -pthread -march=x86-64-v3 -fPIC
+
+all: $(OUT)/libhakm_ref.so $(OUT)/libhakm_ref_model.so $(OUT)/libhakm_ref_nofast.so $(OUT)/build_info.txt
 
 $(OUT):
 	mkdir -p $(OUT)
 
 $(OUT)/libhakm_ref.so: $(REF_ALL) | $(OUT)
 	$(CC) $(REFFLAGS) -o $@ $(REF_ALL) $(LDFLAGS)
+
+$(OUT)/libhakm_ref_nofast.so: $(REF_ALL) | $(OUT)
+	$(CC) $(NOFAST) -o $@ $(REF_ALL) $(LDFLAGS)
 
 $(OUT)/libhakm_ref_model.so: $(REF_MODEL) | $(OUT)
 	$(CC) $(REFFLAGS) -o $@ $(REF_MODEL) $(LDFLAGS)

@@ -17,3 +17,16 @@ def within(name: str, got: np.ndarray, want: np.ndarray, bar: float) -> float:
     print(f"[bar] {name}: {err:.3e} (bar {bar:.0e})", flush=True)
     assert err < bar, f"{name}: {err:.3e} >= {bar:.0e}"
     return err
+
+
+def near_max_steps(logits, want_tokens, want_logits, tol: float) -> list:
+    """The steps at which token want_tokens[i] is not within `tol` (relative
+    to the range of want_logits[i]) of the maximum of logits[i]: those where
+    an implementation could not have picked it up to a rounding drift of
+    that size."""
+    bad = []
+    for i, (lg, t, wl) in enumerate(zip(logits, want_tokens, want_logits)):
+        rng = float(np.max(wl) - np.min(wl))
+        if (float(np.max(lg)) - float(lg[int(t)])) > tol * rng:
+            bad.append(i)
+    return bad

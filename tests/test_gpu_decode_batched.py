@@ -268,3 +268,58 @@ def test_batched_sequences_reach_max_seq(gpu, ref, tmp_path):
         assert int(toks[s]) == want[0]
         # measured 1.9e-7, 8.0e-5, 5.6e-7
         within(f"batched max_seq logits seq {s}", lg[s], want_lg[0], 4e-4)
+
+
+@pytest.mark.timeout(900)
+def test_qwen2_7b_sixteen_sequences_varied_tokens(gpu, ref, tmp_path):
+    """The full Qwen2-7B shape with zero-mean Q4_K matrices (a random model
+    whose greedy tokens change from step to step, and which amplifies every
+    difference in rounding order), 16 sequences at their own positions
+    (seeded caches up to 300 positions), each step of the batch fed every
+    sequence's reference greedy token: the device's logits drift from the
+    reference's no more than 4x the reference's own build without -ffast-math
+    does, and at every step each sequence's reference pick is within that
+    drift of the device's maximum."""
+    import dataclasses
+    from dropin import bind_ctx, prefilled_greedy
+    from hako_amd.decoder import Decoder
+    from helpers import maxabs_rel
+    from oracle.hako_oracle import REF_NOFAST_LIB, prefilled_forced
+    ref_nofast = bind_ctx(C.CDLL(REF_NOFAST_LIB))
+    cfg = dataclasses.replace(mlf2.QWEN2_7B, centered=True)
+    path = str(tmp_path / "qwen2_7b_centered.mlf2")
+    mlf2.write_qwen2(path, cfg, 72)
+    n_seq, steps, max_seq = 16, 6, 320
+    pos, starts, kvs = seq_setup(cfg, n_seq, 72, 300)
+    want, want_lg, nf_lg = [], [], []
+    for s in range(n_seq):
+        w, wl = prefilled_greedy(ref, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=steps,
+                                 vocab=cfg.vocab, max_seq=max_seq)
+        want.append(w)
+        want_lg.append(wl)
+        nf_lg.append(prefilled_forced(ref_nofast, path, kvs[s], int(pos[s]), [int(starts[s])] + w[:-1], cfg.vocab,
+                                      max_seq))
+    want = np.array(want).T                               # [step][sequence]
+    fed = np.concatenate([starts[None], want[:-1]]).astype(np.int32)
+    assert len({int(t) for t in want.ravel()}) >= n_seq * steps // 2   # tokens change from step to step
+    dec = Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
+    try:
+        fill_kv(gpu, dec, kvs, cfg.n_layers)
+        dec.set_pos(pos)
+        got, logits = [], []
+        for t in fed:
+            nxt, lg = dec.step(t, logits=True)
+            got.append(nxt.copy())
+            logits.append(lg)
+    finally:
+        dec.close()
+    from helpers import near_max_steps
+    err_dev = max(maxabs_rel(logits[t][s], want_lg[s][t]) for s in range(n_seq) for t in range(steps))
+    err_nf = max(maxabs_rel(nf_lg[s][t], want_lg[s][t]) for s in range(n_seq) for t in range(steps))
+    same = int(np.sum(np.stack(got) == want))
+    print(f"[drift] 7B x16 centered: device {err_dev:.3e}, reference without fast-math {err_nf:.3e}; "
+          f"picks equal to the reference's {same}/{want.size}", flush=True)
+    assert err_dev <= 4 * max(err_nf, 1e-5)
+    tol = 2 * max(err_nf, err_dev)
+    for s in range(n_seq):
+        assert near_max_steps([logits[t][s] for t in range(steps)], want[:, s], want_lg[s], tol) == [], s

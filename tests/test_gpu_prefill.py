@@ -265,6 +265,57 @@ def test_prefill_qwen2_3b_prompt(gpu, ref, tmp_path):
     assert got == want
 
 
+def test_prefill_qwen2_3b_prompt_varied_tokens(gpu, ref, tmp_path):
+    """The full Qwen2.5-3B shape with zero-mean Q4_K matrices (a random model
+    whose greedy tokens change from step to step and which amplifies every
+    difference in rounding order): a 150-token prompt in one pass, then 8
+    steps each fed the reference's previous greedy token. The device's logits
+    drift from the reference's no more than 4x the reference's own build
+    without -ffast-math does, and at every step the reference's pick is
+    within that drift of the device's maximum."""
+    import dataclasses
+    from dropin import bind_ctx
+    from helpers import maxabs_rel
+    from oracle.hako_oracle import REF_NOFAST_LIB
+    ref_nofast = bind_ctx(C.CDLL(REF_NOFAST_LIB))
+    cfg = dataclasses.replace(mlf2.QWEN2_3B, centered=True)
+    path = str(tmp_path / "qwen2_3b_centered.mlf2")
+    mlf2.write_qwen2(path, cfg, 33)
+    prompt = np.random.default_rng(33).integers(0, cfg.vocab, 150)
+    r, rn = RefSeq(ref, path, 168, cfg), RefSeq(ref_nofast, path, 168, cfg)
+    try:
+        lg = r.feed(prompt)
+        nlg = rn.feed(prompt)
+        want, want_lg, nf_lg = [], [lg], [nlg]
+        for _ in range(8):
+            want.append(int(np.argmax(lg)))
+            lg = r.forward(want[-1])
+            nf_lg.append(rn.forward(want[-1]))
+            want_lg.append(lg)
+    finally:
+        r.close()
+        rn.close()
+    assert len(set(want)) >= 4, want
+    dec = make(gpu, path, 1, 168)
+    try:
+        dec.set_pos(0)
+        first, lg = dec.prefill(prompt, logits=True)
+        got, logits = [first], [lg]
+        for t in want:
+            nxt, l1 = dec.step(t, logits=True)
+            got.append(int(nxt[0]))
+            logits.append(l1[0])
+    finally:
+        dec.close()
+    from helpers import near_max_steps
+    err_dev = max(maxabs_rel(g, w) for g, w in zip(logits, want_lg))
+    err_nf = max(maxabs_rel(g, w) for g, w in zip(nf_lg, want_lg))
+    print(f"[drift] 3B prompt centered: device {err_dev:.3e}, reference without fast-math {err_nf:.3e}; "
+          f"picks equal to the reference's {sum(a == b for a, b in zip(got, want))}/8", flush=True)
+    assert err_dev <= 4 * max(err_nf, 1e-5)
+    assert near_max_steps(logits[:8], want, want_lg[:8], 2 * max(err_nf, err_dev)) == []
+
+
 @pytest.mark.timeout(900)
 def test_prefill_qwen2_7b_512_token_prompt(gpu, ref, tmp_path):
     """The benchmarked prompt workload: the full Qwen2-7B shape (28 layers,
