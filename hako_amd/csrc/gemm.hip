@@ -275,6 +275,217 @@ __global__ __launch_bounds__(kGT, 3) void q4k_gemm_kernel(const SkSegs segs, con
 	for (int v = 0; v < 16; v++) st_f32(ors, off[v], EPI == kSkAdd ? ev[v] + (acc[v] + accm[v]) : (acc[v] + accm[v]) + ev[v]);
 }
 
+// ── Q4_K x q8, resident token tile ──
+//
+// The tiled kernel above stages a 64-token activation block from L2 for
+// every 64-row weight tile and waits out one memory round trip per stage.
+// Here a workgroup keeps all K of 32 tokens in LDS (32·(K+16) bytes of q8 plus
+// the per-(sub-block, token) factors (xs, −xs·Σxq), 40·K + 512 bytes in
+// all: K up to 3840) and its twelve waves stream weight rows past it, each
+// wave a 32-row unit through the whole K with the next super-block's loads in
+// flight, weights straight from memory into the MFMA operand registers. The
+// arithmetic is the tiled kernel's: per sub-block one
+// v_mfma_i32_32x32x32_i8 (the reference's iqx), the fold
+// acc += iqx·(d·s·xs) with the products d·s·xs from a v_mfma_f32_32x32x1f32
+// outer product, and the min term on v_mfma_f32_32x32x2f32.
+// Units: Store / Add rows 32u .. 32u+31 of the launch (a unit lies in one
+// segment: segment starts are multiples of 64); SwiGLU features
+// 16u .. 16u+15, MFMA rows 0-15 their gate rows and 16-31 their up rows, so a
+// lane holds each feature's gate and up sums side by side.
+// Grid: token tiles x R row ranges, in XCD-contiguous order with the token
+// tiles minor: the workgroups of one XCD share a row range, whose weights
+// then come from that XCD's L2 after the first read.
+constexpr int kRT = 32;          // tokens per workgroup
+constexpr int kRWaves = 12;      // waves per workgroup (one workgroup per CU: LDS), three per SIMD
+constexpr int kRMaxK = 3840;     // largest K whose token tile fits 160 KB of LDS
+
+__host__ __device__ inline size_t q4k_res_lds(int K) { return (size_t)kRT * (K + 16) + (size_t)(K / 32) * kRT * 8; }
+
+template <int EPI>
+__global__ __launch_bounds__(kRWaves * kWave, 1) void q4k_gemm_res_kernel(const SkSegs segs,
+                                                                       const int8_t *__restrict__ xq,
+                                                                       const float *__restrict__ xs, int M, int K,
+                                                                       int R, int units) {
+	extern __shared__ __align__(16) uint8_t res_lds[];
+	const int AP = K + 16;                              // bytes per staged token row
+	int8_t *a_s = (int8_t *)res_lds;
+	float2 *xn_s = (float2 *)(res_lds + kRT * AP);      // [sub-block][token]
+	const int mt = (M + kRT - 1) / kRT, G = mt * R;
+	const int p = xcd_tile(blockIdx.x, G);
+	if (p >= G) return;
+	const int rr = p / mt, m0 = (p - rr * mt) * kRT;
+	const int NB = K >> 8, NS = K >> 5;
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+	const int li = lane & 31, kh = lane >> 5;
+
+	// 1. the token tile: 16-byte pieces, all loads of a thread issued before
+	//    its stores (rows past M read as zero)
+	{
+		const __amdgpu_buffer_rsrc_t ars = stream_rsrc(xq, (uint32_t)M * (uint32_t)K);
+		const int ppr = K >> 4, total = kRT * ppr;
+		constexpr int kPer = (kRT * (kRMaxK / 16) + kRWaves * kWave - 1) / (kRWaves * kWave);
+		uint4 v[kPer];
+#pragma unroll
+		for (int u = 0; u < kPer; u++) {
+			const int c = tid + kRWaves * kWave * u, tok = c / ppr, pc = c - tok * ppr;
+			const bool on = c < total && m0 + tok < M;
+			v[u] = ld_b128(ars, on ? (uint32_t)(m0 + tok) * K + 16u * pc : kBufNone);
+		}
+#pragma unroll
+		for (int u = 0; u < kPer; u++) {
+			const int c = tid + kRWaves * kWave * u, tok = c / ppr, pc = c - tok * ppr;
+			if (c < total) *(uint4 *)(a_s + tok * AP + 16 * pc) = v[u];
+		}
+	}
+	__syncthreads();
+	{
+		const __amdgpu_buffer_rsrc_t srs = stream_rsrc(xs, (uint32_t)M * (uint32_t)NS * 4u);
+		for (int c = tid; c < kRT * NS; c += kRWaves * kWave) {
+			const int sb = c / kRT, tok = c - sb * kRT;
+			const float f = ld_f32(srs, m0 + tok < M ? 4u * ((uint32_t)(m0 + tok) * NS + sb) : kBufNone);
+			const int4 a = *(const int4 *)(a_s + tok * AP + 32 * sb), b = *(const int4 *)(a_s + tok * AP + 32 * sb + 16);
+			int ix = sdot4(a.x, 0x01010101, 0);
+			ix = sdot4(a.y, 0x01010101, ix);
+			ix = sdot4(a.z, 0x01010101, ix);
+			ix = sdot4(a.w, 0x01010101, ix);
+			ix = sdot4(b.x, 0x01010101, ix);
+			ix = sdot4(b.y, 0x01010101, ix);
+			ix = sdot4(b.z, 0x01010101, ix);
+			ix = sdot4(b.w, 0x01010101, ix);
+			xn_s[sb * kRT + tok] = make_float2(f, -f * (float)ix);
+		}
+	}
+	__syncthreads();
+
+	// 2. the units of this row range, one per wave at a time
+	const int u0 = (int)((long long)rr * units / R), u1 = (int)((long long)(rr + 1) * units / R);
+	const uint32_t rb = (uint32_t)NB * kQ4Bytes;
+	const int8_t *a_row = a_s + li * AP + 16 * kh;      // B operand: token li, K 16kh.. of each sub-block
+	const float2 *xn_row = xn_s + li;
+	const uint32_t lo4 = 0x0F0F0F0Fu;
+	const v16i zero = {};
+	const v32f zero32 = {};
+	struct Wt {
+		uint4 q[4];   // qs bytes 32g + 16kh .. +16 of the lane's row
+		uint4 h;      // d, dmin, 12 scale bytes
+	};
+	for (int u = u0 + wave; u < u1; u += kRWaves) {
+		// the lane's weight row (clamped into its matrix; rows past the end are
+		// computed and not stored)
+		const int r32 = 32 * u;
+		const int si = EPI == kSkSwiGLU ? 0
+		               : (segs.n > 2 && r32 >= segs.s[2].row0) ? 2 : (segs.n > 1 && r32 >= segs.s[1].row0) ? 1 : 0;
+		const SkSeg S = si == 0 ? segs.s[0] : (si == 1 ? segs.s[1] : segs.s[2]);
+		const int srows = S.rows;
+		// first output row of the unit in its segment (SwiGLU: first feature),
+		// the lane's weight row and matrix
+		const int out_row0 = EPI == kSkSwiGLU ? 16 * u : r32 - S.row0;
+		const int srow = EPI == kSkSwiGLU ? out_row0 + (li & 15) : out_row0 + li;
+		const uint8_t *wmat = (EPI == kSkSwiGLU && li >= 16) ? segs.s[1].w : S.w;
+		const uint8_t *wrow = wmat + (size_t)min(srow, srows - 1) * rb;
+		auto load = [&](Wt &w, int kb) {
+			const uint8_t *b = wrow + (size_t)kb * kQ4Bytes;
+			w.h = *(const uint4 *)b;
+#pragma unroll
+			for (int g = 0; g < 4; g++) w.q[g] = *(const uint4 *)(b + 16 + 32 * g + 16 * kh);
+		};
+		v16f acc = {}, accm = {};
+		auto compute = [&](const Wt &w, int kb) {
+			// (d·s, dmin·m) of sub-blocks 2g + kh, g = 0..3: bytes kh and 2 + kh
+			// of the scale words (reference quant.c:57-66 packing)
+			const float d = f16_to_f32(w.h.x & 0xFFFFu), dmin = f16_to_f32(w.h.x >> 16);
+			const uint32_t sh = 8u * kh;
+			const uint32_t a0 = w.h.y >> sh, a1 = w.h.z >> sh, a2 = w.h.w >> sh;
+			const uint32_t s_lo = a0 & 0x003F003Fu, m_lo = a1 & 0x003F003Fu;
+			const uint32_t s_hi = (a2 & 0x000F000Fu) | ((a0 >> 2) & 0x00300030u);
+			const uint32_t m_hi = ((a2 >> 4) & 0x000F000Fu) | ((a1 >> 2) & 0x00300030u);
+			const float ds[4] = {d * (float)(s_lo & 0xFFu), d * (float)(s_lo >> 16), d * (float)(s_hi & 0xFFu),
+			                     d * (float)(s_hi >> 16)};
+			const float dm[4] = {dmin * (float)(m_lo & 0xFFu), dmin * (float)(m_lo >> 16),
+			                     dmin * (float)(m_hi & 0xFFu), dmin * (float)(m_hi >> 16)};
+			const float2 *xn = xn_row + 8 * kb * kRT;
+#pragma unroll
+			for (int g = 0; g < 4; g++)
+				accm = __builtin_amdgcn_mfma_f32_32x32x2f32(dm[g], xn[(2 * g + kh) * kRT].y, accm, 0, 0, 0);
+			// the block's eight activation operands, all LDS reads issued at once
+			v4i bb[8];
+#pragma unroll
+			for (int j = 0; j < 8; j++) bb[j] = *(const v4i *)(a_row + 256 * kb + 32 * j);
+#pragma unroll
+			for (int g = 0; g < 4; g++) {
+				const v32f P = __builtin_amdgcn_mfma_f32_32x32x1f32(ds[g], xn[(2 * g + kh) * kRT].x, zero32, 0, 0, 0);
+				const uint4 q = w.q[g];
+				const v4i qlo = {(int)(q.x & lo4), (int)(q.y & lo4), (int)(q.z & lo4), (int)(q.w & lo4)};
+				const v4i qhi = {(int)((q.x >> 4) & lo4), (int)((q.y >> 4) & lo4), (int)((q.z >> 4) & lo4),
+				                 (int)((q.w >> 4) & lo4)};
+#pragma unroll
+				for (int h = 0; h < 2; h++) {
+					const v4i b = bb[2 * g + h];
+					const v16i iq = __builtin_amdgcn_mfma_i32_32x32x32_i8(h ? qhi : qlo, b, zero, 0, 0, 0);
+#pragma unroll
+					for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float)iq[v], P[16 * h + v], acc[v]);
+				}
+			}
+		};
+		// super-blocks in pairs, so each register set is named statically; the
+		// loads in the loop are unconditional (past the last block they repeat
+		// it), so the wait before each block's arithmetic counts only the older
+		// set
+		Wt wa, wb;
+		load(wa, 0);
+		int kb = 0;
+		for (; kb + 1 < NB; kb += 2) {
+			load(wb, kb + 1);
+			__builtin_amdgcn_sched_barrier(0);   // issued here, not next to their use
+			compute(wa, kb);
+			load(wa, min(kb + 2, NB - 1));
+			__builtin_amdgcn_sched_barrier(0);
+			compute(wb, kb + 1);
+		}
+		if (kb < NB) compute(wa, kb);   // odd NB: the last block, loaded into wa
+
+		// 3. epilogue; lane: token m0 + li, MFMA rows 8q4 + 4kh + r
+		const int tok = m0 + li;
+		if (EPI == kSkSwiGLU) {
+			if (tok < M) {
+				float *hr = S.out + (size_t)tok * S.ld;
+#pragma unroll
+				for (int q4 = 0; q4 < 2; q4++) {
+					const int f = out_row0 + 8 * q4 + 4 * kh;
+#pragma unroll
+					for (int r = 0; r < 4; r++)
+						if (f + r < srows)
+							hr[f + r] = silu(acc[4 * q4 + r] + accm[4 * q4 + r]) *
+							            (acc[4 * q4 + 8 + r] + accm[4 * q4 + 8 + r]);
+				}
+			}
+			continue;
+		}
+		const int ld = __builtin_amdgcn_readfirstlane(S.ld);
+		float *out = uniform_ptr(S.out);
+		const float *bias = uniform_ptr(S.bias);
+		const __amdgpu_buffer_rsrc_t ors = stream_rsrc(out, (uint32_t)M * (uint32_t)ld * 4u);
+		const __amdgpu_buffer_rsrc_t brs =
+		    stream_rsrc(bias ? (const void *)bias : (const void *)out, (EPI == kSkStore && bias) ? (uint32_t)srows * 4u : 0u);
+		uint32_t off[16];
+		float ev[16];
+#pragma unroll
+		for (int q4 = 0; q4 < 4; q4++) {
+			const int row = out_row0 + 8 * q4 + 4 * kh;
+#pragma unroll
+			for (int r = 0; r < 4; r++) {
+				const bool ok = tok < M && row + r < srows;
+				off[4 * q4 + r] = ok ? 4u * ((uint32_t)tok * ld + row + r) : kBufNone;
+				ev[4 * q4 + r] = EPI == kSkAdd ? ld_f32(ors, off[4 * q4 + r]) : ld_f32(brs, ok ? 4u * (row + r) : kBufNone);
+			}
+		}
+#pragma unroll
+		for (int v = 0; v < 16; v++)
+			st_f32(ors, off[v], EPI == kSkAdd ? ev[v] + (acc[v] + accm[v]) : (acc[v] + accm[v]) + ev[v]);
+	}
+}
+
 // ── Q6_K x fp32 ──
 
 // Token row t of x (K floats): s = 2^-e with max|x_t| in [2^e, 2^(e+1)),
@@ -557,6 +768,10 @@ int gemm_grid(int M, int N) {
 	return kXcds * ((tiles + kXcds - 1) / kXcds);
 }
 
+// Q4_K GEMM with K <= 3840: the resident-token-tile kernel (1) or the tiled
+// one (0); a launch-shape knob
+int g_q4_gemm_res = 1;
+
 int check_gemm(const char *what, int m, int n_out, int n_in, size_t row_bytes, const void *w) {
 	if (int rc = require_device()) return rc;
 	if (m <= 0 || n_out <= 0 || n_in <= 0 || n_in % kQK != 0)
@@ -569,6 +784,8 @@ int check_gemm(const char *what, int m, int n_out, int n_in, size_t row_bytes, c
 }
 
 }  // namespace
+
+void q4k_gemm_set_res(int v) { g_q4_gemm_res = v ? 1 : 0; }
 
 int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const float *bias, int m, int n_out,
              int n_in) {
@@ -602,6 +819,22 @@ int q4k_gemm_segs(const SkSegs &segs, int epi, const int8_t *xq, const float *xs
 		if (!tiled) return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM segment %d does not fit the 64-row tiles", i);
 	}
 	const int N = epi == kSkSwiGLU ? 2 * segs.s[0].rows : vrows;
+	if (g_q4_gemm_res && n_in <= kRMaxK) {
+		const int mt = (m + kRT - 1) / kRT;
+		const int R = cu_count() / mt > 1 ? cu_count() / mt : 1;
+		const int units = epi == kSkSwiGLU ? (segs.s[0].rows + 15) / 16 : (vrows + 31) / 32;
+		const int G = mt * R;
+		const dim3 rgrid(kXcds * ((G + kXcds - 1) / kXcds)), rblock(kRWaves * kWave);
+		const size_t lds = q4k_res_lds(n_in);
+		switch (epi) {
+		case kSkStore: hipLaunchKernelGGL(q4k_gemm_res_kernel<kSkStore>, rgrid, rblock, lds, stream(), segs, xq, xs, m, n_in, R, units); break;
+		case kSkAdd: hipLaunchKernelGGL(q4k_gemm_res_kernel<kSkAdd>, rgrid, rblock, lds, stream(), segs, xq, xs, m, n_in, R, units); break;
+		case kSkSwiGLU: hipLaunchKernelGGL(q4k_gemm_res_kernel<kSkSwiGLU>, rgrid, rblock, lds, stream(), segs, xq, xs, m, n_in, R, units); break;
+		default: return set_error(HAKO_GPU_EINVAL, "Q4_K GEMM epilogue %d", epi);
+		}
+		HK_LAUNCHED("q4k_gemm_res");
+		return ok();
+	}
 	const dim3 grid(gemm_grid(m, N));
 	const int gm = gemm_gm(m, N, (double)kTM * (n_in + n_in / 32 * 4), (double)kTN * (n_in / kQK) * kQ4Bytes);
 	switch (epi) {
