@@ -563,25 +563,53 @@ __device__ __forceinline__ uint32_t q6_pair(uint32_t v, uint32_t sel) {
 constexpr int kQ6Stage = 128;        // K per stage: half a super-block
 constexpr int kHPad = kQ6Stage + 8;  // fp16 per staged row (272 B: conflict-free 16-byte reads)
 
-__global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restrict__ w,
-                                                       const _Float16 *__restrict__ xh,
-                                                       const _Float16 *__restrict__ xl,
-                                                       const float *__restrict__ esc,
-                                                       const float *__restrict__ bias,
-                                                       float *__restrict__ y, int M, int N, int K, int add, int gm) {
-	__shared__ __align__(16) _Float16 ah_s[kTM * kHPad];   // activation hi [token][k]
-	__shared__ __align__(16) _Float16 al_s[kTM * kHPad];   // activation lo
-	__shared__ __align__(16) _Float16 wq_s[kTN * kHPad];   // q - 32 [row][k]
-	__shared__ __align__(16) float dsc_s[8][kTN];          // d*sc [group][row]
+// LDS of one stage buffer of a TN-row tile: activation hi and lo
+// [64][kHPad], q - 32 [TN][kHPad] (fp16), d*sc [8 groups][TN] (fp32).
+__host__ __device__ constexpr size_t q6g_buf_bytes(int tn) {
+	return (size_t)(2 * kTM + tn) * kHPad * 2 + (size_t)8 * tn * 4;
+}
 
-	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
+// Tile: 64 tokens x TN rows (64 or 128), one thread per (weight row,
+// quarter of a stage's bytes), waves of one 32 x 32 MFMA tile each (2 token
+// halves x TN/32 row quarters), so every output's arithmetic is the same at
+// both widths. TN = 64: two workgroups per CU, one LDS buffer, two barriers
+// per stage. TN = 128 (DB): one workgroup per CU with the stage buffers
+// double-buffered in LDS, one barrier per stage; a stage's activation then serves twice
+// the rows, so each output needs ~40% fewer staged bytes.
+template <int TN, bool DB>
+__global__ __launch_bounds__(4 * TN, DB ? 1 : 2) void q6k_gemm_kernel(const uint8_t *__restrict__ w,
+                                                                     const _Float16 *__restrict__ xh,
+                                                                     const _Float16 *__restrict__ xl,
+                                                                     const float *__restrict__ esc,
+                                                                     const float *__restrict__ bias,
+                                                                     float *__restrict__ y, int M, int N, int K,
+                                                                     int add, int gm) {
+	constexpr int T = 4 * TN;           // threads
+	constexpr int PA = kTM * 16 / T;    // activation pieces (16 B) per thread, hi and lo each
+	constexpr int RQ = TN / 32;         // row quarters (waves per token half)
+	extern __shared__ __align__(16) uint8_t q6g_lds[];
+	struct View {
+		_Float16 *ah, *al, *wq;
+		float *dsc;   // [8][TN]
+	};
+	auto view = [&](int b) -> View {
+		uint8_t *p = q6g_lds + (size_t)b * q6g_buf_bytes(TN);
+		View v;
+		v.ah = (_Float16 *)p;
+		v.al = v.ah + kTM * kHPad;
+		v.wq = v.al + kTM * kHPad;
+		v.dsc = (float *)(v.wq + TN * kHPad);
+		return v;
+	};
+
+	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + TN - 1) / TN;
 	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
 	if (tile >= mtiles * ntiles) return;
 	int mt, nt;
 	tile_mn(tile, ntiles, gm, mt, nt);
-	const int m0 = mt * kTM, n0 = nt * kTN;
+	const int m0 = mt * kTM, n0 = nt * TN;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-	const int wr = wave & 1, wt = wave >> 1, li = lane & 31, kh = lane >> 5;
+	const int wr = wave % RQ, wt = wave / RQ, li = lane & 31, kh = lane >> 5;
 	const int NB = K >> 8;
 	const uint32_t rb = (uint32_t)NB * kQ6Bytes;
 	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(w, rb * (uint32_t)N);
@@ -589,18 +617,16 @@ __global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restr
 	const __amdgpu_buffer_rsrc_t lrs = stream_rsrc(xl, (uint32_t)M * (uint32_t)K * 2u);
 
 	// Stage st = half n of block st/2. Activations: 64 tokens x 16 pieces of
-	// 16 B (8 fp16) for hi and lo, 4 + 4 per thread. Weights: thread (row
+	// 16 B (8 fp16) for hi and lo, PA + PA per thread. Weights: thread (row
 	// tid/4, part p = tid%4) takes ql[64n+16p, +16) — K 32(p/2)+16(p%2)+b
 	// (low nibbles) and that + 64 (high nibbles) of the half — with qh
 	// [32n+16(p%2), +16), and the scales 8n+2p, 8n+2p+1 and d.
 	const int wrow = tid >> 2, part = tid & 3;
 	// The activation loads of two stages are in flight while a third is
-	// computed: the workgroups per compute unit are bounded by LDS (two), not
-	// registers, so a second set of staging registers costs no occupancy,
-	// and one stage's arithmetic is too short to cover a load's latency by
-	// itself. The weight pieces (a sixth of the bytes) go one stage ahead.
+	// computed: one stage's arithmetic is too short to cover a load's latency
+	// by itself. The weight pieces (a sixth of the bytes) go one stage ahead.
 	struct Acts {
-		uint4 h[4], l[4];
+		uint4 h[PA], l[PA];
 	};
 	struct Wts {
 		uint2 ql[2], qh[2];
@@ -611,8 +637,8 @@ __global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restr
 	auto load_acts = [&](Acts &r, int st) {
 		const uint32_t k0 = (uint32_t)kQ6Stage * st;
 #pragma unroll
-		for (int u = 0; u < 4; u++) {
-			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
+		for (int u = 0; u < PA; u++) {
+			const int c = tid + T * u, tok = c >> 4, piece = c & 15;
 			const bool on = st < NSt && m0 + tok < M;
 			const uint32_t off = on ? 2u * ((uint32_t)(m0 + tok) * K + k0 + 8u * piece) : kBufNone;
 			r.h[u] = ld_b128(hrs, off);
@@ -631,15 +657,15 @@ __global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restr
 		r.sc = ld_b16(wrs, blk + 192u + 8u * n + 2u * part);
 		r.d = ld_b16(wrs, blk + 208u);
 	};
-	auto store_acts = [&](const Acts &r) {
+	auto store_acts = [&](const Acts &r, const View &v) {
 #pragma unroll
-		for (int u = 0; u < 4; u++) {
-			const int c = tid + kGT * u, tok = c >> 4, piece = c & 15;
-			*(uint4 *)(ah_s + tok * kHPad + 8 * piece) = r.h[u];
-			*(uint4 *)(al_s + tok * kHPad + 8 * piece) = r.l[u];
+		for (int u = 0; u < PA; u++) {
+			const int c = tid + T * u, tok = c >> 4, piece = c & 15;
+			*(uint4 *)(v.ah + tok * kHPad + 8 * piece) = r.h[u];
+			*(uint4 *)(v.al + tok * kHPad + 8 * piece) = r.l[u];
 		}
 	};
-	auto store_wts = [&](const Wts &r) {
+	auto store_wts = [&](const Wts &r, const View &v) {
 		// 6-bit values: low nibble | qh bits 2k1 (k1 = part/2) -> K 32k1 + l,
 		// high nibble | qh bits 2k1+4 -> K 32(k1+2) + l, with l = 16(part%2) + b.
 		const int k1 = part >> 1, l0 = 16 * (part & 1);
@@ -656,55 +682,86 @@ __global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restr
 			hi[2 * j] = q6_pair(vhi, 0x04010400u);
 			hi[2 * j + 1] = q6_pair(vhi, 0x04030402u);
 		}
-		uint8_t *wrow_s = (uint8_t *)(wq_s + wrow * kHPad);
+		uint8_t *wrow_s = (uint8_t *)(v.wq + wrow * kHPad);
 		*(uint4 *)(wrow_s + 2 * (32 * k1 + l0)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
 		*(uint4 *)(wrow_s + 2 * (32 * k1 + l0 + 8)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
 		*(uint4 *)(wrow_s + 2 * (32 * (k1 + 2) + l0)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
 		*(uint4 *)(wrow_s + 2 * (32 * (k1 + 2) + l0 + 8)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
 		// group gg = 2*part + i covers K [16gg, 16gg+16): scale 8n + gg
 		const float d = f16_to_f32(r.d);
-		dsc_s[2 * part][wrow] = d * (float)(int8_t)(r.sc & 0xFFu);
-		dsc_s[2 * part + 1][wrow] = d * (float)(int8_t)(r.sc >> 8);
+		v.dsc[(2 * part) * TN + wrow] = d * (float)(int8_t)(r.sc & 0xFFu);
+		v.dsc[(2 * part + 1) * TN + wrow] = d * (float)(int8_t)(r.sc >> 8);
 	};
 
 	v16f acc = {};
 	const v16f zero = {};
-	const _Float16 *ah = ah_s + (32 * wt + li) * kHPad + 8 * kh;
-	const _Float16 *al = al_s + (32 * wt + li) * kHPad + 8 * kh;
-	const _Float16 *wq = wq_s + (32 * wr + li) * kHPad + 8 * kh;
-	auto compute = [&]() {
+	auto compute = [&](const View &v) {
+		const _Float16 *ah = v.ah + (32 * wt + li) * kHPad + 8 * kh;
+		const _Float16 *al = v.al + (32 * wt + li) * kHPad + 8 * kh;
+		const _Float16 *wq = v.wq + (32 * wr + li) * kHPad + 8 * kh;
 #pragma unroll
 		for (int gg = 0; gg < 8; gg++) {
 			const v8h b = *(const v8h *)(wq + 16 * gg);
 			v16f p = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const v8h *)(ah + 16 * gg), b, zero, 0, 0, 0);
 			p = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const v8h *)(al + 16 * gg), b, p, 0, 0, 0);
-			const float s = dsc_s[gg][32 * wr + li];
+			const float s = v.dsc[gg * TN + 32 * wr + li];
 #pragma unroll
-			for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf(p[v], s, acc[v]);
+			for (int u = 0; u < 16; u++) acc[u] = __builtin_fmaf(p[u], s, acc[u]);
+			// DB: the operand reads of four groups at a time (all eight hoisted
+			// spill beside the second stage buffer's addresses)
+			if (DB && (gg & 3) == 3) __builtin_amdgcn_sched_barrier(0);
 		}
 	};
-	Acts aa, ab;
-	Wts wts;
-	load_acts(aa, 0);
-	load_wts(wts, 0);
-	load_acts(ab, 1);
-	// NSt is even: the loop takes the stages in pairs, so each activation
-	// register set is named statically
-	for (int st = 0; st < NSt; st += 2) {
-		store_acts(aa);
-		store_wts(wts);
-		__syncthreads();
-		load_wts(wts, st + 1);
-		load_acts(aa, st + 2);
-		compute();
-		__syncthreads();
-		store_acts(ab);
-		store_wts(wts);
-		__syncthreads();
-		load_wts(wts, st + 2);
-		load_acts(ab, st + 3);
-		compute();
-		__syncthreads();
+	const View v0 = view(0);
+	if constexpr (!DB) {
+		Acts aa, ab;
+		Wts wts;
+		load_acts(aa, 0);
+		load_wts(wts, 0);
+		load_acts(ab, 1);
+		// NSt is even: the loop takes the stages in pairs, so each activation
+		// register set is named statically
+		for (int st = 0; st < NSt; st += 2) {
+			store_acts(aa, v0);
+			store_wts(wts, v0);
+			__syncthreads();
+			load_wts(wts, st + 1);
+			load_acts(aa, st + 2);
+			compute(v0);
+			__syncthreads();
+			store_acts(ab, v0);
+			store_wts(wts, v0);
+			__syncthreads();
+			load_wts(wts, st + 2);
+			load_acts(ab, st + 3);
+			compute(v0);
+			__syncthreads();
+		}
+	} else {
+		// Stage st lives in LDS buffer st % 2. A wave stores stage st only
+		// after the barrier that followed the stores of stage st - 1, which
+		// every wave passes after computing stage st - 2, the buffer's last
+		// reader: one barrier per stage.
+		const View v1 = view(1);
+		Acts aa, ab;
+		Wts wts;
+		load_acts(aa, 0);
+		load_wts(wts, 0);
+		load_acts(ab, 1);
+		for (int st = 0; st < NSt; st += 2) {
+			store_acts(aa, v0);
+			store_wts(wts, v0);
+			__syncthreads();
+			load_wts(wts, st + 1);
+			load_acts(aa, st + 2);
+			compute(v0);
+			store_acts(ab, v1);
+			store_wts(wts, v1);
+			__syncthreads();
+			load_wts(wts, st + 2);
+			load_acts(ab, st + 3);
+			compute(v1);
+		}
 	}
 	// lane: row n0+32wr+li, tokens m0+32wt+8q4+4kh+r. Every operand load
 	// (token scales, bias, the output added to) first, then the stores;
@@ -719,17 +776,17 @@ __global__ __launch_bounds__(kGT, 2) void q6k_gemm_kernel(const uint8_t *__restr
 	uint32_t off[16];
 	float ev[16], ov[16];
 #pragma unroll
-	for (int v = 0; v < 16; v++) {
-		const int tok = m0 + 32 * wt + 8 * (v >> 2) + 4 * kh + (v & 3);
+	for (int u = 0; u < 16; u++) {
+		const int tok = m0 + 32 * wt + 8 * (u >> 2) + 4 * kh + (u & 3);
 		const bool ok = rok && tok < M;
-		off[v] = ok ? 4u * ((uint32_t)tok * N + row) : kBufNone;
-		ev[v] = ld_f32(ers, ok ? 4u * tok : kBufNone);
-		ov[v] = ld_f32(ars, off[v]);
+		off[u] = ok ? 4u * ((uint32_t)tok * N + row) : kBufNone;
+		ev[u] = ld_f32(ers, ok ? 4u * tok : kBufNone);
+		ov[u] = ld_f32(ars, off[u]);
 	}
 #pragma unroll
-	for (int v = 0; v < 16; v++) {
-		const float r = acc[v] * ev[v] + bv;
-		st_f32(yrs, off[v], add ? ov[v] + r : r);
+	for (int u = 0; u < 16; u++) {
+		const float r = acc[u] * ev[u] + bv;
+		st_f32(yrs, off[u], add ? ov[u] + r : r);
 	}
 }
 
@@ -746,8 +803,8 @@ int skinny_split_workspace(size_t floats, float **part) {
 // Token tiles per XCD group (tile_mn): the divisor of the token tiles that
 // minimizes what one XCD reads, gm token tiles of act_tile bytes each plus
 // its share of the row tiles of w_tile bytes each.
-int gemm_gm(int M, int N, double act_tile, double w_tile) {
-	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + kTN - 1) / kTN;
+int gemm_gm(int M, int N, double act_tile, double w_tile, int tn = kTN) {
+	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + tn - 1) / tn;
 	const double per = (double)mtiles * ntiles / kXcds;
 	int best = 1;
 	double best_bytes = 1e300;
@@ -763,14 +820,17 @@ int gemm_gm(int M, int N, double act_tile, double w_tile) {
 	return best;
 }
 
-int gemm_grid(int M, int N) {
-	const int tiles = ((M + kTM - 1) / kTM) * ((N + kTN - 1) / kTN);
+int gemm_grid(int M, int N, int tn = kTN) {
+	const int tiles = ((M + kTM - 1) / kTM) * ((N + tn - 1) / tn);
 	return kXcds * ((tiles + kXcds - 1) / kXcds);
 }
 
 // Q4_K GEMM with K <= 3840: the resident-token-tile kernel (1) or the tiled
 // one (0); a launch-shape knob
 int g_q4_gemm_res = 1;
+// Q6_K GEMM tile width: -1 by shape, else 64 or 128 rows (a launch-shape knob;
+// the outputs do not depend on it)
+int g_q6_gemm_tn = -1;
 
 int check_gemm(const char *what, int m, int n_out, int n_in, size_t row_bytes, const void *w) {
 	if (int rc = require_device()) return rc;
@@ -786,6 +846,7 @@ int check_gemm(const char *what, int m, int n_out, int n_in, size_t row_bytes, c
 }  // namespace
 
 void q4k_gemm_set_res(int v) { g_q4_gemm_res = v ? 1 : 0; }
+void q6k_gemm_set_tn(int v) { g_q6_gemm_tn = (v == 64 || v == 128) ? v : -1; }
 
 int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const float *bias, int m, int n_out,
              int n_in) {
@@ -881,9 +942,18 @@ int q6k_gemm_split(float *y, const void *w, const _Float16 *xh, const _Float16 *
                    const float *bias, int m, int n_out, int n_in, bool add) {
 	if (int rc = check_gemm("Q6_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ6Bytes, w)) return rc;
 	if (m <= kSkMaxTokens) return set_error(HAKO_GPU_EINVAL, "Q6_K GEMM on split rows needs m > %d", kSkMaxTokens);
-	const int gm = gemm_gm(m, n_out, (double)kTM * n_in * 4, (double)kTN * (n_in / kQK) * kQ6Bytes);
-	hipLaunchKernelGGL(q6k_gemm_kernel, dim3(gemm_grid(m, n_out)), dim3(kGT), 0, stream(), (const uint8_t *)w,
-	                   xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0, gm);
+	// 128-row tiles when they still give about one workgroup per CU
+	const int wide_tiles = ((m + kTM - 1) / kTM) * ((n_out + 127) / 128);
+	const bool wide = g_q6_gemm_tn == 128 || (g_q6_gemm_tn < 0 && 4 * wide_tiles >= 3 * cu_count());
+	const int tn = wide ? 128 : kTN;
+	const int gm = gemm_gm(m, n_out, (double)kTM * n_in * 4, (double)tn * (n_in / kQK) * kQ6Bytes, tn);
+	if (wide)
+		hipLaunchKernelGGL((q6k_gemm_kernel<128, true>), dim3(gemm_grid(m, n_out, 128)), dim3(4 * 128),
+		                   2 * q6g_buf_bytes(128), stream(), (const uint8_t *)w, xh, xl, esc, bias, y, m, n_out, n_in,
+		                   add ? 1 : 0, gm);
+	else
+		hipLaunchKernelGGL((q6k_gemm_kernel<kTN, false>), dim3(gemm_grid(m, n_out)), dim3(4 * kTN), q6g_buf_bytes(kTN),
+		                   stream(), (const uint8_t *)w, xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0, gm);
 	HK_LAUNCHED("q6k_gemm");
 	return ok();
 }

@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
 Q4, Q6 = synth.TYPE_Q4_K, synth.TYPE_Q6_K
+HAKO_TUNE_Q6K_GEMM_TN = 13   # include/hako_gpu.h
 
 
 def run_batch(gpu, qtype, w, x, n_out, n_in, bias=None):
@@ -163,6 +164,28 @@ def test_q4k_gemm_full_7b_shape_sampled_rows(gpu, oracle):
         assert maxabs_rel(got[t], gpu.download(do, np.float32, (n_out,))) < TOL
     for b in (dw, dx, do):
         b.free()
+
+
+@pytest.mark.parametrize("m,n_out,n_in", [(64, 128, 256), (130, 200, 2048), (77, 3648, 1024), (512, 384, 4608)])
+def test_q6k_gemm_tile_widths_agree_bit_exact(gpu, oracle, m, n_out, n_in):
+    """The 64-row and the 128-row (double-buffered) tiles do the same
+    arithmetic per output in the same order, so their outputs are
+    bit-identical, ragged token and row edges included; both within the bar
+    of the oracle."""
+    rng = np.random.default_rng(m + n_out + n_in)
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = rng.standard_normal((m, n_in)).astype(np.float32)
+    bias = 0.1 * rng.standard_normal(n_out).astype(np.float32)
+    got = {}
+    try:
+        for tn in (64, 128):
+            gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, tn)
+            got[tn] = run_batch(gpu, Q6, w, x, n_out, n_in, bias)
+    finally:
+        gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, 0)
+    assert np.array_equal(got[64].view(np.uint32), got[128].view(np.uint32))
+    want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True)
+    assert maxabs_rel(got[128], want) < TOL
 
 
 def test_q6k_gemm_full_7b_shape_sampled_rows(gpu, oracle):
