@@ -113,6 +113,90 @@ __device__ __forceinline__ float q6_dot(const Q6Buf &W, const Q6Col &col, int lh
 	return f16_to_f32(W.d) * ((s0 * acc[0] + s1 * acc[1]) + (s2 * acc[2] + s3 * acc[3]));
 }
 
+// The lane's activation columns as integers, for grids whose lanes keep one
+// chunk for many rows: group k (16 values, one scale group) scaled by its own
+// power of two 2^s[k] so that its largest magnitude lies in [2^21, 2^22),
+// rounded to integers D and split into three balanced signed bytes,
+// D = d0 + 256 d1 + 65536 d2, packed four to a dword per byte plane. A group's
+// sum over its 16 six-bit values is then three v_dot4_i32_i8 chains (exact in
+// int32), recombined in fp32 and scaled back by 2^-s[k]: ~2 vector ops per
+// weight against ~3 for the fp32 product per weight, the activation carried
+// to 2^-22 of its group's maximum (well inside the 1e-5 output tolerance).
+struct Q6Dig {
+	uint32_t d[4][3][4];   // [group k][byte plane][positions 4u .. 4u+3]
+	int s[4];
+	float nsx[4];          // -32 * sum of the group's fp32 values
+};
+
+// false when a group holds an inf or NaN (its sum is not finite): such a lane
+// keeps the fp32 path, which carries them as the reference does
+__device__ __forceinline__ bool q6_digits(const Q6Col &col, Q6Dig &g) {
+	bool ok = true;
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
+		float m = 0.0f;
+#pragma unroll
+		for (int j = 0; j < 16; j++) m = __builtin_fmaxf(m, __builtin_fabsf(col.xv[k][j]));
+		ok = ok && __builtin_isfinite(col.nsx[k]);
+		const int e = m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : 0;
+		const int sk = m > 0.0f ? 22 - e : 0;
+		g.s[k] = sk;
+		g.nsx[k] = col.nsx[k];
+		uint32_t b[3][16];
+#pragma unroll
+		for (int j = 0; j < 16; j++) {
+			const float v = __builtin_isfinite(col.xv[k][j]) ? col.xv[k][j] : 0.0f;
+			const int D = (int)__builtin_rintf(__builtin_ldexpf(v, sk));
+			const int d0 = (int)(int8_t)(D & 0xFF);
+			const int D1 = (D - d0) >> 8;
+			const int d1 = (int)(int8_t)(D1 & 0xFF);
+			const int D2 = (D1 - d1) >> 8;
+			b[0][j] = (uint32_t)D;
+			b[1][j] = (uint32_t)D1;
+			b[2][j] = (uint32_t)D2;
+		}
+#pragma unroll
+		for (int p = 0; p < 3; p++)
+#pragma unroll
+			for (int u = 0; u < 4; u++) {
+				const uint32_t lo = __builtin_amdgcn_perm(b[p][4 * u + 1], b[p][4 * u], 0x0c0c0400u);
+				const uint32_t hi = __builtin_amdgcn_perm(b[p][4 * u + 3], b[p][4 * u + 2], 0x0c0c0400u);
+				g.d[k][p][u] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+			}
+	}
+	return ok;
+}
+
+// q6_dot on the integer columns: d · Σ_k sc_k · (2^-s_k Σ_j q_k,j·D_k,j − 32·Σ_j x_k,j)
+__device__ __forceinline__ float q6_dot_dig(const Q6Buf &W, const Q6Dig &g, int lh) {
+	const uint32_t lo = 0x0F0F0F0Fu, hb = 0x30303030u;
+	const uint32_t qa[4] = {W.qa.x, W.qa.y, W.qa.z, W.qa.w}, qb[4] = {W.qb.x, W.qb.y, W.qb.z, W.qb.w};
+	const uint32_t qh[4] = {W.qh.x, W.qh.y, W.qh.z, W.qh.w};
+	int S[4][3] = {};
+#pragma unroll
+	for (int u = 0; u < 4; u++) {
+		uint32_t wk[4];
+		wk[0] = (qa[u] & lo) | ((qh[u] << 4) & hb);
+		wk[1] = (qb[u] & lo) | ((qh[u] << 2) & hb);
+		wk[2] = ((qa[u] >> 4) & lo) | (qh[u] & hb);
+		wk[3] = ((qb[u] >> 4) & lo) | ((qh[u] >> 2) & hb);
+#pragma unroll
+		for (int k = 0; k < 4; k++)
+#pragma unroll
+			for (int p = 0; p < 3; p++) S[k][p] = sdot4((int)wk[k], (int)g.d[k][p][u], S[k][p]);
+	}
+	float acc[4];
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
+		const float t = ((float)S[k][0] + 256.0f * (float)S[k][1]) + 65536.0f * (float)S[k][2];
+		acc[k] = __builtin_ldexpf(t, -g.s[k]) + g.nsx[k];
+	}
+	const int sh = 8 * lh;
+	const float s0 = (float)(int8_t)((W.s.x >> sh) & 0xFFu), s1 = (float)(int8_t)((W.s.x >> (sh + 16)) & 0xFFu);
+	const float s2 = (float)(int8_t)((W.s.y >> sh) & 0xFFu), s3 = (float)(int8_t)((W.s.y >> (sh + 16)) & 0xFFu);
+	return f16_to_f32(W.d) * ((s0 * acc[0] + s1 * acc[1]) + (s2 * acc[2] + s3 * acc[3]));
+}
+
 struct Q6Geom {
 	int C, seg, rt, tpr, rw, waves;
 };
@@ -137,7 +221,9 @@ __host__ __device__ inline Q6Geom q6_geom(int n_in, int target) {
 	return g;
 }
 
-// One workgroup: waves = parts x row-slices (see q6_geom).
+// One workgroup: waves = parts x row-slices (see q6_geom). DIG: the integer
+// columns (q6_digits) when every lane of the wave has finite activations.
+template <bool DIG>
 __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uint8_t *__restrict__ w,
                                                                        const float *__restrict__ x,
                                                                        const float *__restrict__ bias,
@@ -198,6 +284,12 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 		__builtin_amdgcn_sched_barrier(0);
 	}
 	q6_col_sums(col);   // waits for x only: it was loaded first
+	Q6Dig dg;
+	bool dig = false;
+	if (DIG) {
+		const bool ok = q6_digits(col, dg);
+		dig = __all(ok);
+	}
 
 	// Whole groups of kQ6Depth items (same load count every iteration; slots
 	// past nit load nothing). Their arithmetic is skipped by a wave-uniform
@@ -210,7 +302,7 @@ __global__ __launch_bounds__(kQ6MaxWaves * kWave) void q6k_gemv_kernel(const uin
 			const int row = item_row(it);
 			float d = 0.0f;
 			// Consume buf[j] in place, then reload it (no register rotation).
-			if (it < nit) d = q6_dot(buf[j], col, lh);
+			if (it < nit) d = dig ? q6_dot_dig(buf[j], dg, lh) : q6_dot(buf[j], col, lh);
 			issue(buf[j], it + kQ6Depth);
 			__builtin_amdgcn_sched_barrier(0);
 			rsum[j] = (lane_on && row < r1) ? d : 0.0f;
@@ -509,6 +601,8 @@ int g_q6_flat_items = -1;
 int g_q6_flat_seg = 0;
 // rows grid: 0 by shape, -1 never, else 10 * waves + depth (44, 82, 84, 162)
 int g_q6_rows = 0;
+// persistent grid: integer activation columns (1) or the fp32 product per weight (0)
+int g_q6_dig = 1;
 
 // Measured on MI355X (us per launch, persistent / flat with 1, 2, 4, 8
 // items): 2048x11008 (3 parts) 8.08 / 10.8 / 8.58 / 7.45 / 8.24; 1000x4608
@@ -531,6 +625,7 @@ int q6_flat_items_for(int n_out, const Q6Geom &G) {
 void q6k_set_wgs_per_cu(int v) { g_q6_wgs_per_cu = v < 1 ? 1 : (v > 8 ? 8 : v); }
 void q6k_set_waves(int v) { g_q6_waves = v >= 8 ? 8 : 4; }
 void q6k_set_rows(int v) { g_q6_rows = v; }
+void q6k_set_dig(int v) { g_q6_dig = v ? 1 : 0; }
 void q6k_set_flat_seg(int v) { g_q6_flat_seg = v == 32 || v == 64 ? v : 0; }
 void q6k_set_flat_items(int v) { g_q6_flat_items = v < 0 ? -1 : (v == 0 ? 0 : (v <= 1 ? 1 : (v <= 2 ? 2 : (v <= 4 ? 4 : 8)))); }
 
@@ -621,8 +716,12 @@ int q6k_gemv(float *out, const void *w, const float *x, const float *bias, int n
 	if ((n_out + wgs - 1) / wgs > max_rows_per_wg) wgs = (n_out + max_rows_per_wg - 1) / max_rows_per_wg;
 	const int rows_per_wg = (n_out + wgs - 1) / wgs;
 	const size_t lds = (size_t)rows_per_wg * G.tpr * sizeof(float);
-	hipLaunchKernelGGL(q6k_gemv_kernel, dim3(wgs), dim3(G.waves * kWave), lds, stream(), (const uint8_t *)w, x,
-	                   bias, res, out, n_out, n_in, g_q6_waves);
+	if (g_q6_dig)
+		hipLaunchKernelGGL(q6k_gemv_kernel<true>, dim3(wgs), dim3(G.waves * kWave), lds, stream(), (const uint8_t *)w,
+		                   x, bias, res, out, n_out, n_in, g_q6_waves);
+	else
+		hipLaunchKernelGGL(q6k_gemv_kernel<false>, dim3(wgs), dim3(G.waves * kWave), lds, stream(), (const uint8_t *)w,
+		                   x, bias, res, out, n_out, n_in, g_q6_waves);
 	HK_LAUNCHED("q6k_gemv");
 	return ok();
 }

@@ -31,6 +31,7 @@ void q6k_set_flat_seg(int v);
 void q6k_set_rows(int v);
 void q4k_set_flat_items(int v);
 void q4k_gemm_set_res(int v);
+void q6k_set_dig(int v);
 void q6k_gemm_set_tn(int v);
 // Target workgroups of the skinny (<= 16 token) launches (0: default).
 void q4k_skinny_set_target_wgs(int wgs);

@@ -271,7 +271,7 @@ def test_q6k_nan_propagates(gpu, n_out, n_in):
 
 
 HAKO_TUNE_Q6K_WGS_PER_CU, HAKO_TUNE_Q6K_WAVES, HAKO_TUNE_Q6K_FLAT_ITEMS = 2, 4, 8
-HAKO_TUNE_Q6K_FLAT_SEG, HAKO_TUNE_Q6K_ROWS = 10, 11
+HAKO_TUNE_Q6K_FLAT_SEG, HAKO_TUNE_Q6K_ROWS, HAKO_TUNE_Q6K_DIGITS = 10, 11, 14
 
 
 @pytest.mark.parametrize("n_out,n_in", [(2048, 11008), (300, 2048), (77, 18944), (100, 1792), (64, 512)])
@@ -280,7 +280,8 @@ def test_q6k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
     (1..8 row items per wave), with and without a bias: the lane work and the
     order of every addition are the same, so outputs are identical. (The rows
     grid, which wide rows take by default, adds in its own order: off here,
-    its own test below.)"""
+    its own test below; so do the persistent grid's integer columns, off here
+    and tested below.)"""
     rng = np.random.default_rng(n_out + 5 * n_in)
     w = synth.q6k_weight(rng, n_out, n_in)
     x = synth.activation(rng, n_in)
@@ -288,6 +289,7 @@ def test_q6k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
     dw, dx, db, do = gpu.upload(w), gpu.upload(x), gpu.upload(bias), gpu.alloc(n_out * 4)
     seen = {}
     gpu.tune(HAKO_TUNE_Q6K_ROWS, -1)
+    gpu.tune(HAKO_TUNE_Q6K_DIGITS, 0)
     try:
         for items, waves, wgs in ((-1, 4, 1), (0, 4, 1), (0, 8, 1), (0, 4, 2), (1, 4, 1), (2, 4, 1), (4, 4, 1),
                                   (8, 4, 1)):
@@ -307,10 +309,54 @@ def test_q6k_launch_shapes_agree_bit_exact(gpu, oracle, n_out, n_in):
         gpu.tune(HAKO_TUNE_Q6K_WAVES, 4)
         gpu.tune(HAKO_TUNE_Q6K_WGS_PER_CU, 1)
         gpu.tune(HAKO_TUNE_Q6K_ROWS, 0)
+        gpu.tune(HAKO_TUNE_Q6K_DIGITS, 1)
         for b in (dw, dx, db, do):
             b.free()
     want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True, threads=16)
     assert maxabs_rel(seen[False], want) < TOL
+
+
+@pytest.mark.parametrize("n_out,n_in", [(151936, 2048), (4000, 3584), (300, 2048), (40000, 768), (64, 512)])
+def test_q6k_integer_columns(gpu, oracle, n_out, n_in):
+    """The persistent grid's integer activation columns (each 16-value group
+    scaled by its own power of two and carried as three signed bytes) against
+    its fp32 product per weight and the oracle: within 2e-6 of the first, the
+    GEMV bar of the second; on activation blocks 1e-30 .. 1e30 apart with an
+    all-zero block; and with an inf in one group, which sends every wave
+    whose lanes hold it to the fp32 path: the same outputs (NaN, as the
+    reference gives them) either way."""
+    rng = np.random.default_rng(n_out + 7 * n_in)
+    nb = n_in // 256
+    w = synth.q6k_weight(rng, n_out, n_in)
+    x = synth.activation(rng, n_in)
+    xm = (x.reshape(nb, 256) * (np.float32(10.0) ** rng.integers(-30, 31, nb).astype(np.float32))[:, None])
+    xm = xm.astype(np.float32)
+    xm[0] = 0.0
+    xi = x.copy()
+    xi[n_in // 2 + 5] = np.inf
+    gpu.tune(HAKO_TUNE_Q6K_ROWS, -1)
+    gpu.tune(HAKO_TUNE_Q6K_FLAT_ITEMS, 0)
+    try:
+        for xv in (x, xm.reshape(-1)):
+            gpu.tune(HAKO_TUNE_Q6K_DIGITS, 0)
+            base = gpu_matmul(gpu, Q6, w, xv, n_out, n_in)
+            gpu.tune(HAKO_TUNE_Q6K_DIGITS, 1)
+            got = gpu_matmul(gpu, Q6, w, xv, n_out, n_in)
+            assert maxabs_rel(got, base) < 2e-6
+            if n_out <= 40000:
+                want = oracle.matmul(Q6, w, xv, n_out, n_in, f64=True, threads=16)
+                assert maxabs_rel(got, want) < TOL
+        gpu.tune(HAKO_TUNE_Q6K_DIGITS, 0)
+        base = gpu_matmul(gpu, Q6, w, xi, n_out, n_in)
+        gpu.tune(HAKO_TUNE_Q6K_DIGITS, 1)
+        got = gpu_matmul(gpu, Q6, w, xi, n_out, n_in)
+        assert np.array_equal(np.isnan(got), np.isnan(base)) and np.array_equal(np.isinf(got), np.isinf(base))
+        fin = np.isfinite(base)
+        assert np.array_equal(got[fin].view(np.uint32), base[fin].view(np.uint32))
+    finally:
+        gpu.tune(HAKO_TUNE_Q6K_ROWS, 0)
+        gpu.tune(HAKO_TUNE_Q6K_FLAT_ITEMS, -1)
+        gpu.tune(HAKO_TUNE_Q6K_DIGITS, 1)
 
 
 @pytest.mark.parametrize("n_out,n_in", [(77, 18944), (3584, 18944), (5, 32000), (300, 2048), (9, 4608)])
