@@ -499,7 +499,13 @@ __global__ __launch_bounds__(W * kWave) void q6k_rows_kernel(const uint8_t *__re
 		b.d = ld_b16(wr, v + 208);
 	};
 
-	// 1. the first D items' weights, the activation, this thread's row's residual and bias
+	// 1. the activation, the first D items' weights, this thread's row's
+	//    residual and bias. Staged rows load the activation first: after the
+	//    first workgroups of an XCD it comes from L2, so its LDS copy is
+	//    ready about when the first weights arrive (weights first left the
+	//    waves waiting on the staging with their weights in hand: 7B down
+	//    3584x18944 16.2 -> 15.3 us). One-pass rows keep it in registers
+	//    and load it after the weights.
 	Q6Buf buf[D];
 	int ti_i = 0, p_i = 0;
 	auto advance = [&](int &ti, int &p) {
@@ -508,14 +514,14 @@ __global__ __launch_bounds__(W * kWave) void q6k_rows_kernel(const uint8_t *__re
 			ti++;
 		}
 	};
-#pragma unroll
-	for (int j = 0; j < D; j++) {
-		issue(buf[j], ti_i, p_i);
-		advance(ti_i, p_i);
-		__builtin_amdgcn_sched_barrier(0);
-	}
 	Q6Col col;
 	if (XREG) {
+#pragma unroll
+		for (int j = 0; j < D; j++) {
+			issue(buf[j], ti_i, p_i);
+			advance(ti_i, p_i);
+			__builtin_amdgcn_sched_barrier(0);
+		}
 		q6_col_load(x, min(sub, C - 1), col);
 	} else {
 		// x as float4 f = t, t + T, ...: element 4f is j0..j0+3 of chunk c's run k
@@ -524,6 +530,13 @@ __global__ __launch_bounds__(W * kWave) void q6k_rows_kernel(const uint8_t *__re
 #pragma unroll
 		for (int u = 0; u < XS; u++)
 			xv4[u] = __builtin_bit_cast(float4, ld_b128(xr, (uint32_t)(threadIdx.x + u * T) * 16u));
+		__builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+		for (int j = 0; j < D; j++) {
+			issue(buf[j], ti_i, p_i);
+			advance(ti_i, p_i);
+			__builtin_amdgcn_sched_barrier(0);
+		}
 #pragma unroll
 		for (int u = 0; u < XS; u++) {
 			const int f = threadIdx.x + u * T;
