@@ -1235,6 +1235,8 @@ struct hako_gpu_decoder {
 	int8_t *pf_xq = nullptr;                    // q8 rows [chunk][max(d_model, ffn)] and their scales
 	float *pf_xs = nullptr, *pf_esc = nullptr;  // fp16 split of the SwiGLU rows: hi, lo [chunk][ffn], esc[chunk]
 	_Float16 *pf_xh = nullptr, *pf_xl = nullptr;
+	float *pf_sk = nullptr;   // stream-K slots of the down matmul
+	size_t pf_sk_floats = 0;
 	int *pf_tok = nullptr, *pf_pos = nullptr;
 	int pf_chunk = 0;   // most tokens per prefill pass
 	size_t pf_part_bytes = 0;   // capacity of pf_part
@@ -1754,6 +1756,8 @@ int prefill_alloc(hako_gpu_decoder *d) {
 	HK_ALLOC(d->pf_xh, 2 * C * F);
 	HK_ALLOC(d->pf_xl, 2 * C * F);
 	HK_ALLOC(d->pf_esc, 4 * C);
+	d->pf_sk_floats = q6k_gemm_sk_floats(q6k_gemm_sk_grid());
+	HK_ALLOC(d->pf_sk, 4 * d->pf_sk_floats);
 	HK_ALLOC(d->pf_tok, 4 * C);
 	HK_ALLOC(d->pf_pos, 4 * C);
 #undef HK_ALLOC
@@ -1864,7 +1868,8 @@ int prefill_chunk(hako_gpu_decoder *d, int seq, const int *tokens, int n, int po
 		// down + residual: h = pf_g
 		if (n > kSkMaxTokens && B.t_down == HAKO_TYPE_Q6_K) {
 			if (int rc = f16_split(d->pf_g, d->pf_xh, d->pf_xl, d->pf_esc, n, F)) return rc;
-			if (int rc = q6k_gemm_split(d->pf_x, B.down, d->pf_xh, d->pf_xl, d->pf_esc, nullptr, n, D, F, true))
+			if (int rc = q6k_gemm_split(d->pf_x, B.down, d->pf_xh, d->pf_xl, d->pf_esc, nullptr, n, D, F, true, d->pf_sk,
+			                             d->pf_sk_floats))
 				return rc;
 		} else if (n > kSkMaxTokens && B.t_down == HAKO_TYPE_Q4_K) {
 			if (int rc = hako_gpu_quantize_q8_32(d->pf_g, n, F, d->pf_xq, d->pf_xs)) return rc;

@@ -576,14 +576,56 @@ __host__ __device__ constexpr size_t q6g_buf_bytes(int tn) {
 // per stage. TN = 128 (DB): one workgroup per CU with the stage buffers
 // double-buffered in LDS, one barrier per stage; a stage's activation then serves twice
 // the rows, so each output needs ~40% fewer staged bytes.
-template <int TN, bool DB>
+//
+// Epilogue of a 32 x 32 MFMA tile: lane (li, kh) of wave (wr, wt) holds
+// row n0+32wr+li, tokens m0+32wt+8q4+4kh+r. Every operand load (token
+// scales, bias, the output added to) first, then the stores; lanes past the
+// rows or tokens use an offset past the stream.
+__device__ __forceinline__ void q6g_epilogue(const v16f &acc, int m0, int n0, int wr, int wt, int li, int kh, int M,
+                                             int N, float *y, const float *esc, const float *bias, int add) {
+	const int row = n0 + 32 * wr + li;
+	const bool rok = row < N;
+	const __amdgpu_buffer_rsrc_t yrs = stream_rsrc(y, (uint32_t)M * (uint32_t)N * 4u);
+	const __amdgpu_buffer_rsrc_t ars = stream_rsrc(y, add ? (uint32_t)M * (uint32_t)N * 4u : 0u);
+	const __amdgpu_buffer_rsrc_t ers = stream_rsrc(esc, (uint32_t)M * 4u);
+	const __amdgpu_buffer_rsrc_t brs = stream_rsrc(bias ? (const void *)bias : (const void *)esc, bias ? (uint32_t)N * 4u : 0u);
+	const float bv = ld_f32(brs, rok ? 4u * row : kBufNone);
+	uint32_t off[16];
+	float ev[16], ov[16];
+#pragma unroll
+	for (int u = 0; u < 16; u++) {
+		const int tok = m0 + 32 * wt + 8 * (u >> 2) + 4 * kh + (u & 3);
+		const bool ok = rok && tok < M;
+		off[u] = ok ? 4u * ((uint32_t)tok * N + row) : kBufNone;
+		ev[u] = ld_f32(ers, ok ? 4u * tok : kBufNone);
+		ov[u] = ld_f32(ars, off[u]);
+	}
+#pragma unroll
+	for (int u = 0; u < 16; u++) {
+		const float r = acc[u] * ev[u] + bv;
+		st_f32(yrs, off[u], add ? ov[u] + r : r);
+	}
+}
+
+//
+// SK (stream-K, with DB): the grid's G workgroups split the launch's
+// tiles x super-blocks evenly, workgroup v (its place in the XCD-contiguous
+// order) taking units [v·U/G, (v+1)·U/G) of the U = tiles·NB in tile order.
+// A range shorter than a tile meets at most two tiles; the workgroup leaves
+// each tile's sums, unscaled, in its slot v·2 + (first tile ? 0 : 1) of
+// `skp` (the thread's 16 sums side by side), and q6k_gemm_sk_fixup_kernel
+// adds a tile's slots in workgroup order and applies the epilogue. With 224
+// tiles of 128 rows on 256 CUs (7B down over 512 tokens) every CU works
+// instead of 7 in 8.
+template <int TN, bool DB, bool SK = false>
 __global__ __launch_bounds__(4 * TN, DB ? 1 : 2) void q6k_gemm_kernel(const uint8_t *__restrict__ w,
                                                                      const _Float16 *__restrict__ xh,
                                                                      const _Float16 *__restrict__ xl,
                                                                      const float *__restrict__ esc,
                                                                      const float *__restrict__ bias,
                                                                      float *__restrict__ y, int M, int N, int K,
-                                                                     int add, int gm) {
+                                                                     int add, int gm, float *__restrict__ skp) {
+	static_assert(!SK || DB, "stream-K runs the double-buffered tiles");
 	constexpr int T = 4 * TN;           // threads
 	constexpr int PA = kTM * 16 / T;    // activation pieces (16 B) per thread, hi and lo each
 	constexpr int RQ = TN / 32;         // row quarters (waves per token half)
@@ -603,14 +645,26 @@ __global__ __launch_bounds__(4 * TN, DB ? 1 : 2) void q6k_gemm_kernel(const uint
 	};
 
 	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + TN - 1) / TN;
-	const int tile = xcd_tile(blockIdx.x, mtiles * ntiles);
-	if (tile >= mtiles * ntiles) return;
+	const int NB = K >> 8;
+	// SK: this workgroup's units (super-blocks of tiles in tile order)
+	int64_t u_beg = 0, u_end = 0;
+	int tile, vpos = 0;
+	if constexpr (SK) {
+		vpos = xcd_tile(blockIdx.x, gridDim.x);
+		const int64_t U = (int64_t)mtiles * ntiles * NB;
+		u_beg = (int64_t)vpos * U / gridDim.x;
+		u_end = (int64_t)(vpos + 1) * U / gridDim.x;
+		if (u_end <= u_beg) return;
+		tile = (int)(u_beg / NB);
+	} else {
+		tile = xcd_tile(blockIdx.x, mtiles * ntiles);
+		if (tile >= mtiles * ntiles) return;
+	}
 	int mt, nt;
 	tile_mn(tile, ntiles, gm, mt, nt);
-	const int m0 = mt * kTM, n0 = nt * TN;
+	int m0 = mt * kTM, n0 = nt * TN;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int wr = wave % RQ, wt = wave / RQ, li = lane & 31, kh = lane >> 5;
-	const int NB = K >> 8;
 	const uint32_t rb = (uint32_t)NB * kQ6Bytes;
 	const __amdgpu_buffer_rsrc_t wrs = stream_rsrc(w, rb * (uint32_t)N);
 	const __amdgpu_buffer_rsrc_t hrs = stream_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
@@ -633,13 +687,14 @@ __global__ __launch_bounds__(4 * TN, DB ? 1 : 2) void q6k_gemm_kernel(const uint
 		uint32_t sc, d;
 	};
 	const int NSt = NB * 2;
+	int s_end = NSt;   // stages past it load nothing
 	// unconditional: a stage past the last loads nothing (out-of-range offsets)
 	auto load_acts = [&](Acts &r, int st) {
 		const uint32_t k0 = (uint32_t)kQ6Stage * st;
 #pragma unroll
 		for (int u = 0; u < PA; u++) {
 			const int c = tid + T * u, tok = c >> 4, piece = c & 15;
-			const bool on = st < NSt && m0 + tok < M;
+			const bool on = st < s_end && m0 + tok < M;
 			const uint32_t off = on ? 2u * ((uint32_t)(m0 + tok) * K + k0 + 8u * piece) : kBufNone;
 			r.h[u] = ld_b128(hrs, off);
 			r.l[u] = ld_b128(lrs, off);
@@ -647,7 +702,7 @@ __global__ __launch_bounds__(4 * TN, DB ? 1 : 2) void q6k_gemm_kernel(const uint
 	};
 	auto load_wts = [&](Wts &r, int st) {
 		const int kb = st >> 1, n = st & 1;
-		const bool on = st < NSt && n0 + wrow < N;
+		const bool on = st < s_end && n0 + wrow < N;
 		const uint32_t blk = on ? (uint32_t)(n0 + wrow) * rb + (uint32_t)kb * kQ6Bytes : kBufNone;
 		const uint32_t oql = 64u * n + 16u * part, oqh = 128u + 32u * n + 16u * (part & 1);
 		r.ql[0] = ld_b64(wrs, blk + oql);
@@ -745,49 +800,91 @@ __global__ __launch_bounds__(4 * TN, DB ? 1 : 2) void q6k_gemm_kernel(const uint
 		const View v1 = view(1);
 		Acts aa, ab;
 		Wts wts;
-		load_acts(aa, 0);
-		load_wts(wts, 0);
-		load_acts(ab, 1);
-		for (int st = 0; st < NSt; st += 2) {
-			store_acts(aa, v0);
-			store_wts(wts, v0);
-			__syncthreads();
-			load_wts(wts, st + 1);
-			load_acts(aa, st + 2);
-			compute(v0);
-			store_acts(ab, v1);
-			store_wts(wts, v1);
-			__syncthreads();
-			load_wts(wts, st + 2);
-			load_acts(ab, st + 3);
-			compute(v1);
+		// stages [sa, sb) of the current tile
+		auto pipeline = [&](int sa, int sb) {
+			s_end = sb;
+			load_acts(aa, sa);
+			load_wts(wts, sa);
+			load_acts(ab, sa + 1);
+			for (int st = sa; st < sb; st += 2) {
+				store_acts(aa, v0);
+				store_wts(wts, v0);
+				__syncthreads();
+				load_wts(wts, st + 1);
+				load_acts(aa, st + 2);
+				compute(v0);
+				store_acts(ab, v1);
+				store_wts(wts, v1);
+				__syncthreads();
+				load_wts(wts, st + 2);
+				load_acts(ab, st + 3);
+				compute(v1);
+			}
+		};
+		if constexpr (SK) {
+			// one or two tiles: each piece's sums to its slot, then the next
+			// tile (the buffers' last readers passed a barrier since: v0 was
+			// read before the barrier that followed the stores of v1, and v1
+			// is next written after the barrier that follows those of v0)
+			const int first = tile;
+			for (;;) {
+				const int64_t t0u = (int64_t)tile * NB;
+				const int ka = (int)(u_beg > t0u ? u_beg - t0u : 0);
+				const int kb = (int)(u_end < t0u + NB ? u_end - t0u : NB);
+				pipeline(2 * ka, 2 * kb);
+				float4 *dst = (float4 *)(skp + ((size_t)(2 * vpos + (tile == first ? 0 : 1)) * T + tid) * 16);
+#pragma unroll
+				for (int q = 0; q < 4; q++) dst[q] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+				if (t0u + NB >= u_end) return;
+				acc = zero;
+				tile++;
+				tile_mn(tile, ntiles, gm, mt, nt);
+				m0 = mt * kTM;
+				n0 = nt * TN;
+			}
+		} else {
+			pipeline(0, NSt);
 		}
 	}
-	// lane: row n0+32wr+li, tokens m0+32wt+8q4+4kh+r. Every operand load
-	// (token scales, bias, the output added to) first, then the stores;
-	// lanes past the rows or tokens use an offset past the stream
-	const int row = n0 + 32 * wr + li;
-	const bool rok = row < N;
-	const __amdgpu_buffer_rsrc_t yrs = stream_rsrc(y, (uint32_t)M * (uint32_t)N * 4u);
-	const __amdgpu_buffer_rsrc_t ars = stream_rsrc(y, add ? (uint32_t)M * (uint32_t)N * 4u : 0u);
-	const __amdgpu_buffer_rsrc_t ers = stream_rsrc(esc, (uint32_t)M * 4u);
-	const __amdgpu_buffer_rsrc_t brs = stream_rsrc(bias ? (const void *)bias : (const void *)esc, bias ? (uint32_t)N * 4u : 0u);
-	const float bv = ld_f32(brs, rok ? 4u * row : kBufNone);
-	uint32_t off[16];
-	float ev[16], ov[16];
+	q6g_epilogue(acc, m0, n0, wr, wt, li, kh, M, N, y, esc, bias, add);
+}
+
+// Sums of the stream-K pieces of tile blockIdx.x (q6k_gemm_kernel<128, true,
+// true>: same threads, same slots), added in workgroup order, that is in
+// order of K, and the GEMM's epilogue.
+__global__ __launch_bounds__(512) void q6k_gemm_sk_fixup_kernel(const float *__restrict__ skp,
+                                                                const float *__restrict__ esc,
+                                                                const float *__restrict__ bias, float *__restrict__ y,
+                                                                int M, int N, int NB, int G, int gm, int add) {
+	constexpr int TN = 128, T = 4 * TN, RQ = TN / 32;
+	const int mtiles = (M + kTM - 1) / kTM, ntiles = (N + TN - 1) / TN;
+	const int tile = blockIdx.x;
+	const int64_t U = (int64_t)mtiles * ntiles * NB;
+	auto start = [&](int v) -> int64_t { return (int64_t)v * U / G; };
+	const int64_t a = (int64_t)tile * NB, b = a + NB;
+	int v = (int)(a * G / U);   // the workgroup holding unit a
+	while (start(v + 1) <= a) v++;
+	while (v > 0 && start(v) > a) v--;
+	const int tid = threadIdx.x;
+	v16f acc = {};
+	for (; v < G && start(v) < b; v++) {
+		const int64_t s0 = start(v), s1 = start(v + 1);
+		if (s1 <= s0 || s1 <= a) continue;
+		const int which = s0 / NB == tile ? 0 : 1;   // the tile is the workgroup's first or second
+		const float4 *src = (const float4 *)(skp + ((size_t)(2 * v + which) * T + tid) * 16);
 #pragma unroll
-	for (int u = 0; u < 16; u++) {
-		const int tok = m0 + 32 * wt + 8 * (u >> 2) + 4 * kh + (u & 3);
-		const bool ok = rok && tok < M;
-		off[u] = ok ? 4u * ((uint32_t)tok * N + row) : kBufNone;
-		ev[u] = ld_f32(ers, ok ? 4u * tok : kBufNone);
-		ov[u] = ld_f32(ars, off[u]);
+		for (int q = 0; q < 4; q++) {
+			const float4 t = src[q];
+			acc[4 * q] += t.x;
+			acc[4 * q + 1] += t.y;
+			acc[4 * q + 2] += t.z;
+			acc[4 * q + 3] += t.w;
+		}
 	}
-#pragma unroll
-	for (int u = 0; u < 16; u++) {
-		const float r = acc[u] * ev[u] + bv;
-		st_f32(yrs, off[u], add ? ov[u] + r : r);
-	}
+	int mt, nt;
+	tile_mn(tile, ntiles, gm, mt, nt);
+	const int lane = tid & 63, wave = tid >> 6;
+	q6g_epilogue(acc, mt * kTM, nt * TN, wave % RQ, wave / RQ, lane & 31, lane >> 5, M, N, y, esc, bias, add);
 }
 
 // Split-K partials of the skinny matmuls (workspace slot 5).
@@ -831,6 +928,14 @@ int g_q4_gemm_res = 1;
 // Q6_K GEMM tile width: -1 by shape, else 64 or 128 rows (a launch-shape knob;
 // the outputs do not depend on it)
 int g_q6_gemm_tn = -1;
+// Stream-K for 128-row tile counts below the workgroups of one round: in the
+// decoder's prompt pass (1), there and in the standalone matmul entry points
+// (2), or never (0). Measured on 512x3584x18944: inside the 7B prompt pass
+// the stream-K kernel and its fixup took 243.8 + 7.0 us against 263.7 us for
+// whole tiles (the pass 18.45 -> 18.12 ms); the same launch repeated back to
+// back, the chip's power limit holding its clocks, 270 against 258 us (with
+// a 3 ms pause before each launch 288 against 300 us).
+int g_q6_gemm_sk = 1;
 
 int check_gemm(const char *what, int m, int n_out, int n_in, size_t row_bytes, const void *w) {
 	if (int rc = require_device()) return rc;
@@ -847,6 +952,7 @@ int check_gemm(const char *what, int m, int n_out, int n_in, size_t row_bytes, c
 
 void q4k_gemm_set_res(int v) { g_q4_gemm_res = v ? 1 : 0; }
 void q6k_gemm_set_tn(int v) { g_q6_gemm_tn = (v == 64 || v == 128) ? v : -1; }
+void q6k_gemm_set_sk(int v) { g_q6_gemm_sk = v < 0 ? 0 : (v > 2 ? 2 : v); }
 
 int q4k_gemm(float *y, const void *w, const int8_t *xq, const float *xs, const float *bias, int m, int n_out,
              int n_in) {
@@ -935,11 +1041,23 @@ int q6k_gemm(float *y, const void *w, const float *x, const float *bias, int m, 
 		if (int rc = q6k_skinny(segs, kSkStore, xh, xl, esc, m, n_in, n_out, part, pf)) return rc;
 		return ok();
 	}
-	return q6k_gemm_split(y, w, xh, xl, esc, bias, m, n_out, n_in, false);
+	float *skp = nullptr;
+	size_t skf = 0;
+	if (g_q6_gemm_sk == 2) {   // stream-K slots (workspace slot 6)
+		skf = q6k_gemm_sk_floats(q6k_gemm_sk_grid());
+		void *p = nullptr;
+		if (int rc = workspace(6, skf * 4, &p)) return rc;
+		skp = (float *)p;
+	}
+	return q6k_gemm_split(y, w, xh, xl, esc, bias, m, n_out, n_in, false, skp, skf);
 }
 
+// The stream-K slots of a launch on G workgroups (floats).
+size_t q6k_gemm_sk_floats(int G) { return (size_t)G * 2 * 512 * 16; }
+int q6k_gemm_sk_grid() { return cu_count() / kXcds * kXcds; }
+
 int q6k_gemm_split(float *y, const void *w, const _Float16 *xh, const _Float16 *xl, const float *esc,
-                   const float *bias, int m, int n_out, int n_in, bool add) {
+                   const float *bias, int m, int n_out, int n_in, bool add, float *skp, size_t skp_floats) {
 	if (int rc = check_gemm("Q6_K GEMM", m, n_out, n_in, (size_t)n_in / kQK * kQ6Bytes, w)) return rc;
 	if (m <= kSkMaxTokens) return set_error(HAKO_GPU_EINVAL, "Q6_K GEMM on split rows needs m > %d", kSkMaxTokens);
 	// 128-row tiles when they still give about one workgroup per CU
@@ -947,13 +1065,26 @@ int q6k_gemm_split(float *y, const void *w, const _Float16 *xh, const _Float16 *
 	const bool wide = g_q6_gemm_tn == 128 || (g_q6_gemm_tn < 0 && 4 * wide_tiles >= 3 * cu_count());
 	const int tn = wide ? 128 : kTN;
 	const int gm = gemm_gm(m, n_out, (double)kTM * n_in * 4, (double)tn * (n_in / kQK) * kQ6Bytes, tn);
+	// stream-K when the 128-row tiles leave CUs idle and the caller holds the slots
+	const int G = q6k_gemm_sk_grid();
+	const bool sk = wide && g_q6_gemm_sk && skp && skp_floats >= q6k_gemm_sk_floats(G) && wide_tiles < G &&
+	                n_in / kQK >= 2;
+	if (sk) {
+		hipLaunchKernelGGL((q6k_gemm_kernel<128, true, true>), dim3(G), dim3(4 * 128), 2 * q6g_buf_bytes(128), stream(),
+		                   (const uint8_t *)w, xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0, gm, skp);
+		HK_LAUNCHED("q6k_gemm");
+		hipLaunchKernelGGL(q6k_gemm_sk_fixup_kernel, dim3(wide_tiles), dim3(512), 0, stream(), skp, esc, bias, y, m,
+		                   n_out, n_in / kQK, G, gm, add ? 1 : 0);
+		HK_LAUNCHED("q6k_gemm_sk_fixup");
+		return ok();
+	}
 	if (wide)
 		hipLaunchKernelGGL((q6k_gemm_kernel<128, true>), dim3(gemm_grid(m, n_out, 128)), dim3(4 * 128),
 		                   2 * q6g_buf_bytes(128), stream(), (const uint8_t *)w, xh, xl, esc, bias, y, m, n_out, n_in,
-		                   add ? 1 : 0, gm);
+		                   add ? 1 : 0, gm, nullptr);
 	else
 		hipLaunchKernelGGL((q6k_gemm_kernel<kTN, false>), dim3(gemm_grid(m, n_out)), dim3(4 * kTN), q6g_buf_bytes(kTN),
-		                   stream(), (const uint8_t *)w, xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0, gm);
+		                   stream(), (const uint8_t *)w, xh, xl, esc, bias, y, m, n_out, n_in, add ? 1 : 0, gm, nullptr);
 	HK_LAUNCHED("q6k_gemm");
 	return ok();
 }

@@ -33,6 +33,7 @@ void q4k_set_flat_items(int v);
 void q4k_gemm_set_res(int v);
 void q6k_set_dig(int v);
 void q6k_gemm_set_tn(int v);
+void q6k_gemm_set_sk(int v);
 // Target workgroups of the skinny (<= 16 token) launches (0: default).
 void q4k_skinny_set_target_wgs(int wgs);
 void q6k_skinny_set_target_wgs(int wgs);

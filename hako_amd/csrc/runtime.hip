@@ -173,6 +173,7 @@ int hako_gpu_tune(int knob, int value) {
 	case HAKO_TUNE_Q4K_GEMM_RES: q4k_gemm_set_res(value); return ok();
 	case HAKO_TUNE_Q6K_GEMM_TN: q6k_gemm_set_tn(value); return ok();
 	case HAKO_TUNE_Q6K_DIGITS: q6k_set_dig(value); return ok();
+	case HAKO_TUNE_Q6K_GEMM_SK: q6k_gemm_set_sk(value); return ok();
 	case HAKO_TUNE_SKINNY_Q4K_WGS: q4k_skinny_set_target_wgs(value); return ok();
 	case HAKO_TUNE_SKINNY_Q6K_WGS: q6k_skinny_set_target_wgs(value); return ok();
 	case HAKO_TUNE_DEC_GU_ITEMS: dec_set_gu_items(value); return ok();

@@ -68,7 +68,13 @@ int f16_split(const float *x, _Float16 *xh, _Float16 *xl, float *esc, int m, int
 int q4k_gemm_segs(const SkSegs &segs, int epi, const int8_t *xq, const float *xs, int m, int n_in, int vrows);
 // Q6_K x the fp16 hi/lo rows of f16_split: y[m][n_out] = (or += when add)
 // W x (+ bias).
+// skp: stream-K slots of q6k_gemm_sk_floats(q6k_gemm_sk_grid()) floats, or
+// null (then no stream-K); the launch uses them only when its 128-row tiles
+// would leave CUs idle.
 int q6k_gemm_split(float *y, const void *w, const _Float16 *xh, const _Float16 *xl, const float *esc,
-                   const float *bias, int m, int n_out, int n_in, bool add);
+                   const float *bias, int m, int n_out, int n_in, bool add, float *skp = nullptr,
+                   size_t skp_floats = 0);
+size_t q6k_gemm_sk_floats(int G);
+int q6k_gemm_sk_grid();
 
 }  // namespace hako

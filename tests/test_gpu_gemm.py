@@ -16,6 +16,7 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-5
 Q4, Q6 = synth.TYPE_Q4_K, synth.TYPE_Q6_K
 HAKO_TUNE_Q6K_GEMM_TN = 13   # include/hako_gpu.h
+HAKO_TUNE_Q6K_GEMM_SK = 15
 
 
 def run_batch(gpu, qtype, w, x, n_out, n_in, bias=None):
@@ -171,21 +172,52 @@ def test_q6k_gemm_tile_widths_agree_bit_exact(gpu, oracle, m, n_out, n_in):
     """The 64-row and the 128-row (double-buffered) tiles do the same
     arithmetic per output in the same order, so their outputs are
     bit-identical, ragged token and row edges included; both within the bar
-    of the oracle."""
+    of the oracle. (Stream-K, which adds a tile's K pieces after the fact,
+    is off here and tested below.)"""
     rng = np.random.default_rng(m + n_out + n_in)
     w = synth.q6k_weight(rng, n_out, n_in)
     x = rng.standard_normal((m, n_in)).astype(np.float32)
     bias = 0.1 * rng.standard_normal(n_out).astype(np.float32)
     got = {}
+    gpu.tune(HAKO_TUNE_Q6K_GEMM_SK, 0)   # (the standalone call's default leaves it off too)
     try:
         for tn in (64, 128):
             gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, tn)
             got[tn] = run_batch(gpu, Q6, w, x, n_out, n_in, bias)
     finally:
         gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, 0)
+        gpu.tune(HAKO_TUNE_Q6K_GEMM_SK, 1)
     assert np.array_equal(got[64].view(np.uint32), got[128].view(np.uint32))
     want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True)
     assert maxabs_rel(got[128], want) < TOL
+
+
+@pytest.mark.parametrize("m,n_out,n_in", [(130, 200, 2048), (77, 3648, 1024), (512, 384, 4608), (64, 128, 512),
+                                         (512, 3584, 4608)])
+def test_q6k_gemm_stream_k(gpu, oracle, m, n_out, n_in):
+    """128-row tiles in stream-K form (every CU takes an equal share of the
+    tiles' super-blocks; a tile's pieces meet in a second launch, in order of
+    K) against the same tiles whole: within 1e-6, and the GEMM bar of the
+    oracle. The shapes give tiles held by one to several workgroups, pieces
+    of one super-block, ragged token and row edges; twice in a row, the
+    second call on other inputs, so no stale slot passes."""
+    rng = np.random.default_rng(3 * m + n_out + n_in)
+    w = synth.q6k_weight(rng, n_out, n_in)
+    bias = 0.1 * rng.standard_normal(n_out).astype(np.float32)
+    gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, 128)
+    try:
+        for call in range(2):
+            x = rng.standard_normal((m, n_in)).astype(np.float32) * (1.0 + 9.0 * call)
+            gpu.tune(HAKO_TUNE_Q6K_GEMM_SK, 0)
+            whole = run_batch(gpu, Q6, w, x, n_out, n_in, bias)
+            gpu.tune(HAKO_TUNE_Q6K_GEMM_SK, 2)
+            got = run_batch(gpu, Q6, w, x, n_out, n_in, bias)
+            assert maxabs_rel(got, whole) < 1e-6
+            want = oracle.matmul(Q6, w, x, n_out, n_in, bias=bias, f64=True)
+            assert maxabs_rel(got, want) < TOL
+    finally:
+        gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, 0)
+        gpu.tune(HAKO_TUNE_Q6K_GEMM_SK, 1)
 
 
 def test_q6k_gemm_full_7b_shape_sampled_rows(gpu, oracle):
