@@ -611,7 +611,8 @@ __device__ __forceinline__ void q6g_epilogue(const v16f &acc, int m0, int n0, in
 // SK (stream-K, with DB): the grid's G workgroups split the launch's
 // tiles x super-blocks evenly, workgroup v (its place in the XCD-contiguous
 // order) taking units [v·U/G, (v+1)·U/G) of the U = tiles·NB in tile order.
-// A range shorter than a tile meets at most two tiles; the workgroup leaves
+// (Used when tiles < G, so a range is no longer than a tile and meets at
+// most two tiles.) The workgroup leaves
 // each tile's sums, unscaled, in its slot v·2 + (first tile ? 0 : 1) of
 // `skp` (the thread's 16 sums side by side), and q6k_gemm_sk_fixup_kernel
 // adds a tile's slots in workgroup order and applies the epilogue. With 224

@@ -128,8 +128,9 @@ struct Q6Dig {
 	float nsx[4];          // -32 * sum of the group's fp32 values
 };
 
-// false when a group holds an inf or NaN (its sum is not finite): such a lane
-// keeps the fp32 path, which carries them as the reference does
+// false when a group holds an inf or NaN (its sum is not finite): the wave
+// then keeps the fp32 path for all its lanes, which carries them as the
+// reference does
 __device__ __forceinline__ bool q6_digits(const Q6Col &col, Q6Dig &g) {
 	bool ok = true;
 #pragma unroll
