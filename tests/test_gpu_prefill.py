@@ -167,6 +167,52 @@ def test_prefill_matches_reference_feed(gpu, ref, tmp_path, cfg, seed, n_prompt,
     assert got == want
 
 
+HAKO_TUNE_Q6K_GEMM_TN, HAKO_TUNE_Q6K_GEMM_SK = 13, 15
+
+
+def test_prefill_stream_k_down_matches_reference_feed(gpu, ref, tmp_path):
+    """The down projection's Q6_K GEMM in its stream-K form inside the prompt
+    pass (128-row tiles forced: 3 x 8 tiles of 11 super-blocks over the
+    grid, so every tile's K is split over many workgroups and the fixup adds
+    the pieces into the residual) against whole tiles and the reference's
+    feed: the same greedy tokens, K/V rows and logits within the bars of the
+    SMALL_128 case above."""
+    cfg, seed, n_prompt, max_seq = SMALL_128, 21, 140, 384
+    path = str(tmp_path / "m.mlf2")
+    mlf2.write_qwen2(path, cfg, seed)
+    steps = 6
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    r = RefSeq(ref, path, max_seq, cfg)
+    try:
+        want_lg = r.feed(prompt)
+        want_k, want_v = r.kv(n_prompt)
+        want = r.greedy(want_lg, steps)
+    finally:
+        r.close()
+    got = {}
+    gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, 128)
+    try:
+        for sk in (0, 1):
+            gpu.tune(HAKO_TUNE_Q6K_GEMM_SK, sk)
+            dec = make(gpu, path, 1, max_seq)
+            try:
+                dec.set_pos(0)
+                first, lg = dec.prefill(prompt, logits=True)
+                k, v = device_kv(gpu, dec, 0, n_prompt)
+                toks = [first] + dec.generate(first, steps - 1)[:, 0].tolist()
+            finally:
+                dec.close()
+            got[sk] = (lg, k, v, toks)
+    finally:
+        gpu.tune(HAKO_TUNE_Q6K_GEMM_TN, 0)
+        gpu.tune(HAKO_TUNE_Q6K_GEMM_SK, 1)
+    for sk, (lg, k, v, toks) in got.items():
+        within(f"stream-K {sk} K", k, want_k, 3.8e-4)
+        within(f"stream-K {sk} V", v, want_v, 3.8e-4)
+        within(f"stream-K {sk} logits", lg, want_lg, 3e-6)
+        assert toks == want, sk
+
+
 # head_dim 64 takes the chunk-record attention, head_dim 128 (SMALL_128) the
 # matrix-core prompt attention, here for a pass that starts past position 0
 # (measured K/V 2.4e-7, 1.1e-4; logits 3.1e-7, 4.6e-7)
