@@ -9,6 +9,9 @@ and logits within a max-abs-normalised bar set per case at most 5x the value
 measured on MI355X (the q8 re-quantization of an activation that differs in
 its last bit can flip one int8 value, which moves logits by up to ~5e-4 of
 their range; the step is bit-reproducible, so each case's value is fixed).
+A sequence beyond 1e-5 must be explained: each outlying step as one flipped
+int8 of the lm_head's q8 input, or a drift within 4x that of the
+reference's own build without -ffast-math.
 """
 import ctypes as C
 
@@ -76,23 +79,72 @@ def seq_setup(cfg, n_seq, seed, max_pos):
     return pos.astype(np.int32), starts.astype(np.int32), kvs
 
 
-# logits bars: measured maxima 4.1e-7, 8.1e-5, 2.3e-5, 4.7e-4, 6.5e-7, 4.2e-7, 3.8e-6, 4.3e-4 (one int8
-# of a q8 row flipped, the Q4_K down projection of the dense-type model)
-@pytest.mark.parametrize("cfg,n_seq,seed,max_seq,max_pos,bar", [(TINY, 4, 1, 256, 200, 2e-6),
-                                                                 (TINY, 16, 2, 256, 200, 4e-4),
-                                                                 (SMALL_128, 16, 3, 256, 200, 1.1e-4),
-                                                                 (UNTIED_Q4_OUT, 5, 4, 256, 200, 2.3e-3),
-                                                                 (LONG, 6, 5, 2304, 2200, 3.2e-6),
-                                                                 (KQM, 5, 6, 256, 200, 2.1e-6),
-                                                                 (WIDE, 3, 7, 256, 200, 1.9e-5),
-                                                                 (DENSE, 4, 8, 256, 200, 2.2e-3)])
+def ref_steps_with_head_input(lib, path, kv, pos, start, steps, vocab, d_model, max_seq):
+    """The reference's greedy steps from a prefilled context (as
+    prefilled_greedy), with each step's lm_head input: ctx.xn after
+    hakm_forward, the final rmsnorm's output (src/model.c:158-160)."""
+    from oracle.hako_oracle import HakmCtx, ref_greedy_pick
+    ctx = lib.hakm_ctx_new(path.encode(), max_seq)
+    assert ctx
+    toks, logits, xns = [start], [], []
+    try:
+        c = HakmCtx.from_address(ctx)
+        n_layers, kvd = kv.shape[1], kv.shape[3]
+        for which, ptr in ((0, c.k_cache), (1, c.v_cache)):
+            np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_float)), shape=(n_layers, max_seq, kvd))[:, :pos] = \
+                kv[which]
+        c.pos = pos
+        for _ in range(steps):
+            p = lib.hakm_forward(ctx, toks[-1])
+            lg = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(vocab,)).copy()
+            xns.append(np.ctypeslib.as_array(C.cast(c.xn, C.POINTER(C.c_float)), shape=(d_model,)).copy())
+            logits.append(lg)
+            toks.append(ref_greedy_pick(lg))
+    finally:
+        lib.hakm_ctx_free(ctx)
+    return toks[1:], np.stack(logits), np.stack(xns)
+
+
+def head_flip(diff, w_out, xn, tol):
+    """Whether a logits difference is one int8 of the lm_head's q8_32 input
+    row rounded the other way (src/quant.c:127-144: code = lrintf(x / scale),
+    scale = amax / 127 of the element's 32-block): the difference is then
+    +-scale times one column of the dequantized output matrix, up to `tol`
+    of the logits' range, and the reference's x / scale at that element lies
+    within 1e-4 of a rounding tie k + 1/2. Returns (element, why) or (None, why)."""
+    diff = np.asarray(diff, np.float64)
+    c = w_out.T @ diff / np.sum(w_out * w_out, axis=0)
+    res = np.max(np.abs(diff[:, None] - w_out * c[None, :]), axis=0)
+    i = int(np.argmin(res))
+    blk = xn[i // 32 * 32:(i // 32 + 1) * 32]
+    scale = np.float32(np.max(np.abs(blk))) / np.float32(127.0)
+    t = abs(float(np.float32(xn[i]) * (np.float32(1.0) / scale)))
+    why = f"element {i}: residual {res[i]:.2e}, coefficient {c[i]:.4e} vs scale {scale:.4e}, x/scale {t:.5f}"
+    ok = res[i] <= tol and abs(abs(c[i]) - scale) <= 1e-3 * scale and abs(t - np.floor(t) - 0.5) < 1e-4
+    return (i if ok else None), why
+
+
+# Outliers: a sequence whose logits differ from the reference's by more than
+# 1e-5 of their range must be explained. "head": each such step is one int8
+# of the lm_head's q8 input flipped (head_flip; the Q4_K output matrix).
+# "nofast": the reference's own build without -ffast-math (the same
+# arithmetic in another rounding order) drifts on that sequence at least a
+# quarter as much, so the difference is the model's sensitivity to one int8
+# flip inside the layers. Bars: at most 5x the measured maxima 4.1e-7,
+# 8.1e-5, 2.3e-5, 4.7e-4, 6.5e-7, 4.2e-7, 3.8e-6, 4.4e-4.
+@pytest.mark.parametrize("cfg,n_seq,seed,max_seq,max_pos,bar,explain", [
+    (TINY, 4, 1, 256, 200, 2e-6, None), (TINY, 16, 2, 256, 200, 4e-4, "nofast"),
+    (SMALL_128, 16, 3, 256, 200, 1.1e-4, "nofast"), (UNTIED_Q4_OUT, 5, 4, 256, 200, 2.3e-3, "head"),
+    (LONG, 6, 5, 2304, 2200, 3.2e-6, None), (KQM, 5, 6, 256, 200, 2.1e-6, None),
+    (WIDE, 3, 7, 256, 200, 1.9e-5, "nofast"), (DENSE, 4, 8, 256, 200, 2.2e-3, "nofast")])
 def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, n_seq, seed, max_seq, max_pos,
-                                                       bar):
-    from dropin import prefilled_greedy
+                                                       bar, explain):
+    from dropin import bind_ctx, prefilled_greedy
+    from helpers import maxabs_rel
     from hako_amd.decoder import Decoder
     path = str(tmp_path / "m.mlf2")
     mlf2.write_qwen2(path, cfg, seed)
-    steps = 8
+    steps, tight = 8, 1e-5
     pos, starts, kvs = seq_setup(cfg, n_seq, seed, max_pos)
     dec = Decoder(gpu, path, n_seq=n_seq, max_seq=max_seq)
     try:
@@ -107,12 +159,40 @@ def test_batched_greedy_matches_reference_per_sequence(gpu, ref, tmp_path, cfg, 
     finally:
         dec.close()
     got, logits = np.stack(got), np.stack(logits)
+    w_out = ref_nofast = None
+    if explain == "head":
+        from oracle.hako_oracle import Oracle
+        f = mlf2.Mlf2File(path)
+        t = f.tensors["output.weight"]
+        w_out = Oracle().dequant(t["type"], np.asarray(f.data("output.weight")), cfg.vocab * cfg.d_model)
+        w_out = w_out.reshape(cfg.vocab, cfg.d_model).astype(np.float64)
+    elif explain == "nofast":
+        from oracle.hako_oracle import REF_NOFAST_LIB
+        ref_nofast = bind_ctx(C.CDLL(REF_NOFAST_LIB))
     for s in range(n_seq):
-        want, want_logits = prefilled_greedy(ref, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=steps,
-                                             vocab=cfg.vocab, max_seq=max_seq)
+        want, want_logits, xns = ref_steps_with_head_input(ref, path, kvs[s], int(pos[s]), int(starts[s]), steps,
+                                                           cfg.vocab, cfg.d_model, max_seq)
         assert np.all(np.isfinite(want_logits))
         assert got[:, s].tolist() == want, f"sequence {s} (position {pos[s]})"
-        within(f"batched logits {cfg.d_model}/{seed} seq {s}", logits[:, s], want_logits, bar)
+        err = within(f"batched logits {cfg.d_model}/{seed} seq {s}", logits[:, s], want_logits, bar)
+        if err <= tight:
+            continue
+        assert explain, f"sequence {s}: {err:.2e} above {tight:.0e} with no explanation"
+        if explain == "nofast":
+            _, nf = prefilled_greedy(ref_nofast, path, kvs[s], int(pos[s]), start=int(starts[s]), steps=steps,
+                                     vocab=cfg.vocab, max_seq=max_seq)
+            err_nf = maxabs_rel(nf, want_logits)
+            print(f"[drift] seq {s}: device {err:.2e}, reference without fast-math {err_nf:.2e}", flush=True)
+            assert err <= 4 * err_nf, f"sequence {s}: {err:.2e} > 4x the reference's own drift {err_nf:.2e}"
+        else:
+            for st in range(steps):
+                diff = logits[st, s].astype(np.float64) - want_logits[st]
+                rng = float(np.ptp(want_logits[st]))
+                if np.max(np.abs(diff)) <= tight * rng:
+                    continue
+                i, why = head_flip(diff, w_out, xns[st], tight * rng)
+                print(f"[flip] seq {s} step {st}: {why}", flush=True)
+                assert i is not None, f"sequence {s} step {st}: not one flipped lm_head input ({why})"
 
 
 def test_batched_graph_replays_equal_eager_steps(gpu, tmp_path):
