@@ -86,11 +86,12 @@ def bench_copy(g, nbytes: int, steps: int, warmup: int, eager: bool) -> dict:
     return res
 
 
-def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
+def _time_launches(g, launch, steps: int, warmup: int, eager: bool, spread_reps: int = 8) -> dict:
     """K launches: replayed from a captured HIP graph between two device
     wall-clock marks inside the graph, or (eager) issued one by one from
     Python between two events, as profilers' per-dispatch counter collection
-    needs. Also the median single-launch latency."""
+    needs. Also the median single-launch latency and (graph) the p10 / p50 /
+    p90 of the per-launch time over the first replay and `spread_reps` more."""
     e0, e1 = g.event(), g.event()
     if eager:
         for k in range(warmup):
@@ -141,10 +142,21 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
         g.graph_launch(timed)
         g.record(e1)
         graph_ms = g.elapsed_ms(e0, e1)
-        t = g.download(stamps, np.uint64, (3,)).astype(np.int64)
+
+        def region_ms():
+            t = g.download(stamps, np.uint64, (3,)).astype(np.int64)
+            ticks = int(t[2] - t[1])
+            return (int(t[1] - t[0]) - ticks) / g.timestamp_hz() * 1e3, ticks
+
+        ms, mark_ticks = region_ms()
+        # The spread: the same timed graph replayed `spread_reps` more times (each
+        # replay starts with its own lead-in launches); `ms` stays the first
+        # replay's, the K launches the caller asked for.
+        rep_ms = [ms]
+        for _ in range(spread_reps):
+            g.graph_launch(timed)
+            rep_ms.append(region_ms()[0])
         stamps.free()
-        mark_ticks = int(t[2] - t[1])
-        ms = (int(t[1] - t[0]) - mark_ticks) / g.timestamp_hz() * 1e3
         g.graph_destroy(warm)
         g.graph_destroy(timed)
     single = []
@@ -153,10 +165,14 @@ def _time_launches(g, launch, steps: int, warmup: int, eager: bool) -> dict:
         launch(k)
         g.record(e1)
         single.append(g.elapsed_ms(e0, e1))
-    res = {"ms_total": ms, "us_per_launch": ms * 1e3 / steps, "single_launch_us": float(np.median(single)) * 1e3}
+    res = {"ms_total": ms, "us_per_launch": ms * 1e3 / steps, "single_launch_us": float(np.median(single)) * 1e3,
+           "single_launch_us_p10_p90": [float(np.percentile(single, q)) * 1e3 for q in (10, 90)]}
     if not eager:
         res["graph_ms_with_lead_in"] = graph_ms
         res["mark_slot_us"] = mark_ticks / g.timestamp_hz() * 1e6
+        per = np.array(rep_ms) * 1e3 / steps
+        res["us_per_launch_p10_p50_p90"] = [float(np.percentile(per, q)) for q in (10, 50, 90)]
+        res["timed_replays"] = len(rep_ms)
     return res
 
 
@@ -597,7 +613,9 @@ def main():
             traffic, ratio = read_traffic(name)
             extra[name] = {"us_per_launch": round(r["us_per_launch"], 3), "gbps": round(r["gbps"], 1),
                            "hbm_frac": round(r["gbps"] / HBM_PEAK_GBPS, 4),
+                           "us_per_launch_p10_p50_p90": [round(v, 3) for v in r["us_per_launch_p10_p50_p90"]],
                            "single_launch_us": round(r["single_launch_us"], 3),
+                           "single_launch_us_p10_p90": [round(v, 3) for v in r["single_launch_us_p10_p90"]],
                            "traffic": traffic, "traffic_over_algorithmic": ratio}
             if not args.no_cpu:
                 # copies kept to about 1.3 GB of host memory for the vocab shape
@@ -654,6 +672,9 @@ def main():
                      "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": read_traffic(HEADLINE)[0]},
         "cpu_baseline": cpu,
         "single_launch_us": round(head["single_launch_us"], 3),
+        "single_launch_us_p10_p90": [round(v, 3) for v in head["single_launch_us_p10_p90"]],
+        "us_per_launch_p10_p50_p90": [round(v, 3) for v in head["us_per_launch_p10_p50_p90"]],
+        "timed_replays": head["timed_replays"],
         "extra": extra,
         "decode": decode,
         "decode_7b": decode7,
