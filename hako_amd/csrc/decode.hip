@@ -41,6 +41,7 @@ namespace {
 constexpr int kChunk = 64;   // cache positions per attention workgroup
 constexpr int kMaxG = 8;     // query heads per KV head
 constexpr int kArgBlocks = 64;
+constexpr int kArgHoist = 16;   // loads per thread taken up front by argmax_part_kernel (slices up to 4096)
 constexpr int kDecItems = 4; // row items per wave of the fused GEMV
 constexpr int kDecItemsQkv = 2; // ... of the q/k/v launch (fewer rows: more workgroups)
 // ... of the gate/up launch: 0 = by shape (8 when a row item is one row,
@@ -125,15 +126,44 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
 	return t;
 }
 
+// Rows up to kNormHoist * 256 wide take every load of the row and of w up
+// front (range-checked buffer loads: past n they read zeros, which add
+// nothing to ss) instead of one dependent load per loop step; a thread's
+// elements are i = tid + 256 j either way, in the same order, so the sums
+// and outputs are the same bits.
+constexpr int kNormHoist = 32;
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                       float *__restrict__ y, int n, float eps) {
 	__shared__ float red[4];
 	const float *xr = x + (size_t)blockIdx.x * n;
+	float *yr = y + (size_t)blockIdx.x * n;
+	const int tid = threadIdx.x;
+	if (n <= kNormHoist * 256) {
+		const __amdgpu_buffer_rsrc_t xs = stream_rsrc(xr, (uint32_t)n * 4u), ws = stream_rsrc(w, (uint32_t)n * 4u);
+		const int nj = (n + 255) >> 8;   // uniform
+		float xv[kNormHoist], wv[kNormHoist];
+#pragma unroll
+		for (int j = 0; j < kNormHoist; j++) {
+			const uint32_t off = j < nj ? 4u * (uint32_t)(tid + 256 * j) : kBufNone;
+			xv[j] = ld_f32(xs, off);
+			wv[j] = ld_f32(ws, off);
+		}
+		float ss = 0.0f;
+#pragma unroll
+		for (int j = 0; j < kNormHoist; j++) ss = __builtin_fmaf(xv[j], xv[j], ss);
+		ss = block_sum256(ss, red);
+		const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+		for (int j = 0; j < kNormHoist; j++)
+			if (tid + 256 * j < n) yr[tid + 256 * j] = xv[j] * scale * wv[j];
+		return;
+	}
 	float ss = 0.0f;
-	for (int i = threadIdx.x; i < n; i += 256) ss = __builtin_fmaf(xr[i], xr[i], ss);
+	for (int i = tid; i < n; i += 256) ss = __builtin_fmaf(xr[i], xr[i], ss);
 	ss = block_sum256(ss, red);
 	const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-	for (int i = threadIdx.x; i < n; i += 256) y[(size_t)blockIdx.x * n + i] = xr[i] * scale * w[i];
+	for (int i = tid; i < n; i += 256) yr[i] = xr[i] * scale * w[i];
 }
 
 // x = a + y (a may be x)
@@ -1153,11 +1183,31 @@ __global__ __launch_bounds__(256) void argmax_part_kernel(const float *__restric
 	const int i0 = (int)((int64_t)b * V / kArgBlocks), i1 = (int)((int64_t)(b + 1) * V / kArgBlocks);
 	float bv = NAN;
 	int bi = 0x7FFFFFFF;
-	for (int i = i0 + threadIdx.x; i < i1; i += 256)
-		if (better(lg[i], i, bv, bi)) {
-			bv = lg[i];
-			bi = i;
+	if (i1 - i0 <= kArgHoist * 256) {
+		// every load of the slice up front (past i1 a range-checked load reads
+		// a value no index takes), then the same comparisons in the same order
+		const __amdgpu_buffer_rsrc_t ls = stream_rsrc(lg + i0, (uint32_t)(i1 - i0) * 4u);
+		float lv[kArgHoist];
+#pragma unroll
+		for (int j = 0; j < kArgHoist; j++) {
+			const int i = i0 + threadIdx.x + 256 * j;
+			lv[j] = ld_f32(ls, i < i1 ? 4u * (uint32_t)(i - i0) : kBufNone);
 		}
+#pragma unroll
+		for (int j = 0; j < kArgHoist; j++) {
+			const int i = i0 + threadIdx.x + 256 * j;
+			if (i < i1 && better(lv[j], i, bv, bi)) {
+				bv = lv[j];
+				bi = i;
+			}
+		}
+	} else {
+		for (int i = i0 + threadIdx.x; i < i1; i += 256)
+			if (better(lg[i], i, bv, bi)) {
+				bv = lg[i];
+				bi = i;
+			}
+	}
 	argmax_wave(bv, bi);
 	if (lane == 0) {
 		bv_s[wave] = bv;
