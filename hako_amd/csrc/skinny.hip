@@ -73,23 +73,6 @@ __device__ __forceinline__ SegView seg_of(const SkSegs s, int wrow0, bool swiglu
 	return v;
 }
 
-// Epilogue: lane holds tokens 4*(l/16) + v of row r (its lane's row).
-// Store: out[t][r] = y + bias[r]; Add: out[t][r] += y.
-__device__ __forceinline__ void skinny_epilogue(int epi, const SegView &S, int vrow, bool ok,
-                                                const float y[4], int M, int lane) {
-	const int t0 = 4 * (lane >> 4);
-	if (!ok) return;
-	const int r = vrow - S.row0;
-	const float b = (epi == kSkStore && S.bias) ? S.bias[r] : 0.0f;
-#pragma unroll
-	for (int v = 0; v < 4; v++) {
-		if (t0 + v < M) {
-			float *o = S.out + (size_t)(t0 + v) * S.ld + r;
-			*o = epi == kSkAdd ? *o + y[v] : y[v] + b;
-		}
-	}
-}
-
 // ── Q4_K x q8 ──
 //
 // Persistent grid of G workgroups over the launch's 16-row groups: workgroup
@@ -467,6 +450,27 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 	const __amdgpu_buffer_rsrc_t ers = stream_rsrc(esc, BLK ? (uint32_t)M * (uint32_t)NB * 4u : 0u);
 	const __amdgpu_buffer_rsrc_t enone = stream_rsrc(esc, 0);
 	const int t0 = 4 * kq;
+	// The epilogue's operands, loaded before the stream so that the end of the
+	// workgroup waits on nothing (loaded there, each sat behind its own wait):
+	// the per-token powers of two (not BLK), and the row's bias (Store) or the
+	// lane's four outputs (Add).
+	float ev[4], pv[4];
+	{
+		const __amdgpu_buffer_rsrc_t ets = stream_rsrc(esc, BLK ? 0u : (uint32_t)M * 4u);
+		const float *bsrc = uniform_ptr(S.bias);
+		const __amdgpu_buffer_rsrc_t brs = stream_rsrc(bsrc ? (const void *)bsrc : (const void *)esc,
+		                                               EPI == kSkStore && bsrc ? (uint32_t)S.rows * 4u : 0u);
+		const int ld = __builtin_amdgcn_readfirstlane(S.ld);
+		const __amdgpu_buffer_rsrc_t ors = stream_rsrc(uniform_ptr(S.out), EPI == kSkAdd ? (uint32_t)M * (uint32_t)ld * 4u
+		                                                                              : 0u);
+		const float bv = ld_f32(brs, ok ? 4u * (uint32_t)wr : kBufNone);
+#pragma unroll
+		for (int v = 0; v < 4; v++) {
+			const bool tv = t0 + v < M;
+			ev[v] = ld_f32(ets, tv ? 4u * (uint32_t)(t0 + v) : kBufNone);
+			pv[v] = EPI == kSkAdd ? ld_f32(ors, ok && tv ? 4u * ((uint32_t)(t0 + v) * ld + wr) : kBufNone) : bv;
+		}
+	}
 
 	struct WBuf {
 		uint4 v[4];
@@ -608,14 +612,18 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void q6
 	}
 	float y[4];
 #pragma unroll
-	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? (BLK ? acc[v] : acc[v] * esc[t0 + v]) : 0.0f;
+	for (int v = 0; v < 4; v++) y[v] = t0 + v < M ? (BLK ? acc[v] : acc[v] * ev[v]) : 0.0f;
 	if (EPI == kSkPart) {
 		if (ok)
 #pragma unroll
 			for (int v = 0; v < 4; v++) part[((size_t)split * 16 + t0 + v) * vrows + vrow] = y[v];
 		return;
 	}
-	skinny_epilogue(EPI, S, vrow, ok, y, M, lane);
+	// Store: out[t][r] = y + bias[r] (+ 0 without a bias); Add: out[t][r] += y
+	if (ok)
+#pragma unroll
+		for (int v = 0; v < 4; v++)
+			if (t0 + v < M) S.out[(size_t)(t0 + v) * S.ld + wr] = EPI == kSkAdd ? pv[v] + y[v] : y[v] + pv[v];
 }
 
 // Grid (ceil(rows/256), M): the splits' sums, in split order, through the
