@@ -49,6 +49,8 @@ constexpr int kDecItemsQkv = 2; // ... of the q/k/v launch (fewer rows: more wor
 // over the whole activation; 7B step 1781 -> 1744 us, the 3B shape slower
 // with 8), else 4 or 8 (tuning knob)
 int g_dec_gu_items = 0;
+// gate/up launch of the one-sequence step: 1 flat grid, 2 persistent grid, 0 by shape (persistent)
+int g_dec_gu_grid = 0;
 
 // One sequence's output projection adds its per-input-block row sums into a
 // residual accumulator of 64-bit fixed-point values (2^-32 units): integer
@@ -528,6 +530,169 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(DecSegs segs, const float 
 		} else if (writer) {
 			sout[item_row(j)] = EPI == kEpiAdd ? pre[g] + tot : (sbias ? tot + pre[g] : tot);
 		}
+	}
+}
+
+// Persistent grid for the gate/up launch (rmsnorm prologue, SwiGLU
+// epilogue): one workgroup of WAVES waves per CU, workgroup b owning the row
+// pairs [b F / G, (b+1) F / G) of the two F-row matrices. The prologue (x plus
+// the residual accumulator, rmsnorm, q8_32) runs once per workgroup instead
+// of once per few rows; the waves then walk their row tiles (tile k of wave
+// w: rows p0 + rt (w + WAVES k) + rsub) with kDecDepth items in flight, items
+// 2k and 2k+1 the gate and up rows of tile k, so the two sums of a row meet
+// in neighbouring lanes as in q4k_dec_kernel. Lane work, reductions and the
+// epilogue are q4k_dec_kernel's, so h is the same bit for bit.
+constexpr int kDecDepth = 4;
+
+template <int XP, int WAVES, bool OACC>
+__global__ __launch_bounds__(WAVES * kWave) void q4k_dec_gu_kernel(DecSegs segs, const float *__restrict__ x,
+                                                                  const float *__restrict__ nw, float eps, int n_in,
+                                                                  const long long *__restrict__ oacc,
+                                                                  float *__restrict__ xmid,
+                                                                  long long *__restrict__ oacc_next) {
+	extern __shared__ __align__(16) uint8_t smem[];
+	int8_t *xq_s = (int8_t *)smem;
+	float *xs_s = (float *)(smem + n_in);
+	float *red_s = xs_s + (n_in >> 5);
+	constexpr int T = WAVES * kWave;
+	static_assert(kDecDepth % 2 == 0, "a gate item and its up item share a group");
+	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int NB = n_in >> 8, C = NB * 4;
+	const int seg = next_pow2(C), rt = 64 / seg;
+	const int sub = lane & (seg - 1), rsub = lane / seg;
+	const size_t rb = (size_t)NB * kQ4Bytes;
+	const int F = segs.s[0].rows;
+	const int p0 = (int)((int64_t)blockIdx.x * F / gridDim.x), p1 = (int)((int64_t)(blockIdx.x + 1) * F / gridDim.x);
+	const int ntiles = (p1 - p0 + rt - 1) / rt;
+	const int nit = ntiles > wave ? 2 * ((ntiles - wave + WAVES - 1) / WAVES) : 0;
+	auto item_row = [&](int it) -> int { return p0 + rt * (wave + WAVES * (it >> 1)) + rsub; };
+	const uint32_t mbytes = (uint32_t)(rb * F);
+	const __amdgpu_buffer_rsrc_t wra = stream_rsrc(segs.s[0].w, mbytes), wrb = stream_rsrc(segs.s[1].w, mbytes);
+	// item it is gate (even) or up (odd): the parity of its slot j in a group
+	auto issue = [&](Q4Buf &b, int it, bool up) {
+		const int row = item_row(it);
+		const bool on = it < nit && row < p1 && sub < C;
+		const uint32_t blk = on ? (uint32_t)((size_t)row * rb + (size_t)(sub >> 2) * kQ4Bytes) : kBufNone;
+		const __amdgpu_buffer_rsrc_t r = up ? wrb : wra;
+		b.h = ld_b128(r, blk);
+		b.q0 = ld_b128(r, blk + 16 + 32 * (sub & 3));
+		b.q1 = ld_b128(r, blk + 32 + 32 * (sub & 3));
+	};
+
+	// 1. activation, norm weight and accumulator loads, then the first items' weights
+	float4 xv[XP], nv[XP];
+	uint4 oa[XP][2];
+	uint4 of[XP];
+	const __amdgpu_buffer_rsrc_t fr =
+	    stream_rsrc(OACC ? (const void *)acc_flags(oacc, n_in) : nullptr, (OACC && blockIdx.x == 0) ? 4u * n_in : 0u);
+#pragma unroll
+	for (int k = 0; k < XP; k++) {
+		const int e = min((int)(threadIdx.x + k * T) * 4, n_in - 4);
+		xv[k] = *(const float4 *)(x + e);
+		nv[k] = *(const float4 *)(nw + e);
+		if (OACC) {
+			oa[k][0] = *(const uint4 *)(oacc + e);
+			oa[k][1] = *(const uint4 *)(oacc + e + 2);
+			of[k] = ld_b128(fr, 4u * e);
+		}
+	}
+	__builtin_amdgcn_sched_barrier(0);
+	Q4Buf buf[kDecDepth];
+#pragma unroll
+	for (int j = 0; j < kDecDepth; j++) {
+		issue(buf[j], j, j & 1);
+		__builtin_amdgcn_sched_barrier(0);
+	}
+
+	// 2. prologue (as q4k_dec_kernel): x + o, rmsnorm, q8_32 into LDS;
+	//    workgroup 0 stores x + o and clears the next layer's accumulator
+	if (OACC) {
+		auto fx = [](uint32_t lo, uint32_t hi) -> float {
+			return from_fixed((long long)(((unsigned long long)hi << 32) | lo), 0);
+		};
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			xv[k].x += fx(oa[k][0].x, oa[k][0].y);
+			xv[k].y += fx(oa[k][0].z, oa[k][0].w);
+			xv[k].z += fx(oa[k][1].x, oa[k][1].y);
+			xv[k].w += fx(oa[k][1].z, oa[k][1].w);
+		}
+	}
+	float ss = 0.0f;
+#pragma unroll
+	for (int k = 0; k < XP; k++) {
+		if ((int)(threadIdx.x + k * T) * 4 < n_in) {
+			ss = __builtin_fmaf(xv[k].x, xv[k].x, ss);
+			ss = __builtin_fmaf(xv[k].y, xv[k].y, ss);
+			ss = __builtin_fmaf(xv[k].z, xv[k].z, ss);
+			ss = __builtin_fmaf(xv[k].w, xv[k].w, ss);
+		}
+	}
+	ss = wave_sum(ss);
+	if (lane == 0) red_s[wave] = ss;
+	__syncthreads();
+	ss = red_s[0];
+#pragma unroll
+	for (int w = 1; w < WAVES; w++) ss += red_s[w];
+	const float scale = 1.0f / sqrtf(ss / (float)n_in + eps);
+#pragma unroll
+	for (int k = 0; k < XP; k++) {
+		const int e = (threadIdx.x + k * T) * 4;
+		float4 v = xv[k];
+		v.x = v.x * scale * nv[k].x;
+		v.y = v.y * scale * nv[k].y;
+		v.z = v.z * scale * nv[k].z;
+		v.w = v.w * scale * nv[k].w;
+		float sc;
+		const uint32_t packed = q8_quant4(v, sc);
+		if (e < n_in) {
+			*(uint32_t *)(xq_s + q8_lds_pos(e)) = packed;
+			if ((threadIdx.x & 7) == 0) xs_s[e >> 5] = sc;
+		}
+	}
+	if (OACC && blockIdx.x == 0) {
+#pragma unroll
+		for (int k = 0; k < XP; k++) {
+			const int e = (threadIdx.x + k * T) * 4;
+			if (e < n_in) {
+				auto nf = [](float v, uint32_t fl) -> float { return fl ? v + from_fixed(0, (int)fl) : v; };
+				const float4 xm = make_float4(nf(xv[k].x, of[k].x), nf(xv[k].y, of[k].y), nf(xv[k].z, of[k].z),
+				                              nf(xv[k].w, of[k].w));
+				*(float4 *)(xmid + e) = xm;
+				*(uint4 *)(oacc_next + e) = make_uint4(0u, 0u, 0u, 0u);
+				*(uint4 *)(oacc_next + e + 2) = make_uint4(0u, 0u, 0u, 0u);
+				*(int4 *)(acc_flags(oacc_next, n_in) + e) = make_int4(0, 0, 0, 0);
+			}
+		}
+	}
+	__syncthreads();
+	Q4Col col;
+	q4_col(xq_s, xs_s, min(sub, C - 1), col);
+
+	// 3. groups of kDecDepth items: consume each slot, reload it with the item
+	//    kDecDepth later, then the group's SwiGLU rows
+	float *h = segs.s[0].out;
+	for (int base = 0; base < nit; base += kDecDepth) {
+		float rsum[kDecDepth];
+#pragma unroll
+		for (int j = 0; j < kDecDepth; j++) {
+			const int it = base + j;
+			float f = 0.0f;
+			if (it < nit) {
+				int ia, ib;
+				q4_isum(buf[j], col, ia, ib);
+				f = q4_fold(buf[j], 16u * (sub & 1), (sub & 3) >= 2 ? ~0u : 0u, ia, ib, col);
+			}
+			issue(buf[j], it + kDecDepth, j & 1);
+			__builtin_amdgcn_sched_barrier(0);
+			rsum[j] = (it < nit && item_row(it) < p1 && sub < C) ? f : 0.0f;
+		}
+		const float tot = seg_sum4(rsum, seg, lane);
+		const int j = sub & 3;
+		// the up sum of the same row: item j + 1, in the neighbouring lane
+		const float other = dpp_f<kDppQuadSwap1>(tot);
+		if ((sub >> 2) == 0 && (j & 1) == 0 && base + j < nit && item_row(base + j) < p1)
+			h[item_row(base + j)] = silu(tot) * other;
 	}
 }
 
@@ -1264,6 +1429,7 @@ bool known_type(int t) {
 }  // namespace
 
 void dec_set_gu_items(int v) { g_dec_gu_items = (v == 4 || v == 8) ? v : 0; }
+void dec_set_gu_grid(int v) { g_dec_gu_grid = (v == 1 || v == 2) ? v : 0; }
 
 }  // namespace hako
 
@@ -1351,6 +1517,36 @@ int launch_dec(const DecSegs &segs, const float *x, const float *nw, float eps, 
 	}
 #undef HK_DEC
 	HK_LAUNCHED("q4k_dec");
+	return HAKO_GPU_OK;
+}
+
+// The gate/up launch on the persistent grid (q4k_dec_gu_kernel): one
+// workgroup of four waves per CU. segs: gate (out = h) and up, F rows each.
+int launch_dec_gu(const DecSegs &segs, const float *x, const float *nw, float eps, int n_in,
+                  const long long *oacc = nullptr, float *xmid = nullptr, long long *oacc_next = nullptr) {
+	constexpr int W = 4;
+	const int F = segs.s[0].rows, rt = 64 / next_pow2(n_in / kQK * 4);
+	if ((size_t)F * (n_in / kQK) * kQ4Bytes >= kBufNone)
+		return set_error(HAKO_GPU_EINVAL, "fused Q4_K GEMV segment of %d x %d exceeds 2 GiB", F, n_in);
+	int wgs = cu_count();
+	const int tiles = (F + rt - 1) / rt;
+	if (wgs > tiles) wgs = tiles;
+	const size_t lds = (size_t)n_in + (size_t)(n_in / 32) * 4 + 4 * W + 16;
+	const int xp = (n_in + 4 * W * 64 - 1) / (4 * W * 64);
+#define HK_DGU(XP, OA) \
+	hipLaunchKernelGGL((q4k_dec_gu_kernel<XP, W, OA>), dim3(wgs), dim3(W * kWave), lds, stream(), segs, x, nw, eps, n_in, \
+	                   oacc, xmid, oacc_next)
+	if (oacc) {
+		if (xp <= 1) HK_DGU(1, true);
+		else if (xp <= 2) HK_DGU(2, true);
+		else HK_DGU(4, true);
+	} else {
+		if (xp <= 1) HK_DGU(1, false);
+		else if (xp <= 2) HK_DGU(2, false);
+		else HK_DGU(4, false);
+	}
+#undef HK_DGU
+	HK_LAUNCHED("q4k_dec_gu");
 	return HAKO_GPU_OK;
 }
 
@@ -1686,6 +1882,9 @@ int enqueue_step(hako_gpu_decoder *d) {
 		// kept in xa as the residual of step 5)
 		const float *resid = d->x;
 		const int gu_items = g_dec_gu_items ? g_dec_gu_items : (D > 2048 ? 8 : kDecItems);
+		// the persistent grid by shape (its prologue once per workgroup: 7B
+		// step 1665 -> 1571 us, 3B 1138 -> 1117.5 us, the same bits)
+		const bool gu_persist = g_dec_gu_grid != 1;
 		if (fused_gu) {
 			DecSegs s{};
 			s.n = 2;
@@ -1694,7 +1893,8 @@ int enqueue_step(hako_gpu_decoder *d) {
 			if (merge_o) {
 				// (a workgroup must not clear what the others still read)
 				long long *on = self_next ? d->oacc + (size_t)3 * acc_row(D) : oacc_next;
-				if (int rc = gu_items == 8
+				if (int rc = gu_persist ? launch_dec_gu(s, d->x, B.ffn_norm, m.rms_eps, D, oacc, d->xa, on)
+				             : gu_items == 8
 				                 ? launch_dec<kProNorm, kEpiSwiGLU, 8>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F, oacc,
 				                                                       d->xa, on)
 				                 : launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F, oacc,
@@ -1706,7 +1906,8 @@ int enqueue_step(hako_gpu_decoder *d) {
 					HK_LAUNCHED("residual accumulator clear");
 				}
 				resid = d->xa;
-			} else if (int rc = gu_items == 8
+			} else if (int rc = gu_persist ? launch_dec_gu(s, d->x, B.ffn_norm, m.rms_eps, D)
+			                    : gu_items == 8
 			                        ? launch_dec<kProNorm, kEpiSwiGLU, 8>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)
 			                        : launch_dec<kProNorm, kEpiSwiGLU>(s, d->x, B.ffn_norm, m.rms_eps, D, 2 * F)) {
 				return rc;

@@ -38,6 +38,7 @@ void q6k_gemm_set_sk(int v);
 void q4k_skinny_set_target_wgs(int wgs);
 void q6k_skinny_set_target_wgs(int wgs);
 void dec_set_gu_items(int v);
+void dec_set_gu_grid(int v);
 // Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
 int workspace(int slot, size_t bytes, void **ptr);
 // Look up this device's address of the no-allocation scratch array (with

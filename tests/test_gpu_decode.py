@@ -327,17 +327,19 @@ def test_qwen2_7b_decode_at_position_1024(gpu, ref, tmp_path):
 
 
 def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
-    """The gate/up launch's row items per wave (4 or 8; by shape by default)
+    """The gate/up launch's grid (flat with 4 or 8 row items per wave, or the
+    persistent grid with its prologue once per workgroup; by shape by default)
     changes only which workgroup computes a row, never the order of a row's
     additions: three greedy steps give bit-identical logits either way."""
     cfg = GQA7
     path = str(tmp_path / "gqa7.mlf2")
     mlf2.write_qwen2(path, cfg, 21)
-    HAKO_TUNE_DEC_GU_ITEMS = 9
+    HAKO_TUNE_DEC_GU_ITEMS, HAKO_TUNE_DEC_GU_GRID = 9, 16
     runs = []
     try:
-        for items in (4, 8):
+        for items, grid in ((4, 1), (8, 1), (0, 2)):
             gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, items)
+            gpu.tune(HAKO_TUNE_DEC_GU_GRID, grid)
             dec = make_decoder(gpu, path, max_seq=64)
             try:
                 tok, lg = 7, []
@@ -350,8 +352,10 @@ def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
             runs.append(np.stack(lg))
     finally:
         gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, 0)
+        gpu.tune(HAKO_TUNE_DEC_GU_GRID, 0)
     assert np.all(np.isfinite(runs[0]))
-    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+    for r in runs[1:]:
+        assert np.array_equal(runs[0].view(np.uint32), r.view(np.uint32))
 
 
 # Per-layer mixes of weight types (the reference's matmul takes any type per
