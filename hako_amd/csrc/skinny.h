@@ -34,12 +34,13 @@ enum { kSkStore = 0, kSkAdd = 1, kSkSwiGLU = 2, kSkPart = 3 };
 // Q6_K: workgroups a launch aims for; K is split over workgroups to reach
 // it. Split results go to `part` (the *_part_floats count of floats;
 // part_cap is what the caller holds), summed by a second launch that applies
-// the epilogue. 4 per CU: its waves wait on one super-block of weights per
-// barrier, so more of them in flight pay (the 7B down matmul over 16
-// tokens: 18 splits instead of 10, 3.4% of a 16-sequence step). Q4_K: the
+// the epilogue. 2 per CU: the 7B down matmul over 16 tokens then takes 9
+// splits, and the kernel after it, which adds each token's partials on one
+// CU, reads half of what 18 splits left (16-sequence step 4151-4167 ->
+// 4091-4097 us; 8 splits 4118, 10-11 splits 4210-4222). Q4_K: the
 // persistent grid's workgroups (one per CU); K is split over launches only
 // past 4096. Both are launch-shape knobs (hako_gpu_tune).
-constexpr int kSkTargetWgsQ6 = 1024;
+constexpr int kSkTargetWgsQ6 = 512;
 
 // Q4_K x q8: xq [m][n_in] int8 and xs [m][n_in/32] (q8_32 rows), m <= 16.
 int q4k_skinny_splits(int n_in, int vrows);

@@ -60,7 +60,7 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_Q4K_FLAT_ITEMS 5   /* -1: by shape (default); 0: persistent grid; 1/2/4/8: flat grid, row items per wave */
 /* Skinny (2..16 token) launches: the Q4_K persistent grid's workgroups (0:
  * the default, 256), and the workgroups a Q6_K launch aims for through its K
- * split (0: the default, 1024); the Q6_K split count sets the order in which
+ * split (0: the default, 512); the Q6_K split count sets the order in which
  * its fp32 partial sums are added. A decoder sizes its split workspace when
  * it is created; a later, larger Q6_K target makes its steps fail with
  * EINVAL. */
