@@ -51,6 +51,8 @@ constexpr int kDecItemsQkv = 2; // ... of the q/k/v launch (fewer rows: more wor
 int g_dec_gu_items = 0;
 // gate/up launch of the one-sequence step: 1 flat grid, 2 persistent grid, 0 by shape (persistent)
 int g_dec_gu_grid = 0;
+// rows per merge+o workgroup: 64 or 128, 0 by shape
+int g_dec_merge_rows = 0;
 
 // One sequence's output projection adds its per-input-block row sums into a
 // residual accumulator of 64-bit fixed-point values (2^-32 units): integer
@@ -1249,7 +1251,7 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
 // chunk rc to the fixed-point accumulator oacc (zero before the launch) with
 // an integer atomic add: the D/256 block sums of a row meet in an order-free
 // sum, which the next kernel adds to the residual stream.
-template <int HD>
+template <int HD, int RI>
 __global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ part, const int *__restrict__ posv,
                                                       const uint8_t *__restrict__ wo, long long *__restrict__ oacc,
                                                       int H, int KVH, int max_seq, int max_chunks, int D) {
@@ -1261,15 +1263,21 @@ __global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ 
 	const int pos = posv[0];
 	if (pos < 0 || pos >= max_seq) return;
 
-	// 1. this lane's weights: row 64*rc + 16*wave + lane/4, 64-weight group g of block b
-	const int g = lane & 3, row = blockIdx.y * 64 + 16 * wave + (lane >> 2);
+	// 1. this lane's weights: rows 64*RI*rc + 64*i + 16*wave + lane/4 (i < RI),
+	//    64-weight group g of block b
+	const int g = lane & 3;
 	const uint32_t rb = (uint32_t)(D / kQK) * kQ4Bytes;
 	const __amdgpu_buffer_rsrc_t wr = stream_rsrc(wo, (uint32_t)D * rb);
-	const uint32_t bo = row < D ? (uint32_t)row * rb + (uint32_t)b * kQ4Bytes : kBufNone;
-	Q4Buf wb;
-	wb.h = ld_b128(wr, bo);
-	wb.q0 = ld_b128(wr, bo + 16 + 32 * g);
-	wb.q1 = ld_b128(wr, bo + 32 + 32 * g);
+	int rows[RI];
+	Q4Buf wb[RI];
+#pragma unroll
+	for (int i = 0; i < RI; i++) {
+		rows[i] = blockIdx.y * 64 * RI + 64 * i + 16 * wave + (lane >> 2);
+		const uint32_t bo = rows[i] < D ? (uint32_t)rows[i] * rb + (uint32_t)b * kQ4Bytes : kBufNone;
+		wb[i].h = ld_b128(wr, bo);
+		wb[i].q0 = ld_b128(wr, bo + 16 + 32 * g);
+		wb[i].q1 = ld_b128(wr, bo + 32 + 32 * g);
+	}
 	__builtin_amdgcn_sched_barrier(0);
 
 	// 2. merge of head hh (kvh = hh / G, g = hh % G), HD threads per head
@@ -1286,18 +1294,21 @@ __global__ __launch_bounds__(256) void merge_o_kernel(const float *__restrict__ 
 	}
 	__syncthreads();
 
-	// 4. block b's terms of the lane's row, the row's four lanes summed, one atomic add
+	// 4. block b's terms of the lane's rows, each row's four lanes summed, one atomic add per row
 	Q4Col col;
 	q4_col(xq_s, xs_s, g, col);
-	int ia, ib;
-	q4_isum(wb, col, ia, ib);
-	float f = q4_fold(wb, 16u * (g & 1), g >= 2 ? ~0u : 0u, ia, ib, col);
-	f += __shfl_xor(f, 1);
-	f += __shfl_xor(f, 2);
-	if (g == 0 && row < D) {
-		__hip_atomic_fetch_add(oacc + row, to_fixed(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-		if (const int fl = fixed_flag(f))
-			__hip_atomic_fetch_or(acc_flags(oacc, D) + row, fl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+	for (int i = 0; i < RI; i++) {
+		int ia, ib;
+		q4_isum(wb[i], col, ia, ib);
+		float f = q4_fold(wb[i], 16u * (g & 1), g >= 2 ? ~0u : 0u, ia, ib, col);
+		f += __shfl_xor(f, 1);
+		f += __shfl_xor(f, 2);
+		if (g == 0 && rows[i] < D) {
+			__hip_atomic_fetch_add(oacc + rows[i], to_fixed(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+			if (const int fl = fixed_flag(f))
+				__hip_atomic_fetch_or(acc_flags(oacc, D) + rows[i], fl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		}
 	}
 }
 
@@ -1430,6 +1441,7 @@ bool known_type(int t) {
 
 void dec_set_gu_items(int v) { g_dec_gu_items = (v == 4 || v == 8) ? v : 0; }
 void dec_set_gu_grid(int v) { g_dec_gu_grid = (v == 1 || v == 2) ? v : 0; }
+void dec_set_merge_rows(int v) { g_dec_merge_rows = (v == 64 || v == 128) ? v : 0; }
 
 }  // namespace hako
 
@@ -1854,15 +1866,20 @@ int enqueue_step(hako_gpu_decoder *d) {
 		const bool self_next = oacc_next == oacc;
 		if (int rc = attention(d, l, nullptr, nullptr, !merge_o)) return rc;
 		if (merge_o) {
-			const dim3 grid(D / kQK, (D + 63) / 64);
+			// rows per workgroup: 64, or 128 by shape past d_model 2048 (each
+			// workgroup merges its heads' chunk records once for twice the rows:
+			// 7B step 1589 -> 1566 us; at 3B, 256 workgroups of 64 rows leave
+			// none idle and 128 rows measured 1120 -> 1141 us); the same bits
+			const int ri = (g_dec_merge_rows ? g_dec_merge_rows == 128 : D > 2048) ? 2 : 1;
+			const dim3 grid(D / kQK, (D + 64 * ri - 1) / (64 * ri));
 			if (m.head_dim == 128)
-				hipLaunchKernelGGL(merge_o_kernel<128>, grid, dim3(256), 0, stream(), d->part, d->pos,
-				                   (const uint8_t *)B.wo, oacc, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
-				                   D);
+				hipLaunchKernelGGL((ri == 2 ? merge_o_kernel<128, 2> : merge_o_kernel<128, 1>), grid, dim3(256), 0,
+				                   stream(), d->part, d->pos, (const uint8_t *)B.wo, oacc, m.n_heads, m.n_kv_heads,
+				                   d->max_seq, d->max_chunks, D);
 			else
-				hipLaunchKernelGGL(merge_o_kernel<64>, grid, dim3(256), 0, stream(), d->part, d->pos,
-				                   (const uint8_t *)B.wo, oacc, m.n_heads, m.n_kv_heads, d->max_seq, d->max_chunks,
-				                   D);
+				hipLaunchKernelGGL((ri == 2 ? merge_o_kernel<64, 2> : merge_o_kernel<64, 1>), grid, dim3(256), 0,
+				                   stream(), d->part, d->pos, (const uint8_t *)B.wo, oacc, m.n_heads, m.n_kv_heads,
+				                   d->max_seq, d->max_chunks, D);
 			HK_LAUNCHED("attention merge + o");
 			if (!fused_gu) {
 				hipLaunchKernelGGL(oacc_apply_kernel, dim3((D + 255) / 256), dim3(256), 0, stream(), d->x, oacc,

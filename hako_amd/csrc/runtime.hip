@@ -178,6 +178,7 @@ int hako_gpu_tune(int knob, int value) {
 	case HAKO_TUNE_SKINNY_Q6K_WGS: q6k_skinny_set_target_wgs(value); return ok();
 	case HAKO_TUNE_DEC_GU_ITEMS: dec_set_gu_items(value); return ok();
 	case HAKO_TUNE_DEC_GU_GRID: dec_set_gu_grid(value); return ok();
+	case HAKO_TUNE_DEC_MERGE_ROWS: dec_set_merge_rows(value); return ok();
 	default: return set_error(HAKO_GPU_EINVAL, "unknown tuning knob %d", knob);
 	}
 }
