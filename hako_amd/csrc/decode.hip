@@ -53,6 +53,8 @@ int g_dec_gu_items = 0;
 int g_dec_gu_grid = 0;
 // rows per merge+o workgroup: 64 or 128, 0 by shape
 int g_dec_merge_rows = 0;
+// row items per wave of the q/k/v launch: 2, 4 or 8, 0 by shape
+int g_dec_qkv_items = 0;
 
 // One sequence's output projection adds its per-input-block row sums into a
 // residual accumulator of 64-bit fixed-point values (2^-32 units): integer
@@ -1442,6 +1444,7 @@ bool known_type(int t) {
 void dec_set_gu_items(int v) { g_dec_gu_items = (v == 4 || v == 8) ? v : 0; }
 void dec_set_gu_grid(int v) { g_dec_gu_grid = (v == 1 || v == 2) ? v : 0; }
 void dec_set_merge_rows(int v) { g_dec_merge_rows = (v == 64 || v == 128) ? v : 0; }
+void dec_set_qkv_items(int v) { g_dec_qkv_items = (v == 2 || v == 4 || v == 8) ? v : 0; }
 
 }  // namespace hako
 
@@ -1831,7 +1834,12 @@ int enqueue_step(hako_gpu_decoder *d) {
 		const hako_gpu_block &B = d->blocks[l];
 		float *q = d->qkv, *k = d->qkv + D, *v = d->qkv + D + KV;
 		// 1. q, k, v
-		const int rpw = dec_rows_per_wave(D, kDecItemsQkv);
+		// row items per wave: 2, or 8 past d_model 2048 (fewer workgroups, each
+		// repeating the rmsnorm prologue: 7B step 1569 -> 1556 us; 4 items
+		// 1569, 16 items 1626; at 3B 2 items, 1120 against 1127 / 1181 with 4 / 8)
+		const bool qkv8 = D > 2048 && D % dec_rows_per_wave(D, 8) == 0 && KV % dec_rows_per_wave(D, 8) == 0;
+		const int qkv_items = g_dec_qkv_items ? g_dec_qkv_items : (qkv8 ? 8 : kDecItemsQkv);
+		const int rpw = dec_rows_per_wave(D, qkv_items);
 		if (B.t_q == HAKO_TYPE_Q4_K && B.t_k == HAKO_TYPE_Q4_K && B.t_v == HAKO_TYPE_Q4_K && fusable_q4(D) &&
 		    D % rpw == 0 && KV % rpw == 0) {
 			DecSegs s{};
@@ -1839,7 +1847,11 @@ int enqueue_step(hako_gpu_decoder *d) {
 			s.s[0] = {(const uint8_t *)B.wq, B.bq, q, 0, D};
 			s.s[1] = {(const uint8_t *)B.wk, B.bk, k, D, KV};
 			s.s[2] = {(const uint8_t *)B.wv, B.bv, v, D + KV, KV};
-			if (int rc = launch_dec<kProNorm, kEpiStore, kDecItemsQkv>(s, d->x, B.attn_norm, m.rms_eps, D, D + 2 * KV))
+			const int vr = D + 2 * KV;
+			if (int rc = qkv_items == 8   ? launch_dec<kProNorm, kEpiStore, 8>(s, d->x, B.attn_norm, m.rms_eps, D, vr)
+			             : qkv_items == 4 ? launch_dec<kProNorm, kEpiStore, 4>(s, d->x, B.attn_norm, m.rms_eps, D, vr)
+			                              : launch_dec<kProNorm, kEpiStore, kDecItemsQkv>(s, d->x, B.attn_norm,
+			                                                                              m.rms_eps, D, vr))
 				return rc;
 		} else {
 			if (int rc = rmsnorm(d->x, B.attn_norm, d->xn, D, m.rms_eps, 1)) return rc;

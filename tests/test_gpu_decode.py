@@ -328,21 +328,23 @@ def test_qwen2_7b_decode_at_position_1024(gpu, ref, tmp_path):
 
 def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
     """The gate/up launch's grid (flat with 4 or 8 row items per wave, or the
-    persistent grid with its prologue once per workgroup) and the merge+o
-    launch's rows per workgroup (64 or 128; all by shape by default) change
+    persistent grid with its prologue once per workgroup), the merge+o
+    launch's rows per workgroup (64 or 128) and the q/k/v launch's row items
+    per wave (2, 4 or 8; all by shape by default) change
     only which workgroup computes a row, never the order of a row's additions
     (the merge+o sums meet in an integer accumulator): three greedy steps give
     bit-identical logits either way."""
     cfg = GQA7
     path = str(tmp_path / "gqa7.mlf2")
     mlf2.write_qwen2(path, cfg, 21)
-    HAKO_TUNE_DEC_GU_ITEMS, HAKO_TUNE_DEC_GU_GRID, HAKO_TUNE_DEC_MERGE_ROWS = 9, 16, 17
+    HAKO_TUNE_DEC_GU_ITEMS, HAKO_TUNE_DEC_GU_GRID, HAKO_TUNE_DEC_MERGE_ROWS, HAKO_TUNE_DEC_QKV_ITEMS = 9, 16, 17, 18
     runs = []
     try:
-        for items, grid, mrows in ((4, 1, 64), (8, 1, 64), (0, 2, 64), (0, 2, 128)):
+        for items, grid, mrows, qi in ((4, 1, 64, 2), (8, 1, 64, 4), (0, 2, 64, 8), (0, 2, 128, 2)):
             gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, items)
             gpu.tune(HAKO_TUNE_DEC_GU_GRID, grid)
             gpu.tune(HAKO_TUNE_DEC_MERGE_ROWS, mrows)
+            gpu.tune(HAKO_TUNE_DEC_QKV_ITEMS, qi)
             dec = make_decoder(gpu, path, max_seq=64)
             try:
                 tok, lg = 7, []
@@ -357,6 +359,7 @@ def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
         gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, 0)
         gpu.tune(HAKO_TUNE_DEC_GU_GRID, 0)
         gpu.tune(HAKO_TUNE_DEC_MERGE_ROWS, 0)
+        gpu.tune(HAKO_TUNE_DEC_QKV_ITEMS, 0)
     assert np.all(np.isfinite(runs[0]))
     for r in runs[1:]:
         assert np.array_equal(runs[0].view(np.uint32), r.view(np.uint32))
