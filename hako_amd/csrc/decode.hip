@@ -55,6 +55,8 @@ int g_dec_gu_grid = 0;
 int g_dec_merge_rows = 0;
 // row items per wave of the q/k/v launch: 2, 4 or 8, 0 by shape
 int g_dec_qkv_items = 0;
+// attention parts per query-head group with one sequence: 1..8, 0 by shape
+int g_dec_attn_parts = 0;
 
 // One sequence's output projection adds its per-input-block row sums into a
 // residual accumulator of 64-bit fixed-point values (2^-32 units): integer
@@ -1445,6 +1447,7 @@ void dec_set_gu_items(int v) { g_dec_gu_items = (v == 4 || v == 8) ? v : 0; }
 void dec_set_gu_grid(int v) { g_dec_gu_grid = (v == 1 || v == 2) ? v : 0; }
 void dec_set_merge_rows(int v) { g_dec_merge_rows = (v == 64 || v == 128) ? v : 0; }
 void dec_set_qkv_items(int v) { g_dec_qkv_items = (v == 2 || v == 4 || v == 8) ? v : 0; }
+void dec_set_attn_parts(int v) { g_dec_attn_parts = v > 0 && v <= 8 ? v : 0; }
 
 }  // namespace hako
 
@@ -1602,9 +1605,12 @@ int attention(hako_gpu_decoder *d, int l, int8_t *mxq = nullptr, float *mxs = nu
 	float *kcl = d->kc + (size_t)l * d->max_seq * KV, *vcl = d->vc + (size_t)l * d->max_seq * KV;
 	// one sequence: a grid of chunks x KV heads leaves most CUs idle, so each
 	// group's query heads are split over (up to) four workgroups (3B decode at
-	// position 1024: 1374 / 1322 / 1304 / 1362 us per token for 1 / 2 / 4 / 8)
-	// (16 sequences: two parts per group made the 7B step 4% slower)
-	const int hsplit = d->n_seq == 1 ? (G < 4 ? G : 4) : 1;
+	// position 1024: 1374 / 1322 / 1304 / 1362 us per token for 1 / 2 / 4 / 8
+	// parts). Seven heads per group (7B) take two parts of 4 and 3 heads: four
+	// parts of 2, 2, 2, 1 measured 1554 against 1543 us per token, three 1562,
+	// seven 1568. (16 sequences: two parts per group made the 7B step 4% slower.)
+	const int parts = g_dec_attn_parts ? g_dec_attn_parts : (G == 7 ? 2 : 4);
+	const int hsplit = d->n_seq == 1 ? (G < parts ? G : parts) : 1;
 	const dim3 ag((d->max_chunks + 7) / 8 * 8 * hsplit, m.n_kv_heads, d->n_seq), mg(G, m.n_kv_heads, d->n_seq);
 	if (HD == 128) {
 		hipLaunchKernelGGL((attn_kernel<128, true>), ag, dim3(256), 0, stream(), d->qkv, d->rope, kcl, vcl, d->pos, d->part,

@@ -41,6 +41,7 @@ void dec_set_gu_items(int v);
 void dec_set_gu_grid(int v);
 void dec_set_merge_rows(int v);
 void dec_set_qkv_items(int v);
+void dec_set_attn_parts(int v);
 // Grow-only device workspace slot `slot` (0..7) of at least `bytes`.
 int workspace(int slot, size_t bytes, void **ptr);
 // Look up this device's address of the no-allocation scratch array (with

@@ -180,6 +180,7 @@ int hako_gpu_tune(int knob, int value) {
 	case HAKO_TUNE_DEC_GU_GRID: dec_set_gu_grid(value); return ok();
 	case HAKO_TUNE_DEC_MERGE_ROWS: dec_set_merge_rows(value); return ok();
 	case HAKO_TUNE_DEC_QKV_ITEMS: dec_set_qkv_items(value); return ok();
+	case HAKO_TUNE_DEC_ATTN_PARTS: dec_set_attn_parts(value); return ok();
 	default: return set_error(HAKO_GPU_EINVAL, "unknown tuning knob %d", knob);
 	}
 }

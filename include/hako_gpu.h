@@ -77,6 +77,7 @@ const char *hako_gpu_last_error(void);
 #define HAKO_TUNE_DEC_GU_GRID   16   /* one-sequence decoder gate/up launch: 1 = flat grid, 2 = persistent grid (one workgroup per CU, the rmsnorm prologue once per workgroup), 0 = by shape (default: persistent); read when a step is enqueued or captured */
 #define HAKO_TUNE_DEC_MERGE_ROWS 17  /* one-sequence decoder merge+o launch: rows per workgroup, 64 or 128, or 0 = by shape (default: 128 past d_model 2048); the same bits either way; read when a step is enqueued or captured */
 #define HAKO_TUNE_DEC_QKV_ITEMS  18  /* one-sequence decoder q/k/v launch: row items per wave, 2, 4 or 8, or 0 = by shape (default: 8 past d_model 2048, else 2); the same bits either way; read when a step is enqueued or captured */
+#define HAKO_TUNE_DEC_ATTN_PARTS 19  /* one-sequence decoder attention: workgroups that share a query-head group, 1..8, or 0 = by shape (default: 2 with 7 heads per group, else up to 4); the same bits either way; read when a step is enqueued or captured */
 int hako_gpu_tune(int knob, int value);
 
 typedef struct {

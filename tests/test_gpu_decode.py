@@ -329,8 +329,9 @@ def test_qwen2_7b_decode_at_position_1024(gpu, ref, tmp_path):
 def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
     """The gate/up launch's grid (flat with 4 or 8 row items per wave, or the
     persistent grid with its prologue once per workgroup), the merge+o
-    launch's rows per workgroup (64 or 128) and the q/k/v launch's row items
-    per wave (2, 4 or 8; all by shape by default) change
+    launch's rows per workgroup (64 or 128), the q/k/v launch's row items
+    per wave (2, 4 or 8) and the attention's workgroups per query-head group
+    (1, 2, 4 or 7; all by shape by default) change
     only which workgroup computes a row, never the order of a row's additions
     (the merge+o sums meet in an integer accumulator): three greedy steps give
     bit-identical logits either way."""
@@ -338,13 +339,15 @@ def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
     path = str(tmp_path / "gqa7.mlf2")
     mlf2.write_qwen2(path, cfg, 21)
     HAKO_TUNE_DEC_GU_ITEMS, HAKO_TUNE_DEC_GU_GRID, HAKO_TUNE_DEC_MERGE_ROWS, HAKO_TUNE_DEC_QKV_ITEMS = 9, 16, 17, 18
+    HAKO_TUNE_DEC_ATTN_PARTS = 19
     runs = []
     try:
-        for items, grid, mrows, qi in ((4, 1, 64, 2), (8, 1, 64, 4), (0, 2, 64, 8), (0, 2, 128, 2)):
+        for items, grid, mrows, qi, parts in ((4, 1, 64, 2, 4), (8, 1, 64, 4, 2), (0, 2, 64, 8, 7), (0, 2, 128, 2, 1)):
             gpu.tune(HAKO_TUNE_DEC_GU_ITEMS, items)
             gpu.tune(HAKO_TUNE_DEC_GU_GRID, grid)
             gpu.tune(HAKO_TUNE_DEC_MERGE_ROWS, mrows)
             gpu.tune(HAKO_TUNE_DEC_QKV_ITEMS, qi)
+            gpu.tune(HAKO_TUNE_DEC_ATTN_PARTS, parts)
             dec = make_decoder(gpu, path, max_seq=64)
             try:
                 tok, lg = 7, []
@@ -360,6 +363,7 @@ def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
         gpu.tune(HAKO_TUNE_DEC_GU_GRID, 0)
         gpu.tune(HAKO_TUNE_DEC_MERGE_ROWS, 0)
         gpu.tune(HAKO_TUNE_DEC_QKV_ITEMS, 0)
+        gpu.tune(HAKO_TUNE_DEC_ATTN_PARTS, 0)
     assert np.all(np.isfinite(runs[0]))
     for r in runs[1:]:
         assert np.array_equal(runs[0].view(np.uint32), r.view(np.uint32))
