@@ -326,7 +326,10 @@ def test_qwen2_7b_decode_at_position_1024(gpu, ref, tmp_path):
         within(f"7B logits, start {t}", g, w, 6e-5)
 
 
-def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
+# lane geometries: two rows per wave instruction (d_model 1792), four (1024,
+# head_dim 128) and eight (512, head_dim 64, untied output)
+@pytest.mark.parametrize("cfg", [GQA7, SMALL_128, TINY_UNTIED], ids=["gqa7", "small128", "tiny_untied"])
+def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path, cfg):
     """The gate/up launch's grid (flat with 4 or 8 row items per wave, or the
     persistent grid with its prologue once per workgroup), the merge+o
     launch's rows per workgroup (64 or 128), the q/k/v launch's row items
@@ -335,8 +338,7 @@ def test_gate_up_items_knob_gives_identical_steps(gpu, tmp_path):
     only which workgroup computes a row, never the order of a row's additions
     (the merge+o sums meet in an integer accumulator): three greedy steps give
     bit-identical logits either way."""
-    cfg = GQA7
-    path = str(tmp_path / "gqa7.mlf2")
+    path = str(tmp_path / "model.mlf2")
     mlf2.write_qwen2(path, cfg, 21)
     HAKO_TUNE_DEC_GU_ITEMS, HAKO_TUNE_DEC_GU_GRID, HAKO_TUNE_DEC_MERGE_ROWS, HAKO_TUNE_DEC_QKV_ITEMS = 9, 16, 17, 18
     HAKO_TUNE_DEC_ATTN_PARTS = 19
